@@ -1,0 +1,283 @@
+#!/usr/bin/env python3
+"""Benchmark of the Qwen3-0.6B Q4 decode hot path on one MI355X.
+
+Default workload (the headline line): one Qwen3-0.6B decoder layer, one
+decode step at context 512 (hidden 1024, 16 q / 8 kv heads, head_dim 128,
+intermediate 3072, Q4 random-init weights, fp16 KV cache pre-filled with
+N(0,1) for 512 positions).  A "step" is one such layer step.  Weights are
+rotated over ``--copies`` distinct layers (40 x 8.36 MB > the 256 MB
+Infinity Cache), so the headline is the cache-flushed rate; the
+cache-resident rate (one layer repeated) is reported beside it.
+
+``value`` = algorithmic HBM bytes per step (10,461,184 B: Q4 weights +
+scales, K/V read of 512 positions, new K/V row, hidden in/out) / step time.
+Steps run as HIP-graph replays of ``--copies`` captured layer steps.
+
+Also reported (same run): the 3072x1024 Q4 GEMV (config 1) GB/s flushed and
+resident, full 28-layer greedy decode tok/s (config 3: 64-token prompt, 256
+generated), the roofline of the dominant kernel (gate/up GEMV + SwiGLU)
+from HIP events, and the oracle's CPU rate on the host cores.
+"""
+
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import math
+import os
+import sys
+import time
+
+METRIC = "Q4 GEMV HBM GB/s (% peak) + batch-1 decode tok/s, Qwen3-0.6B-Q4"
+HBM_PEAK_GBPS = 8000.0
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=2000)
+    ap.add_argument("--warmup", type=int, default=200)
+    ap.add_argument("--ctx", type=int, default=512)
+    ap.add_argument("--copies", type=int, default=40)
+    ap.add_argument("--precision", type=int, default=2, choices=(1, 2))
+    ap.add_argument("--no-extras", action="store_true", help="skip the GEMV / full-decode / CPU legs")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--decode-gen", type=int, default=256)
+    return ap.parse_args()
+
+
+def graph_of(fn, n, torch):
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            for i in range(n):
+                fn(i)
+    torch.cuda.current_stream().wait_stream(s)
+    return g
+
+
+def time_graph(g, replays, torch):
+    """Average ms per replay over `replays`, HIP events on the current stream."""
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record()
+    for _ in range(replays):
+        g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / replays
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        sys.exit(f"bench.py measures one GPU only (got --gpus {args.gpus}); this build has no multi-GPU path")
+    import numpy as np
+    import torch
+
+    from llm_accelerator_amd import _lib
+    from llm_accelerator_amd import model as M
+    from llm_accelerator_amd._lib import check
+
+    lib = _lib.load()
+    check(lib.q4d_set_activation_precision(args.precision), "precision")
+    dev = torch.device("cuda:0")
+    st = lambda: torch.cuda.current_stream().cuda_stream  # noqa: E731
+
+    # ------------------------------------------------------------ C2 layer step
+    ctx, copies = args.ctx, args.copies
+    cfg = M.Qwen3Config(num_hidden_layers=copies, vocab_size=2048)
+    t = time.time()
+    host = M.random_host_weights(cfg, seed=0, num_layers=copies)
+    model = M.build_model(cfg, host, max_ctx=ctx + 1, device=dev)
+    del host
+    kv = M.KVCache(cfg, copies, 1, ctx + 1, dev)
+    gen = torch.Generator(device=dev).manual_seed(2)
+    kv.data.normal_(generator=gen)
+    ws = M.Workspace(model, 1)
+    pos = torch.tensor([ctx], dtype=torch.int32, device=dev)
+    h_in = torch.randn(1, 1024, generator=gen, device=dev, dtype=torch.float32)
+    h_out = torch.empty_like(h_in)
+    desc, kvd = model.descriptor(), kv.descriptor()
+    log(f"[bench] C2 setup {time.time() - t:.1f}s: {copies} layers, ctx {ctx}")
+
+    def layer_step(i):
+        check(lib.q4d_decoder_layer(ctypes.byref(desc), i % copies, h_in.data_ptr(), h_out.data_ptr(),
+                                    ctypes.byref(kvd), pos.data_ptr(), ws.ptr, ws.nbytes, st()),
+              "q4d_decoder_layer")
+
+    for i in range(args.warmup):
+        layer_step(i)
+    torch.cuda.synchronize()
+    g_flush = graph_of(layer_step, copies, torch)
+    g_flush.replay()
+    torch.cuda.synchronize()
+    full, rest = divmod(args.steps, copies)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(full):
+        g_flush.replay()
+    for i in range(rest):
+        layer_step(i)
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    ms_per_step = (t1 - t0) * 1e3 / args.steps
+    step_bytes = M.algorithmic_bytes_layer(M.Qwen3Config(), ctx)
+    value = step_bytes / (ms_per_step * 1e-3) / 1e9
+    log(f"[bench] C2 flushed: {ms_per_step * 1e3:.2f} us/step, {value:.1f} GB/s")
+
+    g_res = graph_of(lambda i: layer_step(0), copies, torch)
+    res_ms = time_graph(g_res, max(1, args.steps // copies), torch) / copies
+    resident = step_bytes / (res_ms * 1e-3) / 1e9
+    log(f"[bench] C2 resident: {res_ms * 1e3:.2f} us/step, {resident:.1f} GB/s")
+
+    # per-stage durations (graphs of `copies` launches of one stage, HIP events)
+    stage_names = ["qkv", "attention", "o_proj", "gate_up", "down"]
+    stage_us = {}
+    for sidx, sname in enumerate(stage_names):
+        def stage(i, sidx=sidx):
+            check(lib.q4d_layer_stage(ctypes.byref(desc), i % copies, sidx, h_in.data_ptr(), h_out.data_ptr(),
+                                      ctypes.byref(kvd), pos.data_ptr(), ws.ptr, ws.nbytes, st()),
+                  "q4d_layer_stage")
+        g = graph_of(stage, copies, torch)
+        g.replay()
+        stage_us[sname] = time_graph(g, max(1, args.steps // copies), torch) / copies * 1e3
+    log(f"[bench] stage us (flushed): {json.dumps({k: round(v, 2) for k, v in stage_us.items()})}")
+    h, i_sz = 1024, 3072
+    gate_up_bytes = 2 * (i_sz * h // 2 + 2 * i_sz * h // 64) + 2 * h + 2 * i_sz
+    achieved = gate_up_bytes / (stage_us["gate_up"] * 1e-6) / 1e9
+    roofline = {"bound": "hbm", "kernel": "gemv_kernel<1024,2,X_RMS,*,EP_SWIGLU,pair> (post-norm + gate/up + SwiGLU)",
+                "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None,
+                "bytes_per_launch": gate_up_bytes, "avg_launch_us": round(stage_us["gate_up"], 3)}
+
+    extras = {"c2_resident_GBps": round(resident, 1), "c2_resident_us_per_step": round(res_ms * 1e3, 3),
+              "c2_flushed_us_per_step": round(ms_per_step * 1e3, 3), "stage_us_flushed": stage_us}
+    del model, kv, ws, g_flush, g_res
+    torch.cuda.empty_cache()
+
+    if not args.no_extras:
+        # -------------------------------------------------------- C1 GEMV
+        from llm_accelerator_amd.model import Q4Tensor, gemv_bytes, random_q4
+        rng = np.random.default_rng(0)
+        packed, scale = random_q4(rng, 3072, 1024)
+        ncop = 200
+        P = torch.from_numpy(packed).to(dev).unsqueeze(0).repeat(ncop, 1, 1).contiguous()
+        S = torch.from_numpy(scale).to(dev).unsqueeze(0).repeat(ncop, 1, 1).contiguous()
+        mats = [Q4Tensor(P[i], S[i]).descriptor() for i in range(ncop)]
+        x = torch.randn(1, 1024, generator=gen, device=dev).half()
+        y = torch.empty(1, 3072, device=dev, dtype=torch.float16)
+
+        def gemv(i, fixed=False):
+            m = mats[0 if fixed else i]
+            check(lib.q4d_linear(ctypes.byref(m), x.data_ptr(), 0, y.data_ptr(), 0, 1, st()), "q4d_linear")
+        gb = gemv_bytes(3072, 1024)
+        g1 = graph_of(gemv, ncop, torch)
+        us_fl = time_graph(g1, 20, torch) / ncop * 1e3
+        g2 = graph_of(lambda i: gemv(i, True), ncop, torch)
+        us_res = time_graph(g2, 20, torch) / ncop * 1e3
+        extras["c1_gemv"] = {"shape": "3072x1024 q4, fp16 x/y", "bytes": gb,
+                             "flushed_us": round(us_fl, 3), "flushed_GBps": round(gb / us_fl / 1e3, 1),
+                             "resident_us": round(us_res, 3), "resident_GBps": round(gb / us_res / 1e3, 1)}
+        log(f"[bench] C1 GEMV: {json.dumps(extras['c1_gemv'])}")
+        del P, S, g1, g2
+        torch.cuda.empty_cache()
+
+        # -------------------------------------------------------- C3 decode tok/s
+        from llm_accelerator_amd.decode import GreedyDecoder
+        fcfg = M.Qwen3Config()
+        t = time.time()
+        fhost = M.random_host_weights(fcfg, seed=0)
+        fmodel = M.build_model(fcfg, fhost, max_ctx=64 + args.decode_gen + 16, device=dev)
+        del fhost
+        log(f"[bench] C3 setup {time.time() - t:.1f}s")
+        prompt = np.random.default_rng(1).integers(0, fcfg.vocab_size, 64).tolist()
+        dec = GreedyDecoder(fmodel, steps_per_graph=16, use_graph=True)
+        dec.prefill(prompt)
+        dec.generate(16)  # captures and warms the graph
+        torch.cuda.synchronize()
+        dec.prefill(prompt)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        dec.prefill(prompt)
+        torch.cuda.synchronize()
+        t_pre = time.perf_counter() - t0
+        t0 = time.perf_counter()
+        dec.generate(args.decode_gen - 1)
+        torch.cuda.synchronize()
+        t_gen = time.perf_counter() - t0
+        toks, _ = dec.history()
+        wb = fmodel.weight_bytes()
+        avg_ctx = 64 + args.decode_gen / 2
+        tok_bytes = wb["total"] + 2 * 2 * 1024 * avg_ctx * 28
+        tok_s = (args.decode_gen - 1) / t_gen
+        extras["c3_decode"] = {"prompt": 64, "generated": len(toks), "tok_s": round(tok_s, 1),
+                               "us_per_token": round(1e6 / tok_s, 2),
+                               "serial_prefill_tok_s": round(64 / t_pre, 1),
+                               "GBps_equiv": round(tok_bytes * tok_s / 1e9, 1),
+                               "hbm_frac": round(tok_bytes * tok_s / 1e9 / HBM_PEAK_GBPS, 4),
+                               "status": dec.status()}
+        log(f"[bench] C3 decode: {json.dumps(extras['c3_decode'])}")
+        del fmodel, dec
+        torch.cuda.empty_cache()
+
+    cpu = None
+    if not args.no_cpu and not args.no_extras:
+        cpu = cpu_baseline(args.cpu_seconds, ctx, step_bytes)
+        log(f"[bench] CPU baseline: {json.dumps(cpu)}")
+
+    line = {"metric": METRIC, "value": round(value, 2), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+            "warmup": args.warmup, "ms_per_step": round(ms_per_step, 6), "higher_is_better": True,
+            "scaling": "weak", "vs_baseline": None, "dtype": "q4xf32",
+            "data": "synthetic (seeded random-init Q4 weights, N(0,1) fp16 KV, N(0,1) hidden)",
+            "config": {"workload": "config 2: one Qwen3-0.6B decoder layer, one decode step at ctx 512, "
+                                   f"weights rotated over {copies} distinct layers (cache-flushed)",
+                       "hidden": 1024, "q_heads": 16, "kv_heads": 8, "head_dim": 128, "intermediate": 3072,
+                       "ctx": ctx, "batch": 1, "bytes_per_step": step_bytes, "activation_precision": args.precision},
+            "roofline": roofline, "cpu_baseline": cpu, "extras": extras}
+    print(json.dumps(line), flush=True)
+
+
+def cpu_baseline(seconds, ctx, step_bytes):
+    """The oracle's fp32 layer step (the reference's CPU path, common.py:231-298)
+    on a bounded sample of the same workload, timed on the host cores."""
+    import numpy as np
+
+    import oracle as o
+    from llm_accelerator_amd import model as M
+    try:
+        from threadpoolctl import threadpool_info
+        threads = max([p.get("num_threads", 1) for p in threadpool_info()] or [1])
+    except Exception:  # threadpoolctl missing: numpy default
+        threads = os.cpu_count() or 1
+    cfg = M.Qwen3Config(num_hidden_layers=1, vocab_size=2048)
+    host = M.random_host_weights(cfg, seed=0, num_layers=1)
+    om = o.OracleModel.from_q4(o.OracleConfig(num_hidden_layers=1, vocab_size=2048), host["layers"],
+                               *host["embed_tokens"], host["norm"])
+    rng = np.random.default_rng(2)
+    k = rng.normal(size=(1, 8, ctx, 128)).astype(np.float32)
+    v = rng.normal(size=(1, 8, ctx, 128)).astype(np.float32)
+    h = rng.normal(size=(1, 1, 1024)).astype(np.float32)
+    pos = np.array([[ctx]])
+    o.manual_decoder_layer_cached(h, om.layers[0], om.config, om.inv_freq, pos, k, v)
+    n, t0 = 0, time.perf_counter()
+    while time.perf_counter() - t0 < seconds:
+        o.manual_decoder_layer_cached(h, om.layers[0], om.config, om.inv_freq, pos, k, v)
+        n += 1
+    dt = (time.perf_counter() - t0) / n
+    return {"value": round(step_bytes / dt / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"{n} fp32 numpy layer steps at ctx {ctx} (oracle restatement of common.py:231-298), "
+                      f"{dt * 1e3:.2f} ms/step; os.cpu_count()={os.cpu_count()}, "
+                      f"affinity={len(os.sched_getaffinity(0))}"}
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,219 @@
+/*
+ * q4dec.h -- C ABI of the MI355X (gfx950) Qwen3-0.6B Q4 decode library
+ * (libq4dec.so).
+ *
+ * Conventions (all entry points):
+ *   - Every pointer is a device pointer owned by the caller, except the
+ *     q4d_model_t / q4d_layer_t / q4d_matrix_t / q4d_kv_cache_t descriptor
+ *     structs themselves, which live in host memory and are read on the host.
+ *   - `stream` is a hipStream_t passed as void* (NULL = the null stream).
+ *     Calls are stream-ordered and asynchronous: no allocation and no host
+ *     synchronisation happen inside.  Scratch memory is the caller's
+ *     workspace (q4d_workspace_bytes / q4d_workspace_init).
+ *   - Shapes, alignment, token ids and context lengths that the host can see
+ *     are validated before any launch; a failing call returns a negative
+ *     Q4D_ERR_* code and launches nothing (no memory traffic).  Values that
+ *     only exist on the device (token ids and positions fed back from an
+ *     earlier step) are range-checked by the kernels, which then skip the
+ *     out-of-range work and set the workspace status word (q4d_read_status).
+ *   - fp16 buffers are passed as uint16_t* (IEEE binary16 bit patterns).
+ *
+ * The Q4 weight format is the reference's (Source/Q4_FORMAT.md:75-140):
+ * row-major [rows, cols/2] uint8, two signed int4 per byte with the even
+ * column in the low nibble; uint16 Q2.14 scales [rows, cols/64].
+ *
+ * Reference interfaces replaced (paths in Tyler913/LLM_Accelerator):
+ *   q4d_linear           <- manual_linear_from_weight
+ *                           (Qwen3-0.6B-Base/python_each_module/common.py:137-145)
+ *                           and the integer Q4 GEMV contract (Source/Q4_FORMAT.md:155-190)
+ *   q4d_rms_norm         <- manual_rms_norm (common.py:129-134)
+ *   q4d_qk_norm_rope     <- manual_rms_norm over heads + manual_rope_cos_sin +
+ *                           manual_apply_rope (common.py:155-183, 258-268)
+ *   q4d_kv_append        <- append_cache (common.py:186-189) with the physical
+ *                           [layer][K/V][head][pos][dim] order of
+ *                           23_export_kv_cache_append_vectors.py:64-84
+ *   q4d_cached_attention <- manual_repeat_kv + manual_cached_attention
+ *                           (common.py:192-228)
+ *   q4d_embedding        <- embedding_table[token]
+ *                           (10_validate_full_run_one_token.py:31)
+ *   q4d_lm_head_argmax   <- final manual_rms_norm + LM head + argmax
+ *                           (10_validate_full_run_one_token.py:52-56) with the
+ *                           lowest-index tie rule of
+ *                           56_export_persistent_multitoken_layer_golden.py:860
+ *   q4d_decoder_layer    <- manual_decoder_layer_cached (common.py:231-298)
+ *   q4d_run_one_token    <- run_manual_one_token
+ *                           (10_validate_full_run_one_token.py:17-56) and the
+ *                           hardware step qot_run_token
+ *                           (FPGA_Project/software/qmap_one_token_runtime/
+ *                            qmap_one_token_runtime.h:368-392)
+ *   Q4D_ERR_*            <- QOT_ERR_* (qmap_one_token_runtime.h:17-29)
+ */
+#ifndef Q4DEC_H
+#define Q4DEC_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes; 0..-10 keep the meaning of QOT_ERR_* (qmap_one_token_runtime.h:17-29). */
+enum {
+  Q4D_OK = 0,
+  Q4D_ERR_BUSY = -1,
+  Q4D_ERR_BAD_LAYER = -2,
+  Q4D_ERR_BAD_TABLE = -3,    /* bad model/weight descriptor */
+  Q4D_ERR_BAD_ADDR = -4,     /* misaligned pointer */
+  Q4D_ERR_TIMEOUT = -5,
+  Q4D_ERR_STATUS = -6,       /* device-side status word reported an error */
+  Q4D_ERR_NULL = -7,
+  Q4D_ERR_BAD_TOKEN = -8,
+  Q4D_ERR_CAPACITY = -9,     /* workspace too small / batch too large */
+  Q4D_ERR_CONTEXT = -10,     /* position outside [0, max_ctx) */
+  Q4D_ERR_SHAPE = -11,       /* unsupported or inconsistent shape */
+  Q4D_ERR_LAUNCH = -12,      /* HIP launch error */
+  Q4D_ERR_DTYPE = -13
+};
+
+/* Device status word bits (q4d_read_status). */
+enum {
+  Q4D_STATUS_BAD_TOKEN = 1,
+  Q4D_STATUS_BAD_POSITION = 2
+};
+
+enum { Q4D_F16 = 0, Q4D_F32 = 1 };
+
+typedef struct q4d_matrix {
+  const uint8_t* w;   /* [rows, cols/2] packed int4 */
+  const uint16_t* s;  /* [rows, cols/64] Q2.14 */
+  int32_t rows;
+  int32_t cols;
+} q4d_matrix_t;
+
+/* Attribute names follow the HF layer object read by common.py:245-296. */
+typedef struct q4d_layer {
+  q4d_matrix_t q_proj, k_proj, v_proj, o_proj, gate_proj, up_proj, down_proj;
+  const float* input_layernorm;           /* [hidden] */
+  const float* post_attention_layernorm;  /* [hidden] */
+  const float* q_norm;                    /* [head_dim] */
+  const float* k_norm;                    /* [head_dim] */
+} q4d_layer_t;
+
+typedef struct q4d_model {
+  int32_t hidden_size;        /* 1024 */
+  int32_t intermediate_size;  /* 3072 */
+  int32_t num_layers;         /* 28 */
+  int32_t num_q_heads;        /* 16 */
+  int32_t num_kv_heads;       /* 8 */
+  int32_t head_dim;           /* 128 */
+  int32_t vocab_size;         /* 151936 */
+  int32_t max_ctx;            /* rows of the RoPE tables and KV capacity */
+  float rms_norm_eps;         /* 1e-6 */
+  float attn_scaling;         /* head_dim ** -0.5 */
+  const q4d_layer_t* layers;  /* host array [num_layers] */
+  q4d_matrix_t embed_tokens;  /* tied embedding / LM head [vocab, hidden] */
+  const float* final_norm;    /* [hidden] */
+  const float* rope_cos;      /* [max_ctx, head_dim/2] fp32, cos(pos * inv_freq) */
+  const float* rope_sin;      /* [max_ctx, head_dim/2] fp32 */
+} q4d_model_t;
+
+/* fp16 KV cache, [num_layers][2 (K,V)][batch][num_kv_heads][max_ctx][head_dim]. */
+typedef struct q4d_kv_cache {
+  uint16_t* data;
+  int32_t num_layers;
+  int32_t batch;
+  int32_t num_kv_heads;
+  int32_t max_ctx;
+  int32_t head_dim;
+} q4d_kv_cache_t;
+
+/* ---- library / workspace ------------------------------------------------ */
+int q4d_version(void);
+const char* q4d_status_string(int code);
+/* Bytes of workspace needed by the fused entry points for `batch` sequences. */
+size_t q4d_workspace_bytes(const q4d_model_t* model, int32_t batch);
+/* Zero the workspace counters and status word (call once after allocation). */
+int q4d_workspace_init(void* ws, size_t ws_bytes, const q4d_model_t* model, int32_t batch, void* stream);
+/* Precision of fp32 activations inside the GEMVs: 2 (default) = each value
+ * enters as an fp16 hi + fp16 lo pair (~22 significant bits); 1 = rounded to
+ * fp16.  Process-wide; set it before launching work. */
+int q4d_set_activation_precision(int32_t mode);
+/* Copy the device status word into *out (synchronises `stream`). */
+int q4d_read_status(const void* ws, size_t ws_bytes, const q4d_model_t* model, int32_t batch,
+                    int32_t* out, void* stream);
+
+/* ---- primitive ops ------------------------------------------------------- */
+/* y[m, :] = W x[m, :] for m < batch.  x: [batch, cols] (x_dtype), y: [batch, rows] (y_dtype).
+ * Supported cols: 1024, 2048, 3072; rows even. */
+int q4d_linear(const q4d_matrix_t* w, const void* x, int32_t x_dtype, void* y, int32_t y_dtype,
+               int32_t batch, void* stream);
+/* y = x * rsqrt(mean(x^2) + eps) * gamma over the last dim (fp32 in). */
+int q4d_rms_norm(const float* x, const float* gamma, float eps, int32_t rows, int32_t dim,
+                 void* y, int32_t y_dtype, void* stream);
+/* Per-head RMSNorm with gamma, then rotate-half RoPE at positions[b].
+ * x: fp32 [batch, heads, head_dim] (in place allowed); positions: device int32 [batch]. */
+int q4d_qk_norm_rope(const float* x, float* y, const float* gamma, float eps, int32_t batch,
+                     int32_t heads, int32_t head_dim, const float* rope_cos, const float* rope_sin,
+                     int32_t max_ctx, const int32_t* positions, int32_t* status, void* stream);
+/* RoPE only: y[b,h,:] = x*cos[b] + rotate_half(x)*sin[b] (common.py:148-152,173-183).
+ * x, y: fp32 [batch, heads, head_dim]; cos, sin: fp32 [batch, head_dim] (full width). */
+int q4d_apply_rope(const float* x, float* y, const float* cos, const float* sin, int32_t batch,
+                   int32_t heads, int32_t head_dim, void* stream);
+/* Write k, v (fp32 [batch, kv_heads, head_dim]) into layer `layer` of the cache at positions[b];
+ * either of k / v may be NULL to leave that plane untouched. */
+int q4d_kv_append(const q4d_kv_cache_t* kv, int32_t layer, const float* k, const float* v,
+                  const int32_t* positions, int32_t* status, void* stream);
+/* GQA decode attention over cache positions [0, positions[b]] of `layer`.
+ * q: fp32 [batch, q_heads, head_dim] already normed/roped; out: fp16 [batch, q_heads*head_dim]. */
+int q4d_cached_attention(const q4d_model_t* model, const q4d_kv_cache_t* kv, int32_t layer,
+                         const float* q, const int32_t* positions, void* out, int32_t out_dtype,
+                         void* ws, size_t ws_bytes, void* stream);
+/* hidden[b, :] = dequant(embed_tokens[tokens[b], :]) (fp32). */
+int q4d_embedding(const q4d_matrix_t* table, const int32_t* tokens, int32_t batch, float* hidden,
+                  int32_t* status, void* stream);
+/* Final RMSNorm + tied LM head + argmax (lowest index wins ties).
+ * hidden: fp32 [1, hidden]; out_token int32 [1]; out_score fp32 [1] (the winning logit);
+ * logits: optional fp32 [vocab] (NULL to skip). */
+int q4d_lm_head_argmax(const q4d_model_t* model, const float* hidden, int32_t* out_token,
+                       float* out_score, float* logits, void* ws, size_t ws_bytes, void* stream);
+
+/* ---- fused decode ---------------------------------------------------------- */
+/* One cached decoder layer (batch 1): hidden_out = layer(hidden_in); appends
+ * K/V at positions[0] of the cache.  hidden_in and hidden_out may alias. */
+int q4d_decoder_layer(const q4d_model_t* model, int32_t layer, const float* hidden_in,
+                      float* hidden_out, const q4d_kv_cache_t* kv, const int32_t* positions,
+                      void* ws, size_t ws_bytes, void* stream);
+/* One stage of a decoder layer (batch 1), in the order q4d_decoder_layer runs them.  The
+ * stages follow the per-layer QMAP stage boundaries of the hardware path
+ * (qot_layer_qmap_bases_t, qmap_one_token_runtime.h:31-42):
+ *   Q4D_STAGE_QKV       input RMSNorm + q|k|v projection      -> workspace qkv
+ *   Q4D_STAGE_ATTENTION q/k RMSNorm + RoPE + KV append + GQA attention -> workspace attn
+ *   Q4D_STAGE_O_PROJ    o_proj + residual: hidden_out = hidden_in + W_o attn
+ *   Q4D_STAGE_GATE_UP   post-attention RMSNorm(hidden_out) + gate/up + SiLU*up -> workspace act
+ *   Q4D_STAGE_DOWN      down_proj + residual: hidden_out += W_d act
+ * Running the five stages in order equals one q4d_decoder_layer call. */
+enum { Q4D_STAGE_QKV = 0, Q4D_STAGE_ATTENTION = 1, Q4D_STAGE_O_PROJ = 2, Q4D_STAGE_GATE_UP = 3,
+       Q4D_STAGE_DOWN = 4 };
+int q4d_layer_stage(const q4d_model_t* model, int32_t layer, int32_t stage, const float* hidden_in,
+                    float* hidden_out, const q4d_kv_cache_t* kv, const int32_t* positions, void* ws,
+                    size_t ws_bytes, void* stream);
+/* Embedding -> all layers -> final norm -> LM head argmax for tokens[0] at
+ * positions[0] (batch 1).  Writes next_token[0] and score[0]; logits optional. */
+int q4d_run_one_token(const q4d_model_t* model, const int32_t* tokens, const int32_t* positions,
+                      const q4d_kv_cache_t* kv, int32_t* next_token, float* score, float* logits,
+                      void* ws, size_t ws_bytes, void* stream);
+/* Advance a device-resident decode loop: tokens[0] = next_token[0], positions[0] += 1, and,
+ * if hist_tokens is not NULL and *hist_count < hist_capacity, record next_token[0] and score[0]
+ * at index *hist_count and increment it.  Lets a captured graph replay q4d_run_one_token
+ * without host round trips (the device form of qot_decode_token_ids,
+ * qmap_one_token_runtime.h:399+). */
+int q4d_advance(int32_t* tokens, int32_t* positions, const int32_t* next_token, const float* score,
+                int32_t* hist_tokens, float* hist_scores, int32_t* hist_count, int32_t hist_capacity,
+                void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* Q4DEC_H */

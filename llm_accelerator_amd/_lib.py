@@ -1,0 +1,114 @@
+"""ctypes binding of libq4dec.so (declared in include/q4dec.h).
+
+The library is built in-tree by ``llm_accelerator_amd.build``.  There is no
+fallback: if the shared object is missing or a symbol is absent, loading
+raises immediately.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from ctypes import POINTER, c_float, c_int32, c_size_t, c_void_p
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().with_name("libq4dec.so")
+
+Q4D_F16 = 0
+Q4D_F32 = 1
+STATUS_BAD_TOKEN = 1
+STATUS_BAD_POSITION = 2
+
+# Status codes (include/q4dec.h); 0..-10 mirror QOT_ERR_* of
+# FPGA_Project/software/qmap_one_token_runtime/qmap_one_token_runtime.h:17-29.
+ERRORS = {
+    -1: "BUSY", -2: "BAD_LAYER", -3: "BAD_TABLE", -4: "BAD_ADDR", -5: "TIMEOUT", -6: "STATUS",
+    -7: "NULL", -8: "BAD_TOKEN", -9: "CAPACITY", -10: "CONTEXT", -11: "SHAPE", -12: "LAUNCH",
+    -13: "DTYPE",
+}
+
+
+class Q4DecError(RuntimeError):
+    """A libq4dec entry point returned a negative status code."""
+
+    def __init__(self, code: int, what: str):
+        self.code = code
+        name = ERRORS.get(code, "UNKNOWN")
+        super().__init__(f"{what} failed: Q4D_ERR_{name} ({code})")
+
+
+class Q4dMatrix(ctypes.Structure):
+    _fields_ = [("w", c_void_p), ("s", c_void_p), ("rows", c_int32), ("cols", c_int32)]
+
+
+class Q4dLayer(ctypes.Structure):
+    _fields_ = [(n, Q4dMatrix) for n in ("q_proj", "k_proj", "v_proj", "o_proj", "gate_proj", "up_proj",
+                                         "down_proj")] + [
+        ("input_layernorm", c_void_p), ("post_attention_layernorm", c_void_p),
+        ("q_norm", c_void_p), ("k_norm", c_void_p)]
+
+
+class Q4dModel(ctypes.Structure):
+    _fields_ = [
+        ("hidden_size", c_int32), ("intermediate_size", c_int32), ("num_layers", c_int32),
+        ("num_q_heads", c_int32), ("num_kv_heads", c_int32), ("head_dim", c_int32),
+        ("vocab_size", c_int32), ("max_ctx", c_int32), ("rms_norm_eps", c_float), ("attn_scaling", c_float),
+        ("layers", POINTER(Q4dLayer)), ("embed_tokens", Q4dMatrix), ("final_norm", c_void_p),
+        ("rope_cos", c_void_p), ("rope_sin", c_void_p),
+    ]
+
+
+class Q4dKVCache(ctypes.Structure):
+    _fields_ = [("data", c_void_p), ("num_layers", c_int32), ("batch", c_int32), ("num_kv_heads", c_int32),
+                ("max_ctx", c_int32), ("head_dim", c_int32)]
+
+
+_P = c_void_p
+SIGNATURES = {
+    "q4d_version": ([], c_int32),
+    "q4d_status_string": ([c_int32], ctypes.c_char_p),
+    "q4d_workspace_bytes": ([POINTER(Q4dModel), c_int32], c_size_t),
+    "q4d_workspace_init": ([_P, c_size_t, POINTER(Q4dModel), c_int32, _P], c_int32),
+    "q4d_set_activation_precision": ([c_int32], c_int32),
+    "q4d_read_status": ([_P, c_size_t, POINTER(Q4dModel), c_int32, POINTER(c_int32), _P], c_int32),
+    "q4d_linear": ([POINTER(Q4dMatrix), _P, c_int32, _P, c_int32, c_int32, _P], c_int32),
+    "q4d_rms_norm": ([_P, _P, c_float, c_int32, c_int32, _P, c_int32, _P], c_int32),
+    "q4d_qk_norm_rope": ([_P, _P, _P, c_float, c_int32, c_int32, c_int32, _P, _P, c_int32, _P, _P, _P], c_int32),
+    "q4d_kv_append": ([POINTER(Q4dKVCache), c_int32, _P, _P, _P, _P, _P], c_int32),
+    "q4d_cached_attention": ([POINTER(Q4dModel), POINTER(Q4dKVCache), c_int32, _P, _P, _P, c_int32, _P,
+                              c_size_t, _P], c_int32),
+    "q4d_embedding": ([POINTER(Q4dMatrix), _P, c_int32, _P, _P, _P], c_int32),
+    "q4d_lm_head_argmax": ([POINTER(Q4dModel), _P, _P, _P, _P, _P, c_size_t, _P], c_int32),
+    "q4d_decoder_layer": ([POINTER(Q4dModel), c_int32, _P, _P, POINTER(Q4dKVCache), _P, _P, c_size_t, _P],
+                          c_int32),
+    "q4d_layer_stage": ([POINTER(Q4dModel), c_int32, c_int32, _P, _P, POINTER(Q4dKVCache), _P, _P, c_size_t, _P],
+                        c_int32),
+    "q4d_run_one_token": ([POINTER(Q4dModel), _P, _P, POINTER(Q4dKVCache), _P, _P, _P, _P, c_size_t, _P],
+                          c_int32),
+    "q4d_apply_rope": ([_P, _P, _P, _P, c_int32, c_int32, c_int32, _P], c_int32),
+    "q4d_advance": ([_P, _P, _P, _P, _P, _P, _P, c_int32, _P], c_int32),
+}
+
+_lib = None
+
+
+def load(path: Path | str | None = None) -> ctypes.CDLL:
+    """Load libq4dec.so once; raise if it (or any declared symbol) is missing."""
+    global _lib
+    if _lib is not None and path is None:
+        return _lib
+    p = Path(path) if path is not None else LIB_PATH
+    if not p.exists():
+        raise ImportError(f"{p} is not built; run `python -m llm_accelerator_amd.build` (no CPU fallback exists)")
+    lib = ctypes.CDLL(str(p))
+    for name, (args, res) in SIGNATURES.items():
+        fn = getattr(lib, name)  # AttributeError if the symbol is absent
+        fn.argtypes = args
+        fn.restype = res
+    if path is None:
+        _lib = lib
+    return lib
+
+
+def check(rc: int, what: str) -> None:
+    if rc != 0:
+        raise Q4DecError(rc, what)

@@ -1,0 +1,410 @@
+// extern "C" entry points of libq4dec.so: host-side validation, then
+// stream-ordered launches.  See include/q4dec.h for the contract.
+#include <string.h>
+
+#include "q4d_internal.h"
+
+namespace q4d {
+int launch_gemv_xp(const GemvArgs& a, int xm, int xp, int ep, bool pair, hipStream_t st);
+}
+
+using namespace q4d;
+
+namespace {
+
+// Activation precision inside the fused decode: 2 = fp32 activations enter
+// each GEMV as hi+lo fp16 halves (about 22 significant bits), 1 = rounded to fp16.
+int g_act_precision = 2;
+
+inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+int check_matrix(const q4d_matrix_t* m, int rows, int cols) {
+  if (!m || !m->w || !m->s) return Q4D_ERR_NULL;
+  if (m->rows != rows || m->cols != cols) return Q4D_ERR_BAD_TABLE;
+  if (!aligned(m->w, 16) || !aligned(m->s, 2)) return Q4D_ERR_BAD_ADDR;
+  return Q4D_OK;
+}
+
+int check_model(const q4d_model_t* m) {
+  if (!m || !m->layers || !m->final_norm || !m->rope_cos || !m->rope_sin) return Q4D_ERR_NULL;
+  if (m->hidden_size != 1024 || m->head_dim != 128 || m->num_kv_heads <= 0 ||
+      m->num_q_heads != 2 * m->num_kv_heads)
+    return Q4D_ERR_SHAPE;
+  const int qd = m->num_q_heads * m->head_dim, kd = m->num_kv_heads * m->head_dim;
+  if (qd != 1024 && qd != 2048 && qd != 3072) return Q4D_ERR_SHAPE;
+  const int I = m->intermediate_size;
+  if (I != 1024 && I != 2048 && I != 3072) return Q4D_ERR_SHAPE;
+  if (m->num_layers <= 0 || m->max_ctx <= 0 || m->vocab_size <= 0 || (m->vocab_size & 1)) return Q4D_ERR_SHAPE;
+  if (kd % 2) return Q4D_ERR_SHAPE;
+  int rc;
+  if ((rc = check_matrix(&m->embed_tokens, m->vocab_size, m->hidden_size))) return rc;
+  for (int l = 0; l < m->num_layers; ++l) {
+    const q4d_layer_t& L = m->layers[l];
+    if ((rc = check_matrix(&L.q_proj, qd, 1024)) || (rc = check_matrix(&L.k_proj, kd, 1024)) ||
+        (rc = check_matrix(&L.v_proj, kd, 1024)) || (rc = check_matrix(&L.o_proj, 1024, qd)) ||
+        (rc = check_matrix(&L.gate_proj, I, 1024)) || (rc = check_matrix(&L.up_proj, I, 1024)) ||
+        (rc = check_matrix(&L.down_proj, 1024, I)))
+      return rc == Q4D_ERR_BAD_TABLE ? Q4D_ERR_BAD_LAYER : rc;
+    if (!L.input_layernorm || !L.post_attention_layernorm || !L.q_norm || !L.k_norm) return Q4D_ERR_NULL;
+    if (!aligned(L.input_layernorm, 16) || !aligned(L.post_attention_layernorm, 16)) return Q4D_ERR_BAD_ADDR;
+  }
+  if (!aligned(m->final_norm, 16)) return Q4D_ERR_BAD_ADDR;
+  return Q4D_OK;
+}
+
+int check_kv(const q4d_kv_cache_t* kv, const q4d_model_t* m, int batch) {
+  if (!kv || !kv->data) return Q4D_ERR_NULL;
+  if (kv->num_layers != m->num_layers || kv->num_kv_heads != m->num_kv_heads || kv->head_dim != m->head_dim ||
+      kv->max_ctx != m->max_ctx)
+    return Q4D_ERR_SHAPE;
+  if (kv->batch < batch || batch <= 0) return Q4D_ERR_CAPACITY;
+  if (!aligned(kv->data, 16)) return Q4D_ERR_BAD_ADDR;
+  return Q4D_OK;
+}
+
+int check_ws(const void* ws, size_t bytes, const q4d_model_t* m, int batch) {
+  if (!ws) return Q4D_ERR_NULL;
+  if (!aligned(ws, 256)) return Q4D_ERR_BAD_ADDR;
+  if (bytes < ws_layout(m, batch).total) return Q4D_ERR_CAPACITY;
+  return Q4D_OK;
+}
+
+void kv_planes(const q4d_kv_cache_t* kv, int layer, uint16_t** kp, uint16_t** vp) {
+  const size_t plane = (size_t)kv->batch * kv->num_kv_heads * kv->max_ctx * kv->head_dim;
+  *kp = kv->data + (size_t)layer * 2 * plane;
+  *vp = *kp + plane;
+}
+
+GemvArgs one_matrix(const q4d_matrix_t* w, int batch) {
+  GemvArgs a;
+  memset(&a, 0, sizeof(a));
+  a.w[0] = w->w;
+  a.s[0] = w->s;
+  a.seg_end[0] = w->rows;
+  a.nseg = 1;
+  a.rows = w->rows;
+  a.cols = w->cols;
+  a.batch = batch;
+  return a;
+}
+
+// One decoder layer, batch 1 (common.py:231-298), five launches; `only`
+// selects a single stage (Q4D_STAGE_*) or -1 for all.
+int run_layer(const q4d_model_t* m, int l, const float* hin, float* hout, const q4d_kv_cache_t* kv,
+              const int32_t* positions, void* ws, const WsLayout& W, hipStream_t st, int only = -1) {
+  const q4d_layer_t& L = m->layers[l];
+  const int xp = g_act_precision;
+  float* qkv = ws_ptr<float>(ws, W.qkv);
+  float* attn = ws_ptr<float>(ws, W.attn);
+  float* act = ws_ptr<float>(ws, W.act);
+  int rc;
+
+  // 1. input RMSNorm fused into the q|k|v projection
+  GemvArgs a;
+  memset(&a, 0, sizeof(a));
+  a.w[0] = L.q_proj.w; a.s[0] = L.q_proj.s;
+  a.w[1] = L.k_proj.w; a.s[1] = L.k_proj.s;
+  a.w[2] = L.v_proj.w; a.s[2] = L.v_proj.s;
+  a.seg_end[0] = L.q_proj.rows;
+  a.seg_end[1] = a.seg_end[0] + L.k_proj.rows;
+  a.seg_end[2] = a.seg_end[1] + L.v_proj.rows;
+  a.nseg = 3;
+  a.rows = a.seg_end[2];
+  a.cols = 1024;
+  a.x = hin;
+  a.gamma = L.input_layernorm;
+  a.eps = m->rms_norm_eps;
+  a.y = qkv;
+  a.batch = 1;
+  if ((only < 0 || only == Q4D_STAGE_QKV) && (rc = launch_gemv_xp(a, X_RMS, xp, EP_F32, false, st))) return rc;
+
+  // 2. q/k norm + RoPE + KV append + attention + split merge
+  AttnArgs t;
+  memset(&t, 0, sizeof(t));
+  t.fused = 1;
+  t.qkv = qkv;
+  t.q_gamma = L.q_norm;
+  t.k_gamma = L.k_norm;
+  t.eps = m->rms_norm_eps;
+  t.scaling = m->attn_scaling;
+  t.rope_cos = m->rope_cos;
+  t.rope_sin = m->rope_sin;
+  kv_planes(kv, l, &t.kcache, &t.vcache);
+  t.positions = positions;
+  t.batch = 1;
+  t.qh = m->num_q_heads;
+  t.kvh = m->num_kv_heads;
+  t.d = m->head_dim;
+  t.max_ctx = m->max_ctx;
+  t.nsplit_max = W.nsplit_max;
+  t.part_ml = ws_ptr<float>(ws, W.part_ml);
+  t.part_acc = ws_ptr<float>(ws, W.part_acc);
+  t.counters = ws_ptr<int>(ws, W.counters);
+  t.out = attn;
+  t.out_dtype = Q4D_F32;
+  t.status = ws_ptr<int32_t>(ws, W.status);
+  if ((only < 0 || only == Q4D_STAGE_ATTENTION) && (rc = launch_attention(t, st))) return rc;
+
+  // 3. o_proj + residual
+  a = one_matrix(&L.o_proj, 1);
+  a.x = attn;
+  a.y = hout;
+  a.resid = hin;
+  if ((only < 0 || only == Q4D_STAGE_O_PROJ) && (rc = launch_gemv_xp(a, X_F32, xp, EP_RESID, false, st)))
+    return rc;
+
+  // 4. post-attention RMSNorm + gate/up + SwiGLU
+  memset(&a, 0, sizeof(a));
+  a.w[0] = L.gate_proj.w; a.s[0] = L.gate_proj.s;
+  a.w[1] = L.up_proj.w;   a.s[1] = L.up_proj.s;
+  a.seg_end[0] = L.gate_proj.rows;
+  a.seg_end[1] = 2 * L.gate_proj.rows;
+  a.nseg = 2;
+  a.rows = L.gate_proj.rows;
+  a.cols = 1024;
+  a.x = hout;
+  a.gamma = L.post_attention_layernorm;
+  a.eps = m->rms_norm_eps;
+  a.y = act;
+  a.batch = 1;
+  if ((only < 0 || only == Q4D_STAGE_GATE_UP) && (rc = launch_gemv_xp(a, X_RMS, xp, EP_SWIGLU, true, st)))
+    return rc;
+
+  // 5. down_proj + residual (in place on hout)
+  a = one_matrix(&L.down_proj, 1);
+  a.x = act;
+  a.y = hout;
+  a.resid = hout;
+  if (only < 0 || only == Q4D_STAGE_DOWN) return launch_gemv_xp(a, X_F32, xp, EP_RESID, false, st);
+  return Q4D_OK;
+}
+
+int run_lm_head(const q4d_model_t* m, const float* hidden, int32_t* tok, float* score, float* logits,
+                void* ws, const WsLayout& W, hipStream_t st) {
+  GemvArgs a = one_matrix(&m->embed_tokens, 1);
+  a.x = hidden;
+  a.gamma = m->final_norm;
+  a.eps = m->rms_norm_eps;
+  a.logits = logits;
+  a.lm_part = ws_ptr<void>(ws, W.lm_part);
+  a.counter = ws_ptr<int>(ws, W.counters) + W.lm_counter_index;
+  a.out_token = tok;
+  a.out_score = score;
+  return launch_gemv_xp(a, X_RMS, g_act_precision, EP_ARGMAX, false, st);
+}
+
+}  // namespace
+
+extern "C" {
+
+int q4d_version(void) { return 1; }
+
+const char* q4d_status_string(int code) {
+  switch (code) {
+    case Q4D_OK: return "ok";
+    case Q4D_ERR_BUSY: return "busy";
+    case Q4D_ERR_BAD_LAYER: return "bad layer descriptor";
+    case Q4D_ERR_BAD_TABLE: return "bad weight descriptor";
+    case Q4D_ERR_BAD_ADDR: return "misaligned pointer";
+    case Q4D_ERR_TIMEOUT: return "timeout";
+    case Q4D_ERR_STATUS: return "device status error";
+    case Q4D_ERR_NULL: return "null pointer";
+    case Q4D_ERR_BAD_TOKEN: return "token id outside the vocabulary";
+    case Q4D_ERR_CAPACITY: return "workspace or cache capacity exceeded";
+    case Q4D_ERR_CONTEXT: return "position outside the context";
+    case Q4D_ERR_SHAPE: return "unsupported shape";
+    case Q4D_ERR_LAUNCH: return "kernel launch failed";
+    case Q4D_ERR_DTYPE: return "unsupported dtype";
+    default: return "unknown status";
+  }
+}
+
+int q4d_set_activation_precision(int32_t mode) {
+  if (mode != 1 && mode != 2) return Q4D_ERR_DTYPE;
+  g_act_precision = mode;
+  return Q4D_OK;
+}
+
+size_t q4d_workspace_bytes(const q4d_model_t* model, int32_t batch) {
+  if (!model || batch <= 0) return 0;
+  return ws_layout(model, batch).total;
+}
+
+int q4d_workspace_init(void* ws, size_t ws_bytes, const q4d_model_t* model, int32_t batch, void* stream) {
+  if (!model) return Q4D_ERR_NULL;
+  int rc = check_ws(ws, ws_bytes, model, batch);
+  if (rc) return rc;
+  const WsLayout W = ws_layout(model, batch);
+  // status block and counters are contiguous at the start of the workspace
+  return launch_fill_i32(ws_ptr<int32_t>(ws, 0), 0, W.hidden / 4, as_stream(stream));
+}
+
+int q4d_read_status(const void* ws, size_t ws_bytes, const q4d_model_t* model, int32_t batch, int32_t* out,
+                    void* stream) {
+  if (!model || !out) return Q4D_ERR_NULL;
+  int rc = check_ws(ws, ws_bytes, model, batch);
+  if (rc) return rc;
+  const WsLayout W = ws_layout(model, batch);
+  if (hipMemcpyAsync(out, static_cast<const char*>(ws) + W.status, 4, hipMemcpyDeviceToHost,
+                     as_stream(stream)) != hipSuccess)
+    return Q4D_ERR_LAUNCH;
+  return hipStreamSynchronize(as_stream(stream)) == hipSuccess ? Q4D_OK : Q4D_ERR_LAUNCH;
+}
+
+int q4d_linear(const q4d_matrix_t* w, const void* x, int32_t x_dtype, void* y, int32_t y_dtype, int32_t batch,
+               void* stream) {
+  if (!w) return Q4D_ERR_NULL;
+  int rc = check_matrix(w, w->rows, w->cols);
+  if (rc) return rc;
+  if (x_dtype != Q4D_F16 && x_dtype != Q4D_F32) return Q4D_ERR_DTYPE;
+  if (y_dtype != Q4D_F16 && y_dtype != Q4D_F32) return Q4D_ERR_DTYPE;
+  if (batch <= 0) return Q4D_ERR_SHAPE;
+  GemvArgs a = one_matrix(w, batch);
+  a.x = x;
+  a.y = y;
+  return launch_gemv_xp(a, x_dtype == Q4D_F16 ? X_F16 : X_F32, x_dtype == Q4D_F16 ? 1 : g_act_precision,
+                        y_dtype == Q4D_F16 ? EP_F16 : EP_F32, false, as_stream(stream));
+}
+
+int q4d_rms_norm(const float* x, const float* gamma, float eps, int32_t rows, int32_t dim, void* y,
+                 int32_t y_dtype, void* stream) {
+  if (!x || !gamma || !y) return Q4D_ERR_NULL;
+  if (rows <= 0 || dim <= 0) return Q4D_ERR_SHAPE;
+  if (y_dtype != Q4D_F16 && y_dtype != Q4D_F32) return Q4D_ERR_DTYPE;
+  return launch_rms_norm(x, gamma, eps, rows, dim, y, y_dtype, as_stream(stream));
+}
+
+int q4d_qk_norm_rope(const float* x, float* y, const float* gamma, float eps, int32_t batch, int32_t heads,
+                     int32_t head_dim, const float* rope_cos, const float* rope_sin, int32_t max_ctx,
+                     const int32_t* positions, int32_t* status, void* stream) {
+  if (!x || !y || !gamma || !rope_cos || !rope_sin || !positions || !status) return Q4D_ERR_NULL;
+  if (batch <= 0 || heads <= 0 || max_ctx <= 0) return Q4D_ERR_SHAPE;
+  return launch_qk_norm_rope(x, y, gamma, eps, batch, heads, head_dim, rope_cos, rope_sin, max_ctx, positions,
+                             status, as_stream(stream));
+}
+
+int q4d_kv_append(const q4d_kv_cache_t* kv, int32_t layer, const float* k, const float* v,
+                  const int32_t* positions, int32_t* status, void* stream) {
+  if (!kv || !kv->data || (!k && !v) || !positions || !status) return Q4D_ERR_NULL;
+  if (layer < 0 || layer >= kv->num_layers) return Q4D_ERR_BAD_LAYER;
+  if (kv->batch <= 0 || kv->num_kv_heads <= 0 || kv->max_ctx <= 0 || kv->head_dim <= 0) return Q4D_ERR_SHAPE;
+  return launch_kv_append(kv, layer, k, v, positions, status, as_stream(stream));
+}
+
+int q4d_cached_attention(const q4d_model_t* model, const q4d_kv_cache_t* kv, int32_t layer, const float* q,
+                         const int32_t* positions, void* out, int32_t out_dtype, void* ws, size_t ws_bytes,
+                         void* stream) {
+  if (!model || !q || !positions || !out) return Q4D_ERR_NULL;
+  if (model->head_dim != 128 || model->num_q_heads != 2 * model->num_kv_heads) return Q4D_ERR_SHAPE;
+  if (out_dtype != Q4D_F16 && out_dtype != Q4D_F32) return Q4D_ERR_DTYPE;
+  int rc;
+  if (!kv) return Q4D_ERR_NULL;
+  if (layer < 0 || layer >= kv->num_layers) return Q4D_ERR_BAD_LAYER;
+  if ((rc = check_kv(kv, model, kv->batch))) return rc;
+  if ((rc = check_ws(ws, ws_bytes, model, kv->batch))) return rc;
+  const WsLayout W = ws_layout(model, kv->batch);
+  AttnArgs t;
+  memset(&t, 0, sizeof(t));
+  t.fused = 0;
+  t.q = q;
+  t.scaling = model->attn_scaling;
+  kv_planes(kv, layer, &t.kcache, &t.vcache);
+  t.positions = positions;
+  t.batch = kv->batch;
+  t.qh = model->num_q_heads;
+  t.kvh = model->num_kv_heads;
+  t.d = model->head_dim;
+  t.max_ctx = model->max_ctx;
+  t.nsplit_max = W.nsplit_max;
+  t.part_ml = ws_ptr<float>(ws, W.part_ml);
+  t.part_acc = ws_ptr<float>(ws, W.part_acc);
+  t.counters = ws_ptr<int>(ws, W.counters);
+  t.out = out;
+  t.out_dtype = out_dtype;
+  t.status = ws_ptr<int32_t>(ws, W.status);
+  return launch_attention(t, as_stream(stream));
+}
+
+int q4d_embedding(const q4d_matrix_t* table, const int32_t* tokens, int32_t batch, float* hidden,
+                  int32_t* status, void* stream) {
+  if (!table || !tokens || !hidden) return Q4D_ERR_NULL;
+  int rc = check_matrix(table, table->rows, table->cols);
+  if (rc) return rc;
+  if (batch <= 0 || table->cols % 64) return Q4D_ERR_SHAPE;
+  return launch_embedding(table, tokens, batch, hidden, status, as_stream(stream));
+}
+
+int q4d_lm_head_argmax(const q4d_model_t* model, const float* hidden, int32_t* out_token, float* out_score,
+                       float* logits, void* ws, size_t ws_bytes, void* stream) {
+  if (!model || !hidden || !out_token || !out_score || !model->final_norm) return Q4D_ERR_NULL;
+  int rc = check_matrix(&model->embed_tokens, model->vocab_size, model->hidden_size);
+  if (rc) return rc;
+  if (model->hidden_size != 1024 || (model->vocab_size & 1)) return Q4D_ERR_SHAPE;
+  if ((rc = check_ws(ws, ws_bytes, model, 1))) return rc;
+  return run_lm_head(model, hidden, out_token, out_score, logits, ws, ws_layout(model, 1), as_stream(stream));
+}
+
+int q4d_decoder_layer(const q4d_model_t* model, int32_t layer, const float* hidden_in, float* hidden_out,
+                      const q4d_kv_cache_t* kv, const int32_t* positions, void* ws, size_t ws_bytes,
+                      void* stream) {
+  if (!hidden_in || !hidden_out || !positions) return Q4D_ERR_NULL;
+  int rc = check_model(model);
+  if (rc) return rc;
+  if (layer < 0 || layer >= model->num_layers) return Q4D_ERR_BAD_LAYER;
+  if ((rc = check_kv(kv, model, 1))) return rc;
+  if (kv->batch != 1) return Q4D_ERR_CAPACITY;
+  if ((rc = check_ws(ws, ws_bytes, model, 1))) return rc;
+  return run_layer(model, layer, hidden_in, hidden_out, kv, positions, ws, ws_layout(model, 1), as_stream(stream));
+}
+
+int q4d_layer_stage(const q4d_model_t* model, int32_t layer, int32_t stage, const float* hidden_in,
+                    float* hidden_out, const q4d_kv_cache_t* kv, const int32_t* positions, void* ws,
+                    size_t ws_bytes, void* stream) {
+  if (stage < Q4D_STAGE_QKV || stage > Q4D_STAGE_DOWN) return Q4D_ERR_SHAPE;
+  if (!hidden_in || !hidden_out || !positions) return Q4D_ERR_NULL;
+  int rc = check_model(model);
+  if (rc) return rc;
+  if (layer < 0 || layer >= model->num_layers) return Q4D_ERR_BAD_LAYER;
+  if ((rc = check_kv(kv, model, 1))) return rc;
+  if (kv->batch != 1) return Q4D_ERR_CAPACITY;
+  if ((rc = check_ws(ws, ws_bytes, model, 1))) return rc;
+  return run_layer(model, layer, hidden_in, hidden_out, kv, positions, ws, ws_layout(model, 1),
+                   as_stream(stream), stage);
+}
+
+int q4d_run_one_token(const q4d_model_t* model, const int32_t* tokens, const int32_t* positions,
+                      const q4d_kv_cache_t* kv, int32_t* next_token, float* score, float* logits, void* ws,
+                      size_t ws_bytes, void* stream) {
+  if (!tokens || !positions || !next_token || !score) return Q4D_ERR_NULL;
+  int rc = check_model(model);
+  if (rc) return rc;
+  if ((rc = check_kv(kv, model, 1))) return rc;
+  if (kv->batch != 1) return Q4D_ERR_CAPACITY;
+  if ((rc = check_ws(ws, ws_bytes, model, 1))) return rc;
+  const WsLayout W = ws_layout(model, 1);
+  hipStream_t st = as_stream(stream);
+  float* hidden = ws_ptr<float>(ws, W.hidden);
+  if ((rc = launch_embedding(&model->embed_tokens, tokens, 1, hidden, ws_ptr<int32_t>(ws, W.status), st)))
+    return rc;
+  for (int l = 0; l < model->num_layers; ++l)
+    if ((rc = run_layer(model, l, hidden, hidden, kv, positions, ws, W, st))) return rc;
+  return run_lm_head(model, hidden, next_token, score, logits, ws, W, st);
+}
+
+int q4d_advance(int32_t* tokens, int32_t* positions, const int32_t* next_token, const float* score,
+                int32_t* hist_tokens, float* hist_scores, int32_t* hist_count, int32_t hist_capacity,
+                void* stream) {
+  if (!tokens || !positions || !next_token) return Q4D_ERR_NULL;
+  if (hist_tokens && (!hist_count || !score || hist_capacity < 0)) return Q4D_ERR_NULL;
+  return launch_advance(tokens, positions, next_token, score, hist_tokens, hist_scores, hist_count,
+                        hist_capacity, as_stream(stream));
+}
+
+int q4d_apply_rope(const float* x, float* y, const float* cos, const float* sin, int32_t batch, int32_t heads,
+                   int32_t head_dim, void* stream) {
+  if (!x || !y || !cos || !sin) return Q4D_ERR_NULL;
+  if (batch <= 0 || heads <= 0 || head_dim <= 0 || (head_dim & 1)) return Q4D_ERR_SHAPE;
+  return launch_apply_rope(x, y, cos, sin, batch, heads, head_dim, as_stream(stream));
+}
+
+}  // extern "C"

@@ -1,0 +1,146 @@
+// Host-side internals shared by the libq4dec translation units.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "../../include/q4dec.h"
+
+namespace q4d {
+
+// Decode attention splits the context into chunks of this many positions.
+constexpr int kAttnChunk = 64;
+// Upper bound on the LM-head grid (one partial argmax per block).
+constexpr int kLmMaxBlocks = 2048;
+
+inline size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+// Byte offsets of the regions of a caller-provided workspace.
+struct WsLayout {
+  size_t status;     // int32[64]: [0] = status bits
+  size_t counters;   // int32[batch * kv_heads] attention split counters, then 1 LM counter
+  size_t hidden;     // f32 [batch, hidden]          residual stream
+  size_t qkv;        // f32 [batch, (qh + 2 kvh) * d] raw q|k|v projections
+  size_t qrope;      // f32 [batch, qh * d]          q after norm + RoPE (primitive path)
+  size_t attn;       // f32 [batch, qh * d]          attention output (o_proj input)
+  size_t act;        // f32 [batch, intermediate]    silu(gate) * up
+  size_t part_ml;    // f32 [batch, qh, nsplit, 2]   split max / sum
+  size_t part_acc;   // f32 [batch, qh, nsplit, d]   split partial outputs
+  size_t lm_part;    // {f32 score, i32 idx}[kLmMaxBlocks]
+  size_t total;
+  int nsplit_max;
+  int lm_counter_index;  // index into counters
+};
+
+inline WsLayout ws_layout(const q4d_model_t* m, int batch) {
+  WsLayout L{};
+  const size_t A = 256;
+  const int d = m->head_dim, qh = m->num_q_heads, kvh = m->num_kv_heads;
+  L.nsplit_max = (m->max_ctx + kAttnChunk - 1) / kAttnChunk;
+  size_t o = 0;
+  L.status = o;   o = align_up(o + 64 * 4, A);
+  L.counters = o; o = align_up(o + (size_t)(batch * kvh + 1) * 4, A);
+  L.lm_counter_index = batch * kvh;
+  L.hidden = o;   o = align_up(o + (size_t)batch * m->hidden_size * 4, A);
+  L.qkv = o;      o = align_up(o + (size_t)batch * (qh + 2 * kvh) * d * 4, A);
+  L.qrope = o;    o = align_up(o + (size_t)batch * qh * d * 4, A);
+  L.attn = o;     o = align_up(o + (size_t)batch * qh * d * 4, A);
+  L.act = o;      o = align_up(o + (size_t)batch * m->intermediate_size * 4, A);
+  L.part_ml = o;  o = align_up(o + (size_t)batch * qh * L.nsplit_max * 2 * 4, A);
+  L.part_acc = o; o = align_up(o + (size_t)batch * qh * L.nsplit_max * d * 4, A);
+  L.lm_part = o;  o = align_up(o + (size_t)kLmMaxBlocks * 8, A);
+  L.total = o;
+  return L;
+}
+
+template <class T>
+inline T* ws_ptr(void* ws, size_t off) {
+  return reinterpret_cast<T*>(static_cast<char*>(ws) + off);
+}
+
+inline bool aligned(const void* p, size_t a) {
+  return (reinterpret_cast<uintptr_t>(p) % a) == 0;
+}
+
+inline int check_launch() {
+  hipError_t e = hipGetLastError();
+  return e == hipSuccess ? Q4D_OK : Q4D_ERR_LAUNCH;
+}
+
+// ---- GEMV launcher ---------------------------------------------------------
+enum XMode { X_F16 = 0, X_F32 = 1, X_RMS = 2 };
+enum EpMode { EP_F16 = 0, EP_F32 = 1, EP_RESID = 2, EP_SWIGLU = 3, EP_ARGMAX = 4 };
+
+struct GemvArgs {
+  // Up to three row segments stacked into one logical [rows, K] matrix.
+  const uint8_t* w[3];
+  const uint16_t* s[3];
+  int seg_end[3];   // cumulative row ends
+  int nseg;
+  int rows;         // logical rows (PAIR mode: rows of each of the two segments)
+  int cols;         // K
+  // Activations.
+  const void* x;        // X_F16: fp16 [batch, K]; X_F32 / X_RMS: fp32 [batch, K]
+  const float* gamma;   // X_RMS
+  float eps;            // X_RMS
+  // Epilogue.
+  void* y;              // output (see EpMode)
+  const float* resid;   // EP_RESID: y = resid + W x
+  // EP_ARGMAX.
+  float* logits;        // optional
+  void* lm_part;
+  int* counter;
+  int* out_token;
+  float* out_score;
+  int batch;
+};
+
+// Validates geometry, picks the kernel instance and launches.  Returns Q4D_*.
+int launch_gemv(const GemvArgs& a, int xmode, int epmode, bool pair, hipStream_t stream);
+
+// ---- other launchers ---------------------------------------------------------
+int launch_rms_norm(const float* x, const float* gamma, float eps, int rows, int dim, void* y,
+                    int y_dtype, hipStream_t stream);
+int launch_embedding(const q4d_matrix_t* t, const int32_t* tokens, int batch, float* hidden,
+                     int32_t* status, hipStream_t stream);
+int launch_qk_norm_rope(const float* x, float* y, const float* gamma, float eps, int batch,
+                        int heads, int head_dim, const float* cosT, const float* sinT, int max_ctx,
+                        const int32_t* positions, int32_t* status, hipStream_t stream);
+int launch_kv_append(const q4d_kv_cache_t* kv, int layer, const float* k, const float* v,
+                     const int32_t* positions, int32_t* status, hipStream_t stream);
+
+struct AttnArgs {
+  // fused = 1: q/k/v are raw projections in `qkv` ([batch, (qh+2kvh)*d]); the
+  // kernel applies q/k RMSNorm + RoPE and appends k/v to the cache.
+  // fused = 0: q is ready ([batch, qh*d], normed, roped); cache already holds pos.
+  int fused;
+  const float* qkv;
+  const float* q;
+  const float* q_gamma;
+  const float* k_gamma;
+  float eps;
+  float scaling;
+  const float* rope_cos;
+  const float* rope_sin;
+  uint16_t* kcache;  // layer's K plane: [batch][kvh][max_ctx][d]
+  uint16_t* vcache;
+  const int32_t* positions;
+  int batch, qh, kvh, d, max_ctx, nsplit_max;
+  float* part_ml;
+  float* part_acc;
+  int* counters;
+  void* out;
+  int out_dtype;
+  int32_t* status;
+};
+int launch_attention(const AttnArgs& a, hipStream_t stream);
+
+int launch_fill_i32(int32_t* p, int32_t v, size_t n, hipStream_t stream);
+int launch_advance(int32_t* tokens, int32_t* positions, const int32_t* next_token, const float* score,
+                   int32_t* hist_tokens, float* hist_scores, int32_t* hist_count, int32_t hist_capacity,
+                   hipStream_t stream);
+int launch_apply_rope(const float* x, float* y, const float* cosv, const float* sinv, int batch, int heads,
+                      int head_dim, hipStream_t stream);
+
+}  // namespace q4d

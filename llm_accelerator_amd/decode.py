@@ -1,0 +1,132 @@
+"""Greedy decode driver: serial prefill, then device-resident token feedback.
+
+The loop is the reference's (``10_validate_full_run_one_token.py:81-172``,
+``Qwen3-0.6B-Base/pc_testing/02_serial_decode.py:33-59``, and the board's
+``qot_decode_token_ids``, ``qmap_one_token_runtime.h:399+``): every prompt
+token runs one full step at its position, the argmax after the last prompt
+token is the first generated id, and each generated id is fed back at the
+next position.  Here the token and position live in device memory and
+``q4d_advance`` moves them forward, so a HIP graph of ``steps_per_graph``
+captured steps replays the loop with no host round trip per token.
+"""
+
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from . import _lib
+from ._lib import check
+from .model import KVCache, Q4ForCausalLM, Workspace, current_stream
+
+
+class GreedyDecoder:
+    def __init__(self, model: Q4ForCausalLM, steps_per_graph: int = 16, use_graph: bool = True):
+        self.model = model
+        cfg = model.config
+        dev = model.device
+        self.kv = KVCache(cfg, len(model.model.layers), 1, model.max_ctx, dev)
+        self.ws = Workspace(model, 1)
+        self.tok = torch.zeros(1, dtype=torch.int32, device=dev)
+        self.pos = torch.zeros(1, dtype=torch.int32, device=dev)
+        self.next_tok = torch.zeros(1, dtype=torch.int32, device=dev)
+        self.score = torch.zeros(1, dtype=torch.float32, device=dev)
+        self.hist_cap = model.max_ctx
+        self.hist_tok = torch.zeros(self.hist_cap, dtype=torch.int32, device=dev)
+        self.hist_score = torch.zeros(self.hist_cap, dtype=torch.float32, device=dev)
+        self.hist_count = torch.zeros(1, dtype=torch.int32, device=dev)
+        self.steps_per_graph = steps_per_graph
+        self.use_graph = use_graph
+        self._graph = None
+        self._desc = model.descriptor()
+        self._kvd = self.kv.descriptor()
+        self._lib = _lib.load()
+        self.position = 0
+
+    # -- one step, launched on the current stream ---------------------------------
+    def _launch_step(self, logits: torch.Tensor | None = None, record: bool = True) -> None:
+        st = current_stream()
+        check(self._lib.q4d_run_one_token(ctypes.byref(self._desc), self.tok.data_ptr(), self.pos.data_ptr(),
+                                          ctypes.byref(self._kvd), self.next_tok.data_ptr(),
+                                          self.score.data_ptr(), logits.data_ptr() if logits is not None else None,
+                                          self.ws.ptr, self.ws.nbytes, st), "q4d_run_one_token")
+        check(self._lib.q4d_advance(self.tok.data_ptr(), self.pos.data_ptr(), self.next_tok.data_ptr(),
+                                    self.score.data_ptr(), self.hist_tok.data_ptr() if record else None,
+                                    self.hist_score.data_ptr() if record else None, self.hist_count.data_ptr(),
+                                    self.hist_cap, st), "q4d_advance")
+
+    def reset(self) -> None:
+        self.kv.data.zero_()
+        self.hist_count.zero_()
+        self.pos.zero_()
+        self.position = 0
+
+    def step(self, token: int | None = None, logits: torch.Tensor | None = None, record: bool = True) -> None:
+        """One eager step; ``token`` overrides the fed-back id (teacher forcing)."""
+        if self.position >= self.model.max_ctx:
+            raise _lib.Q4DecError(-10, "GreedyDecoder.step")
+        if token is not None:
+            if not 0 <= int(token) < self.model.config.vocab_size:
+                raise _lib.Q4DecError(-8, "GreedyDecoder.step")
+            self.tok.fill_(int(token))
+        self._launch_step(logits, record)
+        self.position += 1
+
+    def prefill(self, prompt: list[int]) -> None:
+        """Serial prefill: one full step per prompt token; only the step after
+        the last prompt token records its argmax as generated token 0."""
+        self.reset()
+        for i, t in enumerate(prompt):
+            self.step(int(t), record=(i == len(prompt) - 1))
+
+    def _capture(self) -> None:
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.stream(s):
+            with torch.cuda.graph(g, stream=s):
+                for _ in range(self.steps_per_graph):
+                    self._launch_step()
+        torch.cuda.current_stream().wait_stream(s)
+        self._graph = g
+
+    def generate(self, n: int) -> None:
+        """Run ``n`` more feedback steps (graph replays when enabled)."""
+        if self.position + n > self.model.max_ctx:
+            raise _lib.Q4DecError(-10, "GreedyDecoder.generate")
+        if not self.use_graph:
+            for _ in range(n):
+                self.step()
+            return
+        k = self.steps_per_graph
+        full, rest = divmod(n, k)
+        if full:
+            if self._graph is None:
+                # capturing records launches only; the captured steps run on replay
+                self._capture()
+            for _ in range(full):
+                self._graph.replay()
+            self.position += full * k
+        for _ in range(rest):
+            self.step()
+
+    def history(self) -> tuple[list[int], list[float]]:
+        c = int(self.hist_count.item())
+        return self.hist_tok[:c].tolist(), self.hist_score[:c].tolist()
+
+    def status(self) -> int:
+        out = ctypes.c_int32(0)
+        check(self._lib.q4d_read_status(self.ws.ptr, self.ws.nbytes, ctypes.byref(self._desc), 1, ctypes.byref(out),
+                                        current_stream()), "q4d_read_status")
+        return out.value
+
+
+def greedy_generate(model: Q4ForCausalLM, prompt: list[int], max_new_tokens: int, use_graph: bool = True,
+                    steps_per_graph: int = 16) -> tuple[list[int], list[float]]:
+    """Prompt ids -> ``max_new_tokens`` greedy ids and their winning logits."""
+    dec = GreedyDecoder(model, steps_per_graph=steps_per_graph, use_graph=use_graph)
+    dec.prefill(prompt)
+    dec.generate(max_new_tokens - 1)
+    torch.cuda.synchronize()
+    return dec.history()

@@ -1,0 +1,123 @@
+"""CPU-side checks of the C ABI: the library loads, exports every function
+include/q4dec.h declares, and host validation fails closed (negative codes,
+no launch) on bad descriptors.  No kernel is launched here."""
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from llm_accelerator_amd import _lib
+from llm_accelerator_amd._lib import Q4dKVCache, Q4dLayer, Q4dMatrix, Q4dModel
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "q4dec.h"
+
+
+def declared_functions():
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return sorted(set(re.findall(r"\b(q4d_\w+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not _lib.LIB_PATH.exists():
+        pytest.fail("libq4dec.so is not built: run `python -m llm_accelerator_amd.build`")
+    return _lib.load()
+
+
+def test_every_declared_symbol_is_exported_and_bound(lib):
+    names = declared_functions()
+    assert len(names) >= 17
+    for n in names:
+        assert hasattr(lib, n), n
+        assert n in _lib.SIGNATURES, f"{n} has no ctypes signature"
+
+
+def test_version_and_status_strings(lib):
+    assert lib.q4d_version() == 1
+    assert lib.q4d_status_string(0) == b"ok"
+    assert lib.q4d_status_string(-8) == b"token id outside the vocabulary"
+    assert lib.q4d_status_string(-10) == b"position outside the context"
+
+
+FAKE = 0x7F0000000000  # aligned, never dereferenced: validation fails before launch
+
+
+def _model(layers_arr, **kw):
+    d = dict(hidden_size=1024, intermediate_size=3072, num_layers=len(layers_arr), num_q_heads=16, num_kv_heads=8,
+             head_dim=128, vocab_size=151936, max_ctx=512, rms_norm_eps=1e-6, attn_scaling=128 ** -0.5)
+    d.update(kw)
+    m = Q4dModel(**d)
+    m.layers = ctypes.cast(layers_arr, ctypes.POINTER(Q4dLayer))
+    m.embed_tokens = Q4dMatrix(FAKE, FAKE, 151936, 1024)
+    m.final_norm = m.rope_cos = m.rope_sin = FAKE
+    return m
+
+
+def _layers(n=1):
+    arr = (Q4dLayer * n)()
+    for i in range(n):
+        L = arr[i]
+        for name, (r, c) in dict(q_proj=(2048, 1024), k_proj=(1024, 1024), v_proj=(1024, 1024), o_proj=(1024, 2048),
+                                 gate_proj=(3072, 1024), up_proj=(3072, 1024), down_proj=(1024, 3072)).items():
+            setattr(L, name, Q4dMatrix(FAKE, FAKE, r, c))
+        L.input_layernorm = L.post_attention_layernorm = L.q_norm = L.k_norm = FAKE
+    return arr
+
+
+def test_workspace_bytes_grows_with_context(lib):
+    arr = _layers()
+    a = lib.q4d_workspace_bytes(ctypes.byref(_model(arr, max_ctx=512)), 1)
+    b = lib.q4d_workspace_bytes(ctypes.byref(_model(arr, max_ctx=4096)), 1)
+    assert 0 < a < b
+    assert lib.q4d_workspace_bytes(None, 1) == 0
+
+
+def test_linear_rejects_bad_shapes_before_launch(lib):
+    m = Q4dMatrix(FAKE, FAKE, 3072, 1000)  # cols not supported
+    assert lib.q4d_linear(ctypes.byref(m), FAKE, 0, FAKE, 0, 1, None) == -11
+    m = Q4dMatrix(FAKE, FAKE, 3071, 1024)  # odd rows: a row pair would run off the matrix
+    assert lib.q4d_linear(ctypes.byref(m), FAKE, 0, FAKE, 0, 1, None) == -11
+    m = Q4dMatrix(FAKE + 8, FAKE, 3072, 1024)  # 128-bit loads need 16-byte rows
+    assert lib.q4d_linear(ctypes.byref(m), FAKE, 0, FAKE, 0, 1, None) == -4
+    m = Q4dMatrix(None, FAKE, 3072, 1024)
+    assert lib.q4d_linear(ctypes.byref(m), FAKE, 0, FAKE, 0, 1, None) == -7
+    m = Q4dMatrix(FAKE, FAKE, 3072, 1024)
+    assert lib.q4d_linear(ctypes.byref(m), FAKE, 7, FAKE, 0, 1, None) == -13
+    assert lib.q4d_linear(ctypes.byref(m), FAKE, 0, FAKE, 0, 0, None) == -11
+
+
+def test_model_validation_codes(lib):
+    arr = _layers(2)
+    kv = Q4dKVCache(data=FAKE, num_layers=2, batch=1, num_kv_heads=8, max_ctx=512, head_dim=128)
+    ws = FAKE
+    # wrong layer shape -> BAD_LAYER
+    arr[1].down_proj = Q4dMatrix(FAKE, FAKE, 1024, 2048)
+    m = _model(arr)
+    assert lib.q4d_decoder_layer(ctypes.byref(m), 0, FAKE, FAKE, ctypes.byref(kv), FAKE, ws, 1 << 30, None) == -2
+    arr[1].down_proj = Q4dMatrix(FAKE, FAKE, 1024, 3072)
+    # bad layer index
+    assert lib.q4d_decoder_layer(ctypes.byref(m), 5, FAKE, FAKE, ctypes.byref(kv), FAKE, ws, 1 << 30, None) == -2
+    # workspace too small
+    assert lib.q4d_decoder_layer(ctypes.byref(m), 0, FAKE, FAKE, ctypes.byref(kv), FAKE, ws, 16, None) == -9
+    # cache geometry mismatch
+    kv2 = Q4dKVCache(data=FAKE, num_layers=2, batch=1, num_kv_heads=8, max_ctx=256, head_dim=128)
+    assert lib.q4d_decoder_layer(ctypes.byref(m), 0, FAKE, FAKE, ctypes.byref(kv2), FAKE, ws, 1 << 30, None) == -11
+    # unsupported head geometry
+    m3 = _model(arr, num_q_heads=24)
+    assert lib.q4d_run_one_token(ctypes.byref(m3), FAKE, FAKE, ctypes.byref(kv), FAKE, FAKE, None, ws, 1 << 30,
+                                 None) == -11
+    # null outputs
+    assert lib.q4d_run_one_token(ctypes.byref(m), FAKE, FAKE, ctypes.byref(kv), None, FAKE, None, ws, 1 << 30,
+                                 None) == -7
+
+
+def test_activation_precision_setter(lib):
+    assert lib.q4d_set_activation_precision(3) == -13
+    assert lib.q4d_set_activation_precision(2) == 0
+
+
+def test_error_class_carries_code():
+    e = _lib.Q4DecError(-10, "x")
+    assert e.code == -10 and "CONTEXT" in str(e) and isinstance(e, RuntimeError)

@@ -1,0 +1,178 @@
+"""One decoder layer and the primitive ops on the GPU vs
+the oracle restatement of common.py:129-298.
+
+Config 2: hidden 1024, 16 q / 8 kv heads, head_dim 128, intermediate 3072,
+eps 1e-6, theta 1e6, random Q4 weights, fp16 KV cache pre-filled with
+N(0, 1) for 512 positions, one decode step at position 512.
+
+Tolerances (stated): against the oracle that stores K/V through fp16 like the
+device, the layer output must agree to max-abs <= 1e-4 * max|ref| with fp32
+activations (precision mode 2) and <= 3e-3 * max|ref| with fp16 activations
+(mode 1); the appended K/V row to within one fp16 ulp.  Against the pure fp32
+reference (fp32 K/V) the errors are reported.
+"""
+
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+import oracle as o
+from gpu_helpers import report
+from llm_accelerator_amd import _lib, common
+from llm_accelerator_amd._lib import check
+from llm_accelerator_amd.model import KVCache, Qwen3Config, build_model, current_stream, random_host_weights
+
+pytestmark = pytest.mark.gpu
+
+CTX = 512
+
+
+@pytest.fixture(scope="module")
+def layer_setup(dev):
+    cfg = Qwen3Config(num_hidden_layers=1, vocab_size=2048)
+    host = random_host_weights(cfg, seed=0, num_layers=1)
+    model = build_model(cfg, host, max_ctx=1024, device=dev)
+    ocfg = o.OracleConfig(num_hidden_layers=1, vocab_size=2048)
+    om64 = o.OracleModel.from_q4(ocfg, host["layers"], *host["embed_tokens"], host["norm"], dtype=np.float64)
+    om32 = o.OracleModel.from_q4(ocfg, host["layers"], *host["embed_tokens"], host["norm"], dtype=np.float32)
+    rng = np.random.default_rng(2)
+    kv_k = rng.normal(size=(1, 8, CTX, 128)).astype(np.float16)
+    kv_v = rng.normal(size=(1, 8, CTX, 128)).astype(np.float16)
+    hidden = np.random.default_rng(1).normal(size=(1, 1, 1024)).astype(np.float32)
+    return cfg, model, om64, om32, kv_k, kv_v, hidden
+
+
+def _run_gpu_layer(cfg, model, kv_k, kv_v, hidden, precision, dev):
+    lib = _lib.load()
+    check(lib.q4d_set_activation_precision(precision), "set precision")
+    kv = KVCache(cfg, 1, 1, model.max_ctx, dev)
+    kv.data[0, 0, 0, :, :CTX] = torch.from_numpy(kv_k[0]).to(dev)
+    kv.data[0, 1, 0, :, :CTX] = torch.from_numpy(kv_v[0]).to(dev)
+    kcs, vcs = common.layer_views(kv, CTX)
+    h = torch.from_numpy(hidden).to(dev)
+    out, k2, v2 = common.manual_decoder_layer_cached(
+        hidden=h, layer=model.model.layers[0], rotary_emb=model.model.rotary_emb,
+        position_ids=torch.tensor([[CTX]]), k_cache=kcs[0], v_cache=vcs[0], batch_size=1, num_q_heads=16,
+        num_kv_heads=8, head_dim=128, kv_repeat=2, model_config=cfg)
+    torch.cuda.synchronize()
+    check(lib.q4d_set_activation_precision(2), "set precision")
+    assert k2.length == v2.length == CTX + 1
+    return out.cpu().numpy(), kv.data[0, 0, 0, :, CTX].float().cpu().numpy(), kv.data[0, 1, 0, :, CTX].float().cpu().numpy()
+
+
+def _oracle_layer(om, kv_k, kv_v, hidden, kv_store):
+    dt = om.dtype
+    return o.manual_decoder_layer_cached(hidden.astype(dt), om.layers[0], om.config, om.inv_freq,
+                                         np.array([[CTX]]), kv_k.astype(dt), kv_v.astype(dt),
+                                         kv_store_dtype=kv_store)
+
+
+@pytest.mark.parametrize("precision,tol", [(2, 1e-4), (1, 3e-3)])
+def test_decoder_layer_config2(dev, layer_setup, precision, tol):
+    cfg, model, om64, om32, kv_k, kv_v, hidden = layer_setup
+    out, knew, vnew = _run_gpu_layer(cfg, model, kv_k, kv_v, hidden, precision, dev)
+    ref, kc, vc = _oracle_layer(om64, kv_k, kv_v, hidden, np.float16)
+    mx, rel = report(f"layer mode{precision} vs fp16-KV oracle", out, ref)
+    assert rel <= tol
+    # appended row: the oracle's fp16 K/V within one fp16 ulp
+    for got, want in ((knew, kc[0, :, CTX]), (vnew, vc[0, :, CTX])):
+        ulp = np.spacing(np.abs(want).astype(np.float16)).astype(np.float64)
+        assert np.all(np.abs(got - want) <= ulp), float(np.max(np.abs(got - want) / ulp))
+    ref32, _, _ = _oracle_layer(om32, kv_k, kv_v, hidden, None)
+    report(f"layer mode{precision} vs fp32 reference", out, ref32)
+
+
+def test_layer_repeat_is_deterministic(dev, layer_setup):
+    cfg, model, _, _, kv_k, kv_v, hidden = layer_setup
+    a = _run_gpu_layer(cfg, model, kv_k, kv_v, hidden, 2, dev)
+    b = _run_gpu_layer(cfg, model, kv_k, kv_v, hidden, 2, dev)
+    for x, y in zip(a, b):
+        np.testing.assert_array_equal(x, y)
+
+
+def test_primitive_ops_match_oracle(dev, layer_setup):
+    """manual_rms_norm, manual_linear_from_weight, qk-norm + RoPE via
+    manual_rope_cos_sin / manual_apply_rope, append_cache and
+    manual_cached_attention, composed exactly as common.py:245-284 does."""
+    cfg, model, om64, _, kv_k, kv_v, hidden = layer_setup
+    L = model.model.layers[0]
+    OL = om64.layers[0]
+    h = torch.from_numpy(hidden).to(dev)
+    eps = cfg.rms_norm_eps
+    xn = common.manual_rms_norm(h, L.input_layernorm.weight, eps)
+    xn_ref = o.manual_rms_norm(hidden.astype(np.float64), OL.input_layernorm, eps, np.float64)
+    assert report("rms_norm", xn.cpu().numpy(), xn_ref)[1] < 1e-6
+    q = common.manual_linear_from_weight(xn, L.self_attn.q_proj.weight)
+    k = common.manual_linear_from_weight(xn, L.self_attn.k_proj.weight)
+    v = common.manual_linear_from_weight(xn, L.self_attn.v_proj.weight)
+    q_ref = xn_ref @ OL.q_proj.T
+    assert report("q_proj", q.cpu().numpy(), q_ref)[1] < 1e-5
+    qn = common.manual_rms_norm(q.view(1, 1, 16, 128), L.self_attn.q_norm.weight, eps).transpose(1, 2)
+    kn = common.manual_rms_norm(k.view(1, 1, 8, 128), L.self_attn.k_norm.weight, eps).transpose(1, 2)
+    pos = torch.tensor([[CTX]])
+    cos, sin = common.manual_rope_cos_sin(model.model.rotary_emb, h, pos)
+    c_ref, s_ref = o.manual_rope_cos_sin(om64.inv_freq, np.array([[CTX]]))
+    np.testing.assert_allclose(cos.cpu().numpy(), c_ref, atol=2e-6)
+    qr, kr = common.manual_apply_rope(qn, kn, cos, sin)
+    kv = KVCache(cfg, 1, 1, model.max_ctx, dev)
+    kv.data[0, 0, 0, :, :CTX] = torch.from_numpy(kv_k[0]).to(dev)
+    kv.data[0, 1, 0, :, :CTX] = torch.from_numpy(kv_v[0]).to(dev)
+    kcs, vcs = common.layer_views(kv, CTX)
+    kc = common.append_cache(kcs[0], kr)
+    vc = common.append_cache(vcs[0], v.view(1, 1, 8, 128).transpose(1, 2))
+    out, weights = common.manual_cached_attention(qr, common.manual_repeat_kv(kc, 2), common.manual_repeat_kv(vc, 2),
+                                                  L.self_attn.scaling)
+    assert weights is None and kc.length == CTX + 1
+    trace = {}
+    o.manual_decoder_layer_cached(hidden.astype(np.float64), OL, om64.config, om64.inv_freq, np.array([[CTX]]),
+                                  kv_k.astype(np.float64), kv_v.astype(np.float64), kv_store_dtype=np.float16,
+                                  trace=trace)
+    attn_ref = trace["attn"].reshape(1, 16, 1, 128)
+    assert report("attention", out.cpu().numpy(), attn_ref)[1] < 1e-4
+
+
+def test_embedding_gather_exact(dev, layer_setup):
+    cfg, model, om64, _, _, _, _ = layer_setup
+    lib = _lib.load()
+    toks = torch.tensor([0, 7, 2047], dtype=torch.int32, device=dev)
+    out = torch.empty((3, 1024), dtype=torch.float32, device=dev)
+    status = torch.zeros(1, dtype=torch.int32, device=dev)
+    desc = model.lm_head.weight.descriptor()
+    check(lib.q4d_embedding(ctypes.byref(desc), toks.data_ptr(), 3, out.data_ptr(), status.data_ptr(),
+                            current_stream()), "q4d_embedding")
+    np.testing.assert_array_equal(out.cpu().numpy(), om64.embed_tokens[[0, 7, 2047]].astype(np.float32))
+    assert int(status.item()) == 0
+    # a device-side token outside the vocabulary: zero row and a status bit, no fault
+    bad = torch.tensor([2048], dtype=torch.int32, device=dev)
+    check(lib.q4d_embedding(ctypes.byref(desc), bad.data_ptr(), 1, out.data_ptr(), status.data_ptr(),
+                            current_stream()), "q4d_embedding")
+    torch.cuda.synchronize()
+    assert int(status.item()) == _lib.STATUS_BAD_TOKEN and float(out[0].abs().sum()) == 0.0
+
+
+def test_bad_position_is_reported_not_executed(dev, layer_setup):
+    cfg, model, _, _, _, _, hidden = layer_setup
+    lib = _lib.load()
+    ws = common.runtime(model).ws
+    kv = KVCache(cfg, 1, 1, model.max_ctx, dev)
+    before = kv.data.clone()
+    pos = torch.tensor([model.max_ctx], dtype=torch.int32, device=dev)  # one past the end
+    h = torch.from_numpy(hidden.reshape(1, 1024)).to(dev)
+    out = torch.empty_like(h)
+    desc, kvd = model.descriptor(), kv.descriptor()
+    check(lib.q4d_decoder_layer(ctypes.byref(desc), 0, h.data_ptr(), out.data_ptr(), ctypes.byref(kvd),
+                                pos.data_ptr(), ws.ptr, ws.nbytes, current_stream()), "q4d_decoder_layer")
+    st = ctypes.c_int32(0)
+    check(lib.q4d_read_status(ws.ptr, ws.nbytes, ctypes.byref(desc), 1, ctypes.byref(st), current_stream()),
+          "q4d_read_status")
+    assert st.value & _lib.STATUS_BAD_POSITION
+    assert torch.equal(kv.data, before)
+    # clear the sticky status for later tests
+    ws.buf[:256].zero_()
+    with pytest.raises(_lib.Q4DecError) as e:
+        common.manual_decoder_layer_cached(h.view(1, 1, 1024), model.model.layers[0], model.model.rotary_emb,
+                                           torch.tensor([[5]]), *[x[0] for x in common.layer_views(kv, 3)], 1, 16, 8,
+                                           128, 2, cfg)
+    assert e.value.code == -10
