@@ -113,7 +113,10 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const AttnArgs a) {
       const u32x4 kk = *reinterpret_cast<const u32x4*>(kb + (size_t)(start + p) * D + sub * 8);
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const h2 k2 = __builtin_bit_cast(h2, kk[e]);
+        // copy the element out first: bit-casting a vector element expression
+        // directly reads element 0 with this compiler
+        const uint32_t ke = kk[e];
+        const h2 k2 = __builtin_bit_cast(h2, ke);
         const float ka = (float)k2.x, kc = (float)k2.y;
         s0 = fmaf(q0[2 * e], ka, s0);
         s0 = fmaf(q0[2 * e + 1], kc, s0);
