@@ -77,6 +77,38 @@ __device__ __forceinline__ float chunk_dot_hl(const u32x4 w, const XChunk& h, co
          fmaf(c, 16777216.f, fmaf(d, 1048576.f, -l.sum8));
 }
 
+// Issue the loads of U row groups starting at gbase (wave-uniform guards).
+template <int K, int U, bool PAIR>
+__device__ __forceinline__ void load_batch(int gbase, int nw, int NG, int lane, const uint8_t* w0,
+                                           const uint8_t* w1, const uint8_t* w2, const uint16_t* s0,
+                                           const uint16_t* s1, const uint16_t* s2, int e0, int e1,
+                                           u32x4 (&wv)[U][Geo<K>::LG], uint32_t (&sv)[U][Geo<K>::LG]) {
+  constexpr int C = Geo<K>::C, RG = Geo<K>::RG, LG = Geo<K>::LG, G = Geo<K>::G;
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int g = gbase + u * nw;
+    if (g < NG) {
+      int seg = 0, local0 = g;
+      if constexpr (!PAIR) {
+        const int row0 = g * RG;
+        seg = (row0 < e0) ? 0 : ((row0 < e1) ? 1 : 2);
+        local0 = row0 - (seg == 0 ? 0 : (seg == 1 ? e0 : e1));
+      }
+#pragma unroll
+      for (int j = 0; j < LG; ++j) {
+        const int f = j * 64 + lane;
+        const int r = f / C, c = f % C;
+        const int sg = PAIR ? r : seg;
+        const int row = PAIR ? g : local0 + r;
+        const uint8_t* wb = sg == 0 ? w0 : (sg == 1 ? w1 : w2);
+        const uint16_t* sb = sg == 0 ? s0 : (sg == 1 ? s1 : s2);
+        wv[u][j] = *reinterpret_cast<const u32x4*>(wb + (size_t)row * (K / 2) + c * 16);
+        sv[u][j] = sb[(size_t)row * G + (c >> 1)];
+      }
+    }
+  }
+}
+
 template <int K, int U, int XM, int XP, int EP, bool PAIR>
 __global__ __launch_bounds__(256) void gemv_kernel(const GemvArgs a) {
   using Gm = Geo<K>;
@@ -89,111 +121,128 @@ __global__ __launch_bounds__(256) void gemv_kernel(const GemvArgs a) {
   __shared__ float s_red[4];
   __shared__ int s_idx[4];
   __shared__ int s_last;
+  __shared__ f32x4 s_x[XM == X_RMS ? K / 4 : 1];
+
+  // Segment pointers are read with constant indices (scalar kernel-argument
+  // loads) and selected in registers: indexing a.w[] with a runtime value
+  // turns every weight load into a dependent load from the argument block.
+  const uint8_t* const w0 = a.w[0];
+  const uint8_t* const w1 = a.w[1];
+  const uint8_t* const w2 = a.w[2];
+  const uint16_t* const s0 = a.s[0];
+  const uint16_t* const s1 = a.s[1];
+  const uint16_t* const s2 = a.s[2];
+  const int e0 = a.seg_end[0], e1 = a.seg_end[1];
+  const int NG = PAIR ? a.rows : a.rows / RG;
+  const int gw = blockIdx.x * 4 + wid;
+  const int nw = gridDim.x * 4;
+
+  // The first batch of weights is in flight while the activations are prepared.
+  u32x4 wv[U][LG];
+  uint32_t sv[U][LG];
+  load_batch<K, U, PAIR>(gw, nw, NG, lane, w0, w1, w2, s0, s1, s2, e0, e1, wv, sv);
 
   // ---- activations for this lane's chunks ----------------------------------
   XChunk xh[LG];
   XChunk xl[XP == 2 ? LG : 1];
-  float inv_rms = 1.f;
   if constexpr (XM == X_RMS) {
-    const float* h = static_cast<const float*>(a.x) + (size_t)bat * K;
+    // stage the fp32 hidden vector in LDS with one 16-byte load per thread,
+    // reduce sum(x^2) in a fixed order (identical in every block)
+    const f32x4* hv = reinterpret_cast<const f32x4*>(static_cast<const float*>(a.x) + (size_t)bat * K);
     float ss = 0.f;
-    for (int i = threadIdx.x; i < K; i += 256) ss = fmaf(h[i], h[i], ss);
+#pragma unroll
+    for (int i = threadIdx.x; i < K / 4; i += 256) {
+      const f32x4 t = hv[i];
+      s_x[i] = t;
+      ss = fmaf(t[0], t[0], ss);
+      ss = fmaf(t[1], t[1], ss);
+      ss = fmaf(t[2], t[2], ss);
+      ss = fmaf(t[3], t[3], ss);
+    }
     ss = wave_sum(ss);
     if (lane == 0) s_red[wid] = ss;
     __syncthreads();
-    const float tot = (s_red[0] + s_red[1]) + (s_red[2] + s_red[3]);
-    inv_rms = 1.0f / sqrtf(tot / (float)K + a.eps);
-  }
+    const float inv_rms = 1.0f / sqrtf(((s_red[0] + s_red[1]) + (s_red[2] + s_red[3])) / (float)K + a.eps);
 #pragma unroll
-  for (int j = 0; j < LG; ++j) {
-    const int c = (j * 64 + lane) % C;
-    if constexpr (XM == X_F16) {
-      const u32x4* xp = reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(a.x) +
-                                                       (size_t)bat * K + c * 32);
-      uint32_t xw[16];
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const u32x4 t = xp[q];
-        xw[4 * q + 0] = t[0];
-        xw[4 * q + 1] = t[1];
-        xw[4 * q + 2] = t[2];
-        xw[4 * q + 3] = t[3];
-      }
-      xchunk_from_words(xw, xh[j]);
-    } else {
-      const f32x4* xp = reinterpret_cast<const f32x4*>(static_cast<const float*>(a.x) +
-                                                       (size_t)bat * K + c * 32);
+    for (int j = 0; j < LG; ++j) {
+      const int c = (j * 64 + lane) % C;
+      const f32x4* gp = reinterpret_cast<const f32x4*>(a.gamma + c * 32);
       float v[32];
 #pragma unroll
       for (int q = 0; q < 8; ++q) {
-        const f32x4 t = xp[q];
-        v[4 * q + 0] = t[0];
-        v[4 * q + 1] = t[1];
-        v[4 * q + 2] = t[2];
-        v[4 * q + 3] = t[3];
-      }
-      if constexpr (XM == X_RMS) {
-        const f32x4* gp = reinterpret_cast<const f32x4*>(a.gamma + c * 32);
-#pragma unroll
-        for (int q = 0; q < 8; ++q) {
-          const f32x4 g = gp[q];
-          v[4 * q + 0] = (v[4 * q + 0] * inv_rms) * g[0];
-          v[4 * q + 1] = (v[4 * q + 1] * inv_rms) * g[1];
-          v[4 * q + 2] = (v[4 * q + 2] * inv_rms) * g[2];
-          v[4 * q + 3] = (v[4 * q + 3] * inv_rms) * g[3];
-        }
+        const f32x4 t = s_x[c * 8 + q];
+        const f32x4 g = gp[q];
+        v[4 * q + 0] = (t[0] * inv_rms) * g[0];
+        v[4 * q + 1] = (t[1] * inv_rms) * g[1];
+        v[4 * q + 2] = (t[2] * inv_rms) * g[2];
+        v[4 * q + 3] = (t[3] * inv_rms) * g[3];
       }
       xchunks_from_f32<XP>(v, xh[j], xl[XP == 2 ? j : 0]);
     }
+  } else {
+#pragma unroll
+    for (int j = 0; j < LG; ++j) {
+      const int c = (j * 64 + lane) % C;
+      if constexpr (XM == X_F16) {
+        const u32x4* xp = reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(a.x) +
+                                                         (size_t)bat * K + c * 32);
+        uint32_t xw[16];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const u32x4 t = xp[q];
+          xw[4 * q + 0] = t[0];
+          xw[4 * q + 1] = t[1];
+          xw[4 * q + 2] = t[2];
+          xw[4 * q + 3] = t[3];
+        }
+        xchunk_from_words(xw, xh[j]);
+      } else {
+        const f32x4* xp = reinterpret_cast<const f32x4*>(static_cast<const float*>(a.x) +
+                                                         (size_t)bat * K + c * 32);
+        float v[32];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+          const f32x4 t = xp[q];
+          v[4 * q + 0] = t[0];
+          v[4 * q + 1] = t[1];
+          v[4 * q + 2] = t[2];
+          v[4 * q + 3] = t[3];
+        }
+        xchunks_from_f32<XP>(v, xh[j], xl[XP == 2 ? j : 0]);
+      }
+    }
   }
 
-  // ---- stream row groups -----------------------------------------------------
-  const int NG = PAIR ? a.rows : a.rows / RG;
-  const int gw = blockIdx.x * 4 + wid;
-  const int nw = gridDim.x * 4;
+  // ---- stream row groups (software-pipelined: next batch in flight) -----------
   float best = -INFINITY;
   int besti = 0x7fffffff;
 
   for (int g0 = gw; g0 < NG; g0 += nw * U) {
-    u32x4 wv[U][LG];
-    uint32_t sv[U][LG];
+    u32x4 cw[U][LG];
+    uint32_t cs[U][LG];
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+      for (int j = 0; j < LG; ++j) {
+        cw[u][j] = wv[u][j];
+        cs[u][j] = sv[u][j];
+      }
+    if (g0 + nw * U < NG)
+      load_batch<K, U, PAIR>(g0 + nw * U, nw, NG, lane, w0, w1, w2, s0, s1, s2, e0, e1, wv, sv);
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int g = g0 + u * nw;
       if (g < NG) {
-        int seg = 0, local0 = g;
-        if constexpr (!PAIR) {
-          const int row0 = g * RG;
-          seg = (row0 < a.seg_end[0]) ? 0 : ((row0 < a.seg_end[1]) ? 1 : 2);
-          local0 = row0 - (seg == 0 ? 0 : a.seg_end[seg - 1]);
-        }
-#pragma unroll
-        for (int j = 0; j < LG; ++j) {
-          const int f = j * 64 + lane;
-          const int r = f / C, c = f % C;
-          const int sg = PAIR ? r : seg;
-          const int row = PAIR ? g : local0 + r;
-          const uint8_t* wp = a.w[sg] + (size_t)row * (K / 2) + c * 16;
-          const uint16_t* sp = a.s[sg] + (size_t)row * G + (c >> 1);
-          wv[u][j] = *reinterpret_cast<const u32x4*>(wp);
-          sv[u][j] = *sp;
-        }
-      }
-    }
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int g = g0 + u * nw;
-      if (g >= NG) break;
       float acc0 = 0.f, acc1 = 0.f;
 #pragma unroll
       for (int j = 0; j < LG; ++j) {
         const int r = (j * 64 + lane) / C;
         float p;
         if constexpr (XP == 2)
-          p = chunk_dot_hl(wv[u][j], xh[j], xl[j]);
+          p = chunk_dot_hl(cw[u][j], xh[j], xl[j]);
         else
-          p = chunk_dot(wv[u][j], xh[j]);
-        p *= scale_q2_14(sv[u][j]);
+          p = chunk_dot(cw[u][j], xh[j]);
+        p *= scale_q2_14(cs[u][j]);
         if (RG == 1 || r == 0)
           acc0 += p;
         else
@@ -236,6 +285,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(const GemvArgs a) {
           }
         }
       }
+      }  // g < NG
     }
   }
 
@@ -267,18 +317,20 @@ __global__ __launch_bounds__(256) void gemv_kernel(const GemvArgs a) {
         }
       part[2 * blockIdx.x] = bb;
       reinterpret_cast<int*>(part)[2 * blockIdx.x + 1] = bi;
-      __threadfence();
+      // release this thread's partial before counting in (agent scope)
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
       const int done = atomicAdd(a.counter, 1);
       s_last = (done == (int)gridDim.x - 1);
     }
     __syncthreads();
     if (s_last) {
-      __threadfence();
+      // acquire the partials released by every other block
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
       float bb = -INFINITY;
       int bi = 0x7fffffff;
       for (int i = threadIdx.x; i < (int)gridDim.x; i += 256) {
-        const float sc = __builtin_nontemporal_load(&part[2 * i]);
-        const int ix = __builtin_nontemporal_load(&reinterpret_cast<int*>(part)[2 * i + 1]);
+        const float sc = part[2 * i];
+        const int ix = reinterpret_cast<int*>(part)[2 * i + 1];
         if (arg_better(sc, ix, bb, bi)) {
           bb = sc;
           bi = ix;

@@ -180,3 +180,37 @@ def test_bad_position_is_reported_not_executed(dev, layer_setup):
                                            torch.tensor([[5]]), *[x[0] for x in common.layer_views(kv, 3)], 1, 16, 8,
                                            128, 2, cfg)
     assert e.value.code == -10
+
+
+@pytest.mark.parametrize("lengths", [[1], [63], [64], [65], [256], [257], [1000], [5, 300, 64, 777]])
+def test_attention_context_lengths_and_batch(dev, lengths):
+    """q4d_cached_attention over a batch whose sequences have their own
+    positions: chunk boundaries (64), group boundaries (4 x 64) and ragged
+    batches, against the oracle (common.py:192-228) per sequence."""
+    from llm_accelerator_amd._lib import Q4dModel
+    lib = _lib.load()
+    B, max_ctx = len(lengths), 1024
+    cfg = Qwen3Config()
+    kv = KVCache(cfg, 1, B, max_ctx, dev)
+    rng = np.random.default_rng(sum(lengths))
+    kv_host = rng.normal(size=(2, B, 8, max_ctx, 128)).astype(np.float16)
+    kv.data[0] = torch.from_numpy(kv_host).to(dev)
+    q = rng.normal(size=(B, 16, 128)).astype(np.float32)
+    m = Q4dModel(hidden_size=1024, intermediate_size=3072, num_layers=1, num_q_heads=16, num_kv_heads=8,
+                 head_dim=128, vocab_size=2, max_ctx=max_ctx, rms_norm_eps=1e-6, attn_scaling=128 ** -0.5)
+    nbytes = int(lib.q4d_workspace_bytes(ctypes.byref(m), B))
+    ws = torch.zeros(nbytes, dtype=torch.uint8, device=dev)
+    pos = torch.tensor([n - 1 for n in lengths], dtype=torch.int32, device=dev)
+    out = torch.empty(B, 2048, dtype=torch.float32, device=dev)
+    qd = torch.from_numpy(q).to(dev)
+    kvd = kv.descriptor()
+    check(lib.q4d_cached_attention(ctypes.byref(m), ctypes.byref(kvd), 0, qd.data_ptr(), pos.data_ptr(),
+                                   out.data_ptr(), 1, ws.data_ptr(), nbytes, current_stream()), "attention")
+    got = out.cpu().numpy().reshape(B, 16, 128)
+    for bi, n in enumerate(lengths):
+        k = kv_host[0, bi:bi + 1, :, :n].astype(np.float64)
+        v = kv_host[1, bi:bi + 1, :, :n].astype(np.float64)
+        ref, _ = o.manual_cached_attention(q[bi:bi + 1, :, None].astype(np.float64), o.manual_repeat_kv(k, 2),
+                                           o.manual_repeat_kv(v, 2), 128 ** -0.5)
+        mx, rel = report(f"attention T={n}", got[bi], ref[0, :, 0])
+        assert mx <= 2e-6 * max(1.0, float(np.abs(ref).max())) + 1e-6, (n, mx)
