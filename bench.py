@@ -49,6 +49,8 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--decode-gen", type=int, default=256)
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="also run a plain 256 MiB device copy (scales FETCH_SIZE/WRITE_SIZE counters)")
     return ap.parse_args()
 
 
@@ -215,6 +217,22 @@ def main():
         torch.cuda.synchronize()
         t_gen = time.perf_counter() - t0
         toks, _ = dec.history()
+        # LM head alone: final RMSNorm + 151936x1024 Q4 GEMV + argmax
+        lm_desc = fmodel.descriptor()
+        hid = torch.randn(1, 1024, generator=gen, device=dev)
+        lm_tok = torch.zeros(1, dtype=torch.int32, device=dev)
+        lm_score = torch.zeros(1, dtype=torch.float32, device=dev)
+        lws = M.Workspace(fmodel, 1)
+
+        def lm_head(i):
+            check(lib.q4d_lm_head_argmax(ctypes.byref(lm_desc), hid.data_ptr(), lm_tok.data_ptr(),
+                                         lm_score.data_ptr(), None, lws.ptr, lws.nbytes, st()), "lm_head")
+        g_lm = graph_of(lm_head, 10, torch)
+        g_lm.replay()
+        lm_us = time_graph(g_lm, 10, torch) / 10 * 1e3
+        lm_bytes = wb_lm = fmodel.lm_head.weight.nbytes + 4 * 1024
+        extras["lm_head"] = {"us": round(lm_us, 2), "bytes": wb_lm, "GBps": round(lm_bytes / lm_us / 1e3, 1)}
+        log(f"[bench] LM head: {json.dumps(extras['lm_head'])}")
         wb = fmodel.weight_bytes()
         avg_ctx = 64 + args.decode_gen / 2
         tok_bytes = wb["total"] + 2 * 2 * 1024 * avg_ctx * 28
@@ -228,6 +246,17 @@ def main():
         log(f"[bench] C3 decode: {json.dumps(extras['c3_decode'])}")
         del fmodel, dec
         torch.cuda.empty_cache()
+
+    if args.copy_calibration:
+        # a plain copy of known size: its FETCH_SIZE / WRITE_SIZE per dispatch
+        # converts the counters of the GEMV dispatches to bytes
+        src = torch.empty(256 << 20, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        extras["copy_calibration_bytes"] = 256 << 20
+        del src, dst
 
     cpu = None
     if not args.no_cpu and not args.no_extras:

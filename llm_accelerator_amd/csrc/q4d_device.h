@@ -91,6 +91,41 @@ __device__ __forceinline__ float scale_q2_14(uint32_t code) {
 }
 
 // ---------------------------------------------------------------- reductions
+// DPP lane movement (gfx9 DPP: quad_perm, row mirrors, row broadcasts).
+// Lanes whose DPP source is disabled by the row mask read 0.
+template <int CTRL, int ROW_MASK = 0xF>
+__device__ __forceinline__ float dpp_f(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, ROW_MASK,
+                                                                0xF, false));
+}
+constexpr int kDppQuadSwap1 = 0xB1;     // quad_perm [1,0,3,2]
+constexpr int kDppQuadSwap2 = 0x4E;     // quad_perm [2,3,0,1]
+constexpr int kDppRowHalfMirror = 0x141;
+constexpr int kDppRowMirror = 0x140;
+constexpr int kDppRowBcast15 = 0x142;   // lane 15 of each row -> next row
+constexpr int kDppRowBcast31 = 0x143;   // lane 31 -> rows 2 and 3
+
+// Sum over each 16-lane row; every lane of the row receives the row sum.
+__device__ __forceinline__ float row16_sum(float v) {
+  v += dpp_f<kDppQuadSwap1>(v);
+  v += dpp_f<kDppQuadSwap2>(v);
+  v += dpp_f<kDppRowHalfMirror>(v);
+  v += dpp_f<kDppRowMirror>(v);
+  return v;
+}
+
+// Sums of lanes 0-31 and 32-63: valid in lanes 16-31 and 48-63 respectively.
+__device__ __forceinline__ float half_wave_sum_dpp(float v) {
+  v = row16_sum(v);
+  return v + dpp_f<kDppRowBcast15, 0xA>(v);
+}
+
+// Sum of all 64 lanes, valid in lanes 48-63.
+__device__ __forceinline__ float wave_sum_dpp(float v) {
+  v = half_wave_sum_dpp(v);
+  return v + dpp_f<kDppRowBcast31, 0xC>(v);
+}
+
 __device__ __forceinline__ float shfl_xor_f(float v, int mask) {
   return __shfl_xor(v, mask, kWave);
 }
@@ -111,6 +146,14 @@ __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
   for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, shfl_xor_f(v, m));
   return v;
+}
+
+// Workgroup barrier for LDS exchange only: waits for this wave's LDS
+// operations, not for its outstanding global loads (which __syncthreads()
+// would drain), so prefetched weights stay in flight across it.
+__device__ __forceinline__ void block_sync_lds() {
+  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0), vmcnt/expcnt untouched
+  __builtin_amdgcn_s_barrier();
 }
 
 // Argmax order: higher score wins; equal scores -> lower index wins

@@ -112,7 +112,7 @@ __device__ __forceinline__ void load_batch(int gbase, int nw, int NG, int lane, 
 template <int K, int U, int XM, int XP, int EP, bool PAIR>
 __global__ __launch_bounds__(256) void gemv_kernel(const GemvArgs a) {
   using Gm = Geo<K>;
-  constexpr int C = Gm::C, RG = Gm::RG, LG = Gm::LG, G = Gm::G;
+  constexpr int C = Gm::C, RG = Gm::RG, LG = Gm::LG;
   static_assert(!PAIR || RG == 2, "row-pair epilogue needs two rows per group");
   const int lane = threadIdx.x & 63;
   const int wid = threadIdx.x >> 6;
@@ -137,41 +137,71 @@ __global__ __launch_bounds__(256) void gemv_kernel(const GemvArgs a) {
   const int gw = blockIdx.x * 4 + wid;
   const int nw = gridDim.x * 4;
 
-  // The first batch of weights is in flight while the activations are prepared.
+  // ---- activation loads go out first --------------------------------------
+  // vmcnt drains in issue order, so anything issued after the weight prefetch
+  // could only be waited for together with the weights.
+  f32x4 hreg = f32x4{0.f, 0.f, 0.f, 0.f};
+  f32x4 gam[XM == X_RMS ? LG : 1][8];
+  u32x4 xr16[XM == X_F16 ? LG : 1][4];
+  f32x4 xr32[XM == X_F32 ? LG : 1][8];
+  if constexpr (XM == X_RMS) {
+    static_assert(K / 4 <= 256, "RMS prologue stages one 16-byte vector per thread");
+    if (threadIdx.x < K / 4)
+      hreg = reinterpret_cast<const f32x4*>(static_cast<const float*>(a.x) + (size_t)bat * K)[threadIdx.x];
+#pragma unroll
+    for (int j = 0; j < LG; ++j) {
+      const int c = (j * 64 + lane) % C;
+#pragma unroll
+      for (int q = 0; q < 8; ++q) gam[j][q] = reinterpret_cast<const f32x4*>(a.gamma + c * 32)[q];
+    }
+  } else if constexpr (XM == X_F16) {
+#pragma unroll
+    for (int j = 0; j < LG; ++j) {
+      const int c = (j * 64 + lane) % C;
+      const u32x4* xp = reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(a.x) + (size_t)bat * K + c * 32);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) xr16[j][q] = xp[q];
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < LG; ++j) {
+      const int c = (j * 64 + lane) % C;
+      const f32x4* xp = reinterpret_cast<const f32x4*>(static_cast<const float*>(a.x) + (size_t)bat * K + c * 32);
+#pragma unroll
+      for (int q = 0; q < 8; ++q) xr32[j][q] = xp[q];
+    }
+  }
+
+  // ---- first batch of weights in flight while the activations are prepared ---
   u32x4 wv[U][LG];
   uint32_t sv[U][LG];
   load_batch<K, U, PAIR>(gw, nw, NG, lane, w0, w1, w2, s0, s1, s2, e0, e1, wv, sv);
 
-  // ---- activations for this lane's chunks ----------------------------------
   XChunk xh[LG];
   XChunk xl[XP == 2 ? LG : 1];
   if constexpr (XM == X_RMS) {
-    // stage the fp32 hidden vector in LDS with one 16-byte load per thread,
-    // reduce sum(x^2) in a fixed order (identical in every block)
-    const f32x4* hv = reinterpret_cast<const f32x4*>(static_cast<const float*>(a.x) + (size_t)bat * K);
+    // stage the fp32 hidden vector in LDS and reduce sum(x^2) in a fixed order
+    // (identical in every block); LDS-only barriers keep the weights in flight
     float ss = 0.f;
-#pragma unroll
-    for (int i = threadIdx.x; i < K / 4; i += 256) {
-      const f32x4 t = hv[i];
-      s_x[i] = t;
-      ss = fmaf(t[0], t[0], ss);
-      ss = fmaf(t[1], t[1], ss);
-      ss = fmaf(t[2], t[2], ss);
-      ss = fmaf(t[3], t[3], ss);
+    if (threadIdx.x < K / 4) {
+      s_x[threadIdx.x] = hreg;
+      ss = fmaf(hreg[0], hreg[0], ss);
+      ss = fmaf(hreg[1], hreg[1], ss);
+      ss = fmaf(hreg[2], hreg[2], ss);
+      ss = fmaf(hreg[3], hreg[3], ss);
     }
-    ss = wave_sum(ss);
-    if (lane == 0) s_red[wid] = ss;
-    __syncthreads();
+    ss = wave_sum_dpp(ss);
+    if (lane == 63) s_red[wid] = ss;
+    block_sync_lds();
     const float inv_rms = 1.0f / sqrtf(((s_red[0] + s_red[1]) + (s_red[2] + s_red[3])) / (float)K + a.eps);
 #pragma unroll
     for (int j = 0; j < LG; ++j) {
       const int c = (j * 64 + lane) % C;
-      const f32x4* gp = reinterpret_cast<const f32x4*>(a.gamma + c * 32);
       float v[32];
 #pragma unroll
       for (int q = 0; q < 8; ++q) {
         const f32x4 t = s_x[c * 8 + q];
-        const f32x4 g = gp[q];
+        const f32x4 g = gam[j][q];
         v[4 * q + 0] = (t[0] * inv_rms) * g[0];
         v[4 * q + 1] = (t[1] * inv_rms) * g[1];
         v[4 * q + 2] = (t[2] * inv_rms) * g[2];
@@ -179,37 +209,33 @@ __global__ __launch_bounds__(256) void gemv_kernel(const GemvArgs a) {
       }
       xchunks_from_f32<XP>(v, xh[j], xl[XP == 2 ? j : 0]);
     }
+  } else if constexpr (XM == X_F16) {
+#pragma unroll
+    for (int j = 0; j < LG; ++j) {
+      uint32_t xw[16];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const u32x4 t = xr16[j][q];
+        xw[4 * q + 0] = t[0];
+        xw[4 * q + 1] = t[1];
+        xw[4 * q + 2] = t[2];
+        xw[4 * q + 3] = t[3];
+      }
+      xchunk_from_words(xw, xh[j]);
+    }
   } else {
 #pragma unroll
     for (int j = 0; j < LG; ++j) {
-      const int c = (j * 64 + lane) % C;
-      if constexpr (XM == X_F16) {
-        const u32x4* xp = reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(a.x) +
-                                                         (size_t)bat * K + c * 32);
-        uint32_t xw[16];
+      float v[32];
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const u32x4 t = xp[q];
-          xw[4 * q + 0] = t[0];
-          xw[4 * q + 1] = t[1];
-          xw[4 * q + 2] = t[2];
-          xw[4 * q + 3] = t[3];
-        }
-        xchunk_from_words(xw, xh[j]);
-      } else {
-        const f32x4* xp = reinterpret_cast<const f32x4*>(static_cast<const float*>(a.x) +
-                                                         (size_t)bat * K + c * 32);
-        float v[32];
-#pragma unroll
-        for (int q = 0; q < 8; ++q) {
-          const f32x4 t = xp[q];
-          v[4 * q + 0] = t[0];
-          v[4 * q + 1] = t[1];
-          v[4 * q + 2] = t[2];
-          v[4 * q + 3] = t[3];
-        }
-        xchunks_from_f32<XP>(v, xh[j], xl[XP == 2 ? j : 0]);
+      for (int q = 0; q < 8; ++q) {
+        const f32x4 t = xr32[j][q];
+        v[4 * q + 0] = t[0];
+        v[4 * q + 1] = t[1];
+        v[4 * q + 2] = t[2];
+        v[4 * q + 3] = t[3];
       }
+      xchunks_from_f32<XP>(v, xh[j], xl[XP == 2 ? j : 0]);
     }
   }
 
@@ -248,25 +274,31 @@ __global__ __launch_bounds__(256) void gemv_kernel(const GemvArgs a) {
         else
           acc1 += p;
       }
+      // DPP reductions: lane 63 ends up with row g*RG (RG == 1) or, for
+      // RG == 2, lane 31 with row 2g and lane 63 with row 2g+1
       float v;
       if constexpr (RG == 1) {
-        v = wave_sum(acc0);
+        v = wave_sum_dpp(acc0);
       } else if constexpr (K == 1024) {
         // lanes 0-31 only hold row 0, lanes 32-63 only row 1
-        v = half_wave_sum(lane < 32 ? acc0 : acc1);
+        v = half_wave_sum_dpp(lane < 32 ? acc0 : acc1);
       } else {
-        const float keep = lane < 32 ? acc0 : acc1;
-        const float send = lane < 32 ? acc1 : acc0;
-        v = half_wave_sum(keep + shfl_xor_f(send, 32));
+        // both rows spread over all lanes: full-wave sums, then lane 31
+        // takes row 0 from lane 63's neighbourhood via a row broadcast
+        const float r0 = wave_sum_dpp(acc0);
+        const float r1 = wave_sum_dpp(acc1);
+        // the permute must run with every lane active: an inactive source
+        // lane reads as zero
+        const float r0_all = __shfl(r0, 63, kWave);
+        v = lane < 32 ? r0_all : r1;
       }
-      // lane 0 holds row g*RG, lane 32 holds row g*RG+1 (RG == 2)
-      const bool owner = (RG == 1) ? (lane == 0) : ((lane & 31) == 0);
+      const bool owner = (RG == 1) ? (lane == 63) : ((lane & 31) == 31);
       const int row = (RG == 1) ? g : (g * 2 + (lane >> 5));
       if constexpr (EP == EP_SWIGLU) {
-        const float up = __shfl(v, 32, kWave);
-        if (lane == 0) {
-          const float gate = v;
-          const float act = (gate / (1.0f + expf(-gate))) * up;
+        // lane 63 holds up; row_bcast31 brings the gate from lane 31
+        const float gate = dpp_f<kDppRowBcast31, 0xC>(v);
+        if (lane == 63) {
+          const float act = (gate / (1.0f + expf(-gate))) * v;
           static_cast<float*>(a.y)[(size_t)bat * a.rows + g] = act;
         }
       } else if (owner) {
@@ -366,12 +398,31 @@ __global__ __launch_bounds__(256) void gemv_kernel(const GemvArgs a) {
 }
 
 // ---------------------------------------------------------------------------
+// Blocks of one kernel instance that fit on the device at once (queried once
+// per instance); large GEMVs launch one resident wave set that loops, so the
+// per-block activation prologue is paid once per resident block.
+template <class F>
+static int resident_blocks(F kernel) {
+  static int cached = 0;
+  if (cached == 0) {
+    int dev = 0, cus = 0, per_cu = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, 256, 0) != hipSuccess || per_cu < 1)
+      return 1024;  // conservative fallback, recomputed next call
+    cached = cus * per_cu;
+  }
+  return cached;
+}
+
 template <int K, int U, int XM, int XP, int EP, bool PAIR>
 static int launch_inst(const GemvArgs& a, int max_blocks, hipStream_t stream) {
   using Gm = Geo<K>;
   const int NG = PAIR ? a.rows : a.rows / Gm::RG;
   int waves = (NG + U - 1) / U;
   int blocks = (waves + 3) / 4;
+  const int res = resident_blocks(gemv_kernel<K, U, XM, XP, EP, PAIR>);
+  if (blocks > res) blocks = res;
   if (blocks > max_blocks) blocks = max_blocks;
   if (blocks < 1) blocks = 1;
   dim3 grid(blocks, a.batch);
@@ -384,6 +435,8 @@ static int launch_u(const GemvArgs& a, hipStream_t stream) {
   if constexpr (EP == EP_ARGMAX) return launch_inst<K, 4, XM, XP, EP, PAIR>(a, kLmMaxBlocks, stream);
   const int rg = Geo<K>::RG;
   const int NG = PAIR ? a.rows : a.rows / rg;
+  // three chunks per lane: one row group per batch keeps VGPRs below 256
+  if constexpr (K == 3072) return launch_inst<K, 1, XM, XP, EP, PAIR>(a, 4096, stream);
   if (NG <= 16384) return launch_inst<K, 2, XM, XP, EP, PAIR>(a, 4096, stream);
   return launch_inst<K, 4, XM, XP, EP, PAIR>(a, 4096, stream);
 }
