@@ -156,9 +156,20 @@ def main():
     h, i_sz = 1024, 3072
     gate_up_bytes = 2 * (i_sz * h // 2 + 2 * i_sz * h // 64) + 2 * h + 2 * i_sz
     achieved = gate_up_bytes / (stage_us["gate_up"] * 1e-6) / 1e9
+    # HBM bytes per launch of this kernel, measured with rocprofv3 FETCH_SIZE /
+    # WRITE_SIZE (copy-calibrated) and committed under profiles/
+    traffic, traffic_src = None, None
+    tfile = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
+                         "decode_layer_ctx512_hbm_traffic.json")
+    if os.path.exists(tfile) and args.precision == 2:
+        with open(tfile) as f:
+            tj = json.load(f)
+        ent = tj["kernels"].get("void q4d::gemv_kernel<1024, 2, 2, 2, 3, true>")
+        if ent:
+            traffic, traffic_src = ent["total_bytes"], tj["source"]
     roofline = {"bound": "hbm", "kernel": "gemv_kernel<1024,2,X_RMS,*,EP_SWIGLU,pair> (post-norm + gate/up + SwiGLU)",
                 "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None,
+                "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": traffic, "traffic_source": traffic_src,
                 "bytes_per_launch": gate_up_bytes, "avg_launch_us": round(stage_us["gate_up"], 3)}
 
     extras = {"c2_resident_GBps": round(resident, 1), "c2_resident_us_per_step": round(res_ms * 1e3, 3),
