@@ -26,6 +26,9 @@
  *   q4d_linear           <- manual_linear_from_weight
  *                           (Qwen3-0.6B-Base/python_each_module/common.py:137-145)
  *                           and the integer Q4 GEMV contract (Source/Q4_FORMAT.md:155-190)
+ *   q4d_lm_head_argmax_batch <- q4d_lm_head_argmax per row of a batch
+ *   q4d_gemm             <- manual_linear_from_weight over many activation rows
+ *                           (x [B, S, K], common.py:137-145), for prefill and batched decode
  *   q4d_rms_norm         <- manual_rms_norm (common.py:129-134)
  *   q4d_qk_norm_rope     <- manual_rms_norm over heads + manual_rope_cos_sin +
  *                           manual_apply_rope (common.py:155-183, 258-268)
@@ -178,6 +181,21 @@ int q4d_embedding(const q4d_matrix_t* table, const int32_t* tokens, int32_t batc
 int q4d_lm_head_argmax(const q4d_model_t* model, const float* hidden, int32_t* out_token,
                        float* out_score, float* logits, void* ws, size_t ws_bytes, void* stream);
 
+/* Batched q4d_lm_head_argmax: final RMSNorm, LM head on MFMA (hidden rounded to fp16,
+ * Q4 tiles dequantised to fp16, fp32 accumulation) and a two-stage argmax per row
+ * (lowest index wins ties).  hidden fp32 [batch, hidden]; out_tokens int32 [batch];
+ * out_scores fp32 [batch]; logits optional fp32 [batch, vocab].  vocab % 128 == 0. */
+int q4d_lm_head_argmax_batch(const q4d_model_t* model, const float* hidden, int32_t batch,
+                             int32_t* out_tokens, float* out_scores, float* logits, void* ws,
+                             size_t ws_bytes, void* stream);
+
+/* y[m, :] = W x[m, :] for m < M on MFMA, for many activation rows sharing the weights
+ * (prefill, batched decode): x fp16 [M, cols]; y [M, rows] in y_dtype; if resid is not
+ * NULL, y (fp32) = resid + W x (resid may alias y).  Q4 tiles are dequantised to fp16
+ * (one rounding of q*scale) and accumulated in fp32.  rows % 128 == 0, cols % 64 == 0. */
+int q4d_gemm(const q4d_matrix_t* w, const uint16_t* x, int32_t M, void* y, int32_t y_dtype,
+             const float* resid, void* stream);
+
 /* ---- fused decode ---------------------------------------------------------- */
 /* One cached decoder layer (batch 1): hidden_out = layer(hidden_in); appends
  * K/V at positions[0] of the cache.  hidden_in and hidden_out may alias. */
@@ -203,6 +221,17 @@ int q4d_layer_stage(const q4d_model_t* model, int32_t layer, int32_t stage, cons
 int q4d_run_one_token(const q4d_model_t* model, const int32_t* tokens, const int32_t* positions,
                       const q4d_kv_cache_t* kv, int32_t* next_token, float* score, float* logits,
                       void* ws, size_t ws_bytes, void* stream);
+/* One decode step for `batch` independent sequences (batched decode): tokens[b] at
+ * positions[b] (device int32 [batch], each sequence its own position) through embedding,
+ * all layers (projections as MFMA GEMMs over the batch, GQA attention per sequence) and the
+ * LM head; writes next_tokens[b], scores[b] and, if logits is not NULL, logits
+ * [batch, vocab] (fp32).  Activations enter each projection as fp16.  The KV cache must
+ * have batch >= `batch`; the workspace is sized by q4d_workspace_bytes(model, batch).
+ * No counterpart in the reference (its decode is batch 1); per sequence it computes
+ * run_manual_one_token (10_validate_full_run_one_token.py:17-56). */
+int q4d_decode_batch(const q4d_model_t* model, const int32_t* tokens, const int32_t* positions,
+                     int32_t batch, const q4d_kv_cache_t* kv, int32_t* next_tokens, float* scores,
+                     float* logits, void* ws, size_t ws_bytes, void* stream);
 /* Advance a device-resident decode loop: tokens[0] = next_token[0], positions[0] += 1, and,
  * if hist_tokens is not NULL and *hist_count < hist_capacity, record next_token[0] and score[0]
  * at index *hist_count and increment it.  Lets a captured graph replay q4d_run_one_token

@@ -82,6 +82,10 @@ SIGNATURES = {
                           c_int32),
     "q4d_layer_stage": ([POINTER(Q4dModel), c_int32, c_int32, _P, _P, POINTER(Q4dKVCache), _P, _P, c_size_t, _P],
                         c_int32),
+    "q4d_lm_head_argmax_batch": ([POINTER(Q4dModel), _P, c_int32, _P, _P, _P, _P, c_size_t, _P], c_int32),
+    "q4d_gemm": ([POINTER(Q4dMatrix), _P, c_int32, _P, c_int32, _P, _P], c_int32),
+    "q4d_decode_batch": ([POINTER(Q4dModel), _P, _P, c_int32, POINTER(Q4dKVCache), _P, _P, _P, _P, c_size_t, _P],
+                         c_int32),
     "q4d_run_one_token": ([POINTER(Q4dModel), _P, _P, POINTER(Q4dKVCache), _P, _P, _P, _P, c_size_t, _P],
                           c_int32),
     "q4d_apply_rope": ([_P, _P, _P, _P, c_int32, c_int32, c_int32, _P], c_int32),

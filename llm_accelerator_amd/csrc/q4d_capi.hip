@@ -357,6 +357,164 @@ int q4d_decoder_layer(const q4d_model_t* model, int32_t layer, const float* hidd
   return run_layer(model, layer, hidden_in, hidden_out, kv, positions, ws, ws_layout(model, 1), as_stream(stream));
 }
 
+int q4d_gemm(const q4d_matrix_t* w, const uint16_t* x, int32_t M, void* y, int32_t y_dtype, const float* resid,
+             void* stream) {
+  if (!w) return Q4D_ERR_NULL;
+  int rc = check_matrix(w, w->rows, w->cols);
+  if (rc) return rc;
+  if (y_dtype != Q4D_F16 && y_dtype != Q4D_F32) return Q4D_ERR_DTYPE;
+  if (resid && y_dtype != Q4D_F32) return Q4D_ERR_DTYPE;
+  GemmArgs a;
+  memset(&a, 0, sizeof(a));
+  a.w[0] = w->w;
+  a.s[0] = w->s;
+  a.seg_end[0] = w->rows;
+  a.nseg = 1;
+  a.N = w->rows;
+  a.K = w->cols;
+  a.M = M;
+  a.x = x;
+  a.y = y;
+  a.ldy = w->rows;
+  a.resid = resid;
+  return launch_gemm(a, resid ? EP_RESID : (y_dtype == Q4D_F16 ? EP_F16 : EP_F32), false, as_stream(stream));
+}
+
+// Final RMSNorm (to fp16) + LM head GEMM with per-row argmax partials over
+// 128-column blocks + one wave per row reducing them.
+static int run_lm_head_batch(const q4d_model_t* model, const float* hidden, int batch, int32_t* next_tokens,
+                             float* scores, float* logits, void* ws, const WsLayout& W, hipStream_t st) {
+  const int H = model->hidden_size;
+  uint16_t* xh = ws_ptr<uint16_t>(ws, W.xh);
+  int rc = launch_rms_norm(hidden, model->final_norm, model->rms_norm_eps, batch, H, xh, Q4D_F16, st);
+  if (rc) return rc;
+  GemmArgs g;
+  memset(&g, 0, sizeof(g));
+  g.w[0] = model->embed_tokens.w;
+  g.s[0] = model->embed_tokens.s;
+  g.seg_end[0] = model->vocab_size;
+  g.nseg = 1;
+  g.N = model->vocab_size;
+  g.K = H;
+  g.M = batch;
+  g.x = xh;
+  g.logits = logits;
+  g.part_score = ws_ptr<float>(ws, W.row_score);
+  g.part_idx = ws_ptr<int>(ws, W.row_idx);
+  if ((rc = launch_gemm(g, EP_ARGMAX, false, st))) return rc;
+  return launch_argmax_rows(g.part_score, g.part_idx, model->vocab_size / 128, batch, next_tokens, scores, st);
+}
+
+int q4d_decode_batch(const q4d_model_t* model, const int32_t* tokens, const int32_t* positions, int32_t batch,
+                     const q4d_kv_cache_t* kv, int32_t* next_tokens, float* scores, float* logits, void* ws,
+                     size_t ws_bytes, void* stream) {
+  if (!tokens || !positions || !next_tokens || !scores) return Q4D_ERR_NULL;
+  int rc = check_model(model);
+  if (rc) return rc;
+  if (batch <= 0) return Q4D_ERR_SHAPE;
+  if ((rc = check_kv(kv, model, batch))) return rc;
+  if ((rc = check_ws(ws, ws_bytes, model, batch))) return rc;
+  if (model->vocab_size % 128) return Q4D_ERR_SHAPE;
+  const WsLayout W = ws_layout(model, batch);
+  hipStream_t st = as_stream(stream);
+  const int H = model->hidden_size, qd = model->num_q_heads * model->head_dim;
+  const int I = model->intermediate_size;
+  float* hidden = ws_ptr<float>(ws, W.hidden);
+  uint16_t* xh = ws_ptr<uint16_t>(ws, W.xh);
+  float* qkv = ws_ptr<float>(ws, W.qkv);
+  uint16_t* attn = ws_ptr<uint16_t>(ws, W.attn);
+  uint16_t* act = ws_ptr<uint16_t>(ws, W.act);
+  int32_t* status = ws_ptr<int32_t>(ws, W.status);
+  if ((rc = launch_embedding(&model->embed_tokens, tokens, batch, hidden, status, st))) return rc;
+  for (int l = 0; l < model->num_layers; ++l) {
+    const q4d_layer_t& L = model->layers[l];
+    if ((rc = launch_rms_norm(hidden, L.input_layernorm, model->rms_norm_eps, batch, H, xh, Q4D_F16, st)))
+      return rc;
+    GemmArgs g;
+    memset(&g, 0, sizeof(g));
+    g.w[0] = L.q_proj.w; g.s[0] = L.q_proj.s;
+    g.w[1] = L.k_proj.w; g.s[1] = L.k_proj.s;
+    g.w[2] = L.v_proj.w; g.s[2] = L.v_proj.s;
+    g.seg_end[0] = L.q_proj.rows;
+    g.seg_end[1] = g.seg_end[0] + L.k_proj.rows;
+    g.seg_end[2] = g.seg_end[1] + L.v_proj.rows;
+    g.nseg = 3;
+    g.N = g.seg_end[2];
+    g.K = H;
+    g.M = batch;
+    g.x = xh;
+    g.y = qkv;
+    g.ldy = g.N;
+    if ((rc = launch_gemm(g, EP_F32, false, st))) return rc;
+
+    AttnArgs t;
+    memset(&t, 0, sizeof(t));
+    t.fused = 1;
+    t.qkv = qkv;
+    t.q_gamma = L.q_norm;
+    t.k_gamma = L.k_norm;
+    t.eps = model->rms_norm_eps;
+    t.scaling = model->attn_scaling;
+    t.rope_cos = model->rope_cos;
+    t.rope_sin = model->rope_sin;
+    kv_planes(kv, l, &t.kcache, &t.vcache);
+    t.positions = positions;
+    t.batch = batch;
+    t.qh = model->num_q_heads;
+    t.kvh = model->num_kv_heads;
+    t.d = model->head_dim;
+    t.max_ctx = model->max_ctx;
+    t.nsplit_max = W.nsplit_max;
+    t.part_ml = ws_ptr<float>(ws, W.part_ml);
+    t.part_acc = ws_ptr<float>(ws, W.part_acc);
+    t.out = attn;
+    t.out_dtype = Q4D_F16;
+    t.status = status;
+    if ((rc = launch_attention(t, st))) return rc;
+
+    memset(&g, 0, sizeof(g));
+    g.w[0] = L.o_proj.w; g.s[0] = L.o_proj.s;
+    g.seg_end[0] = H;
+    g.nseg = 1;
+    g.N = H; g.K = qd; g.M = batch;
+    g.x = attn; g.y = hidden; g.ldy = H; g.resid = hidden;
+    if ((rc = launch_gemm(g, EP_RESID, false, st))) return rc;
+
+    if ((rc = launch_rms_norm(hidden, L.post_attention_layernorm, model->rms_norm_eps, batch, H, xh, Q4D_F16, st)))
+      return rc;
+    memset(&g, 0, sizeof(g));
+    g.w[0] = L.gate_proj.w; g.s[0] = L.gate_proj.s;
+    g.w[1] = L.up_proj.w;   g.s[1] = L.up_proj.s;
+    g.seg_end[0] = I; g.seg_end[1] = 2 * I;
+    g.nseg = 2;
+    g.N = I; g.K = H; g.M = batch;
+    g.x = xh; g.y = act; g.ldy = I;
+    if ((rc = launch_gemm(g, EP_SWIGLU, true, st))) return rc;
+
+    memset(&g, 0, sizeof(g));
+    g.w[0] = L.down_proj.w; g.s[0] = L.down_proj.s;
+    g.seg_end[0] = H;
+    g.nseg = 1;
+    g.N = H; g.K = I; g.M = batch;
+    g.x = act; g.y = hidden; g.ldy = H; g.resid = hidden;
+    if ((rc = launch_gemm(g, EP_RESID, false, st))) return rc;
+  }
+  return run_lm_head_batch(model, hidden, batch, next_tokens, scores, logits, ws, W, st);
+}
+
+int q4d_lm_head_argmax_batch(const q4d_model_t* model, const float* hidden, int32_t batch, int32_t* out_tokens,
+                             float* out_scores, float* logits, void* ws, size_t ws_bytes, void* stream) {
+  if (!hidden || !out_tokens || !out_scores) return Q4D_ERR_NULL;
+  if (!model) return Q4D_ERR_NULL;
+  int rc = check_matrix(&model->embed_tokens, model->vocab_size, model->hidden_size);
+  if (rc) return rc;
+  if (!model->final_norm) return Q4D_ERR_NULL;
+  if (batch <= 0 || model->vocab_size % 128) return Q4D_ERR_SHAPE;
+  if ((rc = check_ws(ws, ws_bytes, model, batch))) return rc;
+  return run_lm_head_batch(model, hidden, batch, out_tokens, out_scores, logits, ws, ws_layout(model, batch),
+                           as_stream(stream));
+}
+
 int q4d_layer_stage(const q4d_model_t* model, int32_t layer, int32_t stage, const float* hidden_in,
                     float* hidden_out, const q4d_kv_cache_t* kv, const int32_t* positions, void* ws,
                     size_t ws_bytes, void* stream) {

@@ -1,0 +1,368 @@
+// Q4 weight GEMM on MFMA for prefill and batched decode (gfx950).
+//
+//   Y[M, N] = X[M, K] . W[N, K]^T,   X fp16, W Q4 (reference Source/Q4_FORMAT.md)
+//
+// When many activation rows share each weight (prefill, batched decode), the
+// work becomes a dense contraction: each 128(N) x 64(K) Q4 tile (one scale
+// group per row) is dequantised once per block into LDS as fp16 and read by
+// every MFMA of the block.  Dequantisation uses packed fp16: after
+// v = w ^ 0x88888888 the nibble u = q + 8 placed in the low byte of an fp16
+// with exponent bits 0x6400 reads 1024 + u, so (0x6400|u) - 1032 = q exactly,
+// and q * scale is one correctly rounded fp16 multiply (the scale code is an
+// exact fp16 below 2048, i.e. scale < 0.125).
+//
+// Block tile 128 (M, BM = 128) or 64 (BM = 64) x 128 (N) x 64 (K), 256 threads
+// = 2 x 2 waves; each wave owns (BM/2) x 64 of the output as 16x16 tiles of
+// v_mfma_f32_16x16x32_f16 with fp32 accumulation.  LDS is double-buffered:
+// the global loads of the next K step are issued before the MFMAs of the
+// current one.
+//
+// Epilogues: fp32 / fp16 store, residual add (common.py:284,297), SwiGLU of a
+// gate/up row pair (common.py:293-295; the B tile then holds 64 gate rows and
+// the matching 64 up rows), and per-row argmax partials over the block's
+// columns for the batched LM head (lowest index wins ties).
+#include <math.h>
+
+#include "q4d_device.h"
+#include "q4d_internal.h"
+
+namespace q4d {
+
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+
+constexpr int kGemmBN = 128;
+constexpr int kGemmBK = 64;
+constexpr int kGemmPad = 8;  // fp16 elements of padding per LDS row
+constexpr int kGemmLds = kGemmBK + kGemmPad;
+
+// Dequantise 32 consecutive int4 (one 16-byte chunk) times `scale` to fp16,
+// in column order.
+__device__ __forceinline__ void dequant32(const u32x4 w, h2 scale2, uint32_t (&out)[16]) {
+  const h2 bias = make_h2((_Float16)1032.0f, (_Float16)1032.0f);
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    const uint32_t v = w[m] ^ 0x88888888u;
+    const uint32_t lo = v & 0x0F0F0F0Fu;         // nibbles 0, 2, 4, 6 in bytes 0..3
+    const uint32_t hi = (v >> 4) & 0x0F0F0F0Fu;  // nibbles 1, 3, 5, 7
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+      // fp16 pair (nibble 2p, nibble 2p+1): low byte of each half from lo / hi byte p
+      const uint32_t sel = (uint32_t)(p) | (0x0Cu << 8) | ((uint32_t)(4 + p) << 16) | (0x0Cu << 24);
+      const uint32_t pr = __builtin_amdgcn_perm(hi, lo, sel) | 0x64006400u;
+      const h2 q = __builtin_bit_cast(h2, pr) - bias;
+      out[4 * m + p] = __builtin_bit_cast(uint32_t, q * scale2);
+    }
+  }
+}
+
+struct GemmTileLoad {
+  u32x4 x[4];  // up to 4 x 16 B of X per thread
+  u32x4 w;     // 16 B of Q4 codes
+  uint32_t s;  // the row's scale code for this K step
+};
+
+// Segment pointers read with constant indices and selected in registers;
+// indexing a.w[] with a runtime segment number copies the argument block to
+// scratch memory.
+struct SegPtrs {
+  const uint8_t* w0;
+  const uint8_t* w1;
+  const uint8_t* w2;
+  const uint16_t* s0;
+  const uint16_t* s1;
+  const uint16_t* s2;
+  int e0, e1;
+};
+
+__device__ __forceinline__ SegPtrs seg_ptrs(const GemmArgs& a) {
+  return SegPtrs{a.w[0], a.w[1], a.w[2], a.s[0], a.s[1], a.s[2], a.seg_end[0], a.seg_end[1]};
+}
+
+template <int BM, bool PAIR>
+__device__ __forceinline__ void gemm_load(const GemmArgs& a, const SegPtrs& P, int m0, int nblk, int k0, int t,
+                                          GemmTileLoad& L) {
+  // X: BM x 64 fp16 = BM * 8 chunks of 16 B
+#pragma unroll
+  for (int i = 0; i < BM * 8 / 256; ++i) {
+    const int c = t + 256 * i;
+    const int row = c >> 3, seg = c & 7;
+    const int m = m0 + row;
+    if (m < a.M)
+      L.x[i] = *reinterpret_cast<const u32x4*>(a.x + (size_t)m * a.K + k0 + seg * 8);
+    else
+      L.x[i] = u32x4{0u, 0u, 0u, 0u};
+  }
+  // W: 128 rows x 32 B; thread t -> row t/2, half t%2
+  const int r = t >> 1, half = t & 1;
+  const uint8_t* wb;
+  const uint16_t* sb;
+  int grow;
+  if (PAIR) {
+    const int n0 = nblk * 64;
+    const int sg = r >> 6;
+    grow = n0 + (r & 63);
+    wb = sg == 0 ? P.w0 : P.w1;
+    sb = sg == 0 ? P.s0 : P.s1;
+  } else {
+    const int row = nblk * kGemmBN + r;
+    if (row < P.e0) {
+      grow = row;
+      wb = P.w0;
+      sb = P.s0;
+    } else if (row < P.e1) {
+      grow = row - P.e0;
+      wb = P.w1;
+      sb = P.s1;
+    } else {
+      grow = row - P.e1;
+      wb = P.w2;
+      sb = P.s2;
+    }
+  }
+  L.w = *reinterpret_cast<const u32x4*>(wb + (size_t)grow * (a.K / 2) + k0 / 2 + half * 16);
+  L.s = sb[(size_t)grow * (a.K / 64) + k0 / 64];
+}
+
+template <int BM>
+__device__ __forceinline__ void gemm_store_lds(_Float16 (*As)[kGemmLds], _Float16 (*Bs)[kGemmLds], int t,
+                                               const GemmTileLoad& L) {
+#pragma unroll
+  for (int i = 0; i < BM * 8 / 256; ++i) {
+    const int c = t + 256 * i;
+    *reinterpret_cast<u32x4*>(&As[c >> 3][(c & 7) * 8]) = L.x[i];
+  }
+  const int r = t >> 1, half = t & 1;
+  const _Float16 sc = (_Float16)((float)L.s * (1.0f / 16384.0f));
+  uint32_t out[16];
+  dequant32(L.w, make_h2(sc, sc), out);
+  u32x4* dst = reinterpret_cast<u32x4*>(&Bs[r][half * 32]);
+#pragma unroll
+  for (int q = 0; q < 4; ++q) dst[q] = u32x4{out[4 * q], out[4 * q + 1], out[4 * q + 2], out[4 * q + 3]};
+}
+
+template <int BM, int EP, bool PAIR>
+__global__ __launch_bounds__(256) void q4_gemm_kernel(const GemmArgs a) {
+  constexpr int WM = BM / 2;       // rows per wave
+  constexpr int MI = WM / 16;      // 16-row MFMA tiles per wave
+  constexpr int NI = 4;            // 16-col MFMA tiles per wave (64 columns)
+  __shared__ _Float16 As[2][BM][kGemmLds];
+  __shared__ _Float16 Bs[2][kGemmBN][kGemmLds];
+  __shared__ float s_best[2][BM];
+  __shared__ int s_bidx[2][BM];
+
+  const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+  const int wm = (w >> 1) * WM, wn = (w & 1);
+  const int nblk = blockIdx.x, m0 = blockIdx.y * BM;
+  const int nk = a.K / kGemmBK;
+
+  f32x4 acc[MI][NI];
+#pragma unroll
+  for (int i = 0; i < MI; ++i)
+#pragma unroll
+    for (int j = 0; j < NI; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  // B-tile rows read by this wave's four 16-col tiles
+  int brow[NI];
+#pragma unroll
+  for (int j = 0; j < NI; ++j)
+    brow[j] = PAIR ? ((j < 2) ? (32 * wn + 16 * j) : (64 + 32 * wn + 16 * (j - 2))) : (64 * wn + 16 * j);
+
+  const SegPtrs P = seg_ptrs(a);
+  GemmTileLoad L;
+  gemm_load<BM, PAIR>(a, P, m0, nblk, 0, t, L);
+  gemm_store_lds<BM>(As[0], Bs[0], t, L);
+  __syncthreads();
+
+  for (int ks = 0; ks < nk; ++ks) {
+    const int buf = ks & 1;
+    if (ks + 1 < nk) gemm_load<BM, PAIR>(a, P, m0, nblk, (ks + 1) * kGemmBK, t, L);
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk) {
+      const int kc = kk * 32 + (lane >> 4) * 8;
+      h8 bf[NI];
+#pragma unroll
+      for (int j = 0; j < NI; ++j) bf[j] = *reinterpret_cast<const h8*>(&Bs[buf][brow[j] + (lane & 15)][kc]);
+#pragma unroll
+      for (int i = 0; i < MI; ++i) {
+        const h8 af = *reinterpret_cast<const h8*>(&As[buf][wm + 16 * i + (lane & 15)][kc]);
+#pragma unroll
+        for (int j = 0; j < NI; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, bf[j], acc[i][j], 0, 0, 0);
+      }
+    }
+    if (ks + 1 < nk) gemm_store_lds<BM>(As[buf ^ 1], Bs[buf ^ 1], t, L);
+    __syncthreads();
+  }
+
+  // ---- epilogue: lane holds rows (lane/16)*4 + r of each 16x16 tile, column lane%16
+  const int cl = lane & 15, rq = (lane >> 4) * 4;
+  if constexpr (EP == EP_SWIGLU) {
+#pragma unroll
+    for (int i = 0; i < MI; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int n = nblk * 64 + 32 * wn + 16 * j + cl;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int m = m0 + wm + 16 * i + rq + r;
+          if (m < a.M) {
+            const float g = acc[i][j][r], u = acc[i][j + 2][r];
+            const float act = (g / (1.0f + expf(-g))) * u;
+            static_cast<_Float16*>(a.y)[(size_t)m * a.ldy + n] = (_Float16)act;
+          }
+        }
+      }
+  } else if constexpr (EP == EP_ARGMAX) {
+    // per row: best (score, column) over this wave's 64 columns, then over the block's two N-waves
+#pragma unroll
+    for (int i = 0; i < MI; ++i)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int lrow = wm + 16 * i + rq + r;
+        float bs = -INFINITY;
+        int bi = 0x7fffffff;
+#pragma unroll
+        for (int j = 0; j < NI; ++j) {
+          const int n = nblk * kGemmBN + 64 * wn + 16 * j + cl;
+          const float v = acc[i][j][r];
+          if (a.logits && m0 + lrow < a.M) a.logits[(size_t)(m0 + lrow) * a.N + n] = v;
+          if (arg_better(v, n, bs, bi)) {
+            bs = v;
+            bi = n;
+          }
+        }
+        // the 16 lanes sharing this row differ in lane & 15
+#pragma unroll
+        for (int msk = 8; msk >= 1; msk >>= 1) {
+          const float os = shfl_xor_f(bs, msk);
+          const int oi = __shfl_xor(bi, msk, kWave);
+          if (arg_better(os, oi, bs, bi)) {
+            bs = os;
+            bi = oi;
+          }
+        }
+        if (cl == 0) {
+          s_best[wn][lrow] = bs;
+          s_bidx[wn][lrow] = bi;
+        }
+      }
+    __syncthreads();
+    for (int lr = t; lr < BM; lr += 256) {
+      const int m = m0 + lr;
+      if (m < a.M) {
+        float bs = s_best[0][lr];
+        int bi = s_bidx[0][lr];
+        if (arg_better(s_best[1][lr], s_bidx[1][lr], bs, bi)) {
+          bs = s_best[1][lr];
+          bi = s_bidx[1][lr];
+        }
+        a.part_score[(size_t)m * gridDim.x + nblk] = bs;
+        a.part_idx[(size_t)m * gridDim.x + nblk] = bi;
+      }
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < MI; ++i)
+#pragma unroll
+      for (int j = 0; j < NI; ++j) {
+        const int n = nblk * kGemmBN + 64 * wn + 16 * j + cl;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int m = m0 + wm + 16 * i + rq + r;
+          if (m < a.M) {
+            const size_t o = (size_t)m * a.ldy + n;
+            const float v = acc[i][j][r];
+            if constexpr (EP == EP_F16)
+              static_cast<_Float16*>(a.y)[o] = (_Float16)v;
+            else if constexpr (EP == EP_RESID)
+              static_cast<float*>(a.y)[o] = a.resid[o] + v;
+            else
+              static_cast<float*>(a.y)[o] = v;
+          }
+        }
+      }
+  }
+}
+
+// Row-wise reduction of the argmax partials: one wave per activation row.
+__global__ __launch_bounds__(64) void argmax_rows_kernel(const float* part_score, const int* part_idx, int nparts,
+                                                         int M, int32_t* out_token, float* out_score) {
+  const int m = blockIdx.x, lane = threadIdx.x;
+  if (m >= M) return;
+  float bs = -INFINITY;
+  int bi = 0x7fffffff;
+  for (int i = lane; i < nparts; i += 64) {
+    const float s = part_score[(size_t)m * nparts + i];
+    const int ix = part_idx[(size_t)m * nparts + i];
+    if (arg_better(s, ix, bs, bi)) {
+      bs = s;
+      bi = ix;
+    }
+  }
+#pragma unroll
+  for (int msk = 32; msk >= 1; msk >>= 1) {
+    const float os = shfl_xor_f(bs, msk);
+    const int oi = __shfl_xor(bi, msk, kWave);
+    if (arg_better(os, oi, bs, bi)) {
+      bs = os;
+      bi = oi;
+    }
+  }
+  if (lane == 0) {
+    out_token[m] = bi;
+    out_score[m] = bs;
+  }
+}
+
+template <int BM, int EP, bool PAIR>
+static int launch_gemm_inst(const GemmArgs& a, hipStream_t st) {
+  const int nblk = PAIR ? a.N / 64 : a.N / kGemmBN;
+  dim3 grid(nblk, (a.M + BM - 1) / BM);
+  hipLaunchKernelGGL((q4_gemm_kernel<BM, EP, PAIR>), grid, dim3(256), 0, st, a);
+  return check_launch();
+}
+
+template <int BM>
+static int launch_gemm_bm(const GemmArgs& a, int ep, bool pair, hipStream_t st) {
+  if (pair) return ep == EP_SWIGLU ? launch_gemm_inst<BM, EP_SWIGLU, true>(a, st) : Q4D_ERR_SHAPE;
+  switch (ep) {
+    case EP_F32: return launch_gemm_inst<BM, EP_F32, false>(a, st);
+    case EP_F16: return launch_gemm_inst<BM, EP_F16, false>(a, st);
+    case EP_RESID: return launch_gemm_inst<BM, EP_RESID, false>(a, st);
+    case EP_ARGMAX: return launch_gemm_inst<BM, EP_ARGMAX, false>(a, st);
+    default: return Q4D_ERR_SHAPE;
+  }
+}
+
+int launch_gemm(const GemmArgs& a, int ep, bool pair, hipStream_t st) {
+  if (a.M <= 0 || a.K <= 0 || a.K % kGemmBK || a.N <= 0) return Q4D_ERR_SHAPE;
+  if (a.nseg < 1 || a.nseg > 3) return Q4D_ERR_SHAPE;
+  if (pair) {
+    if (a.nseg != 2 || a.N % 64) return Q4D_ERR_SHAPE;
+  } else {
+    if (a.N % kGemmBN || a.seg_end[a.nseg - 1] != a.N) return Q4D_ERR_SHAPE;
+    for (int i = 0; i < a.nseg; ++i)
+      if (a.seg_end[i] % kGemmBN) return Q4D_ERR_SHAPE;
+  }
+  for (int i = 0; i < a.nseg; ++i) {
+    if (!a.w[i] || !a.s[i]) return Q4D_ERR_NULL;
+    if (!aligned(a.w[i], 16) || !aligned(a.s[i], 2)) return Q4D_ERR_BAD_ADDR;
+  }
+  if (!a.x || !aligned(a.x, 16)) return a.x ? Q4D_ERR_BAD_ADDR : Q4D_ERR_NULL;
+  if (ep == EP_ARGMAX) {
+    if (!a.part_score || !a.part_idx) return Q4D_ERR_NULL;
+  } else if (!a.y) {
+    return Q4D_ERR_NULL;
+  }
+  if (ep == EP_RESID && !a.resid) return Q4D_ERR_NULL;
+  // small M (batched decode) uses 64-row tiles
+  return a.M <= 64 ? launch_gemm_bm<64>(a, ep, pair, st) : launch_gemm_bm<128>(a, ep, pair, st);
+}
+
+int launch_argmax_rows(const float* part_score, const int* part_idx, int nparts, int M, int32_t* out_token,
+                       float* out_score, hipStream_t st) {
+  hipLaunchKernelGGL(argmax_rows_kernel, dim3(M), dim3(64), 0, st, part_score, part_idx, nparts, M, out_token,
+                     out_score);
+  return check_launch();
+}
+
+}  // namespace q4d

@@ -28,6 +28,9 @@ struct WsLayout {
   size_t part_ml;    // f32 [batch, qh, nsplit, 2]   split max / sum
   size_t part_acc;   // f32 [batch, qh, nsplit, d]   split partial outputs
   size_t lm_part;    // {f32 score, i32 idx}[kLmMaxBlocks]
+  size_t xh;         // f16 [batch, max(hidden, qh*d, intermediate)]  MFMA-path activations
+  size_t row_score;  // f32 [batch, vocab/128]  batched LM-head argmax partials
+  size_t row_idx;    // i32 [batch, vocab/128]
   size_t total;
   int nsplit_max;
   int lm_counter_index;  // index into counters
@@ -50,6 +53,13 @@ inline WsLayout ws_layout(const q4d_model_t* m, int batch) {
   L.part_ml = o;  o = align_up(o + (size_t)batch * qh * L.nsplit_max * 2 * 4, A);
   L.part_acc = o; o = align_up(o + (size_t)batch * qh * L.nsplit_max * d * 4, A);
   L.lm_part = o;  o = align_up(o + (size_t)kLmMaxBlocks * 8, A);
+  int wmax = m->hidden_size;
+  if (qh * d > wmax) wmax = qh * d;
+  if (m->intermediate_size > wmax) wmax = m->intermediate_size;
+  const size_t nparts = (size_t)(m->vocab_size + 127) / 128;
+  L.xh = o;        o = align_up(o + (size_t)batch * wmax * 2, A);
+  L.row_score = o; o = align_up(o + (size_t)batch * nparts * 4, A);
+  L.row_idx = o;   o = align_up(o + (size_t)batch * nparts * 4, A);
   L.total = o;
   return L;
 }
@@ -135,6 +145,27 @@ struct AttnArgs {
   int32_t* status;
 };
 int launch_attention(const AttnArgs& a, hipStream_t stream);
+
+// ---- Q4 GEMM on MFMA (prefill / batched decode) ------------------------------
+struct GemmArgs {
+  const uint8_t* w[3];
+  const uint16_t* s[3];
+  int seg_end[3];
+  int nseg;
+  int N;               // output columns (PAIR: rows of each of gate / up)
+  int K;
+  int M;               // activation rows
+  const uint16_t* x;   // fp16 [M, K]
+  void* y;             // output [M, ldy]
+  int ldy;
+  const float* resid;  // EP_RESID: y = resid + X W^T (fp32, [M, ldy])
+  float* logits;       // EP_ARGMAX: optional [M, N]
+  float* part_score;   // EP_ARGMAX: [M, N/128]
+  int* part_idx;
+};
+int launch_gemm(const GemmArgs& a, int ep, bool pair, hipStream_t st);
+int launch_argmax_rows(const float* part_score, const int* part_idx, int nparts, int M, int32_t* out_token,
+                       float* out_score, hipStream_t st);
 
 int launch_fill_i32(int32_t* p, int32_t v, size_t n, hipStream_t stream);
 int launch_advance(int32_t* tokens, int32_t* positions, const int32_t* next_token, const float* score,

@@ -130,3 +130,48 @@ def greedy_generate(model: Q4ForCausalLM, prompt: list[int], max_new_tokens: int
     dec.generate(max_new_tokens - 1)
     torch.cuda.synchronize()
     return dec.history()
+
+
+class BatchedDecoder:
+    """One decode step for many independent sequences at once (q4d_decode_batch).
+
+    Every sequence has its own cache slot and position; per sequence the step
+    is ``run_manual_one_token`` (``10_validate_full_run_one_token.py:17-56``).
+    The projections and the LM head run as MFMA GEMMs over the batch, so the
+    weights are read once per step for all sequences.
+    """
+
+    def __init__(self, model: Q4ForCausalLM, batch: int, cache: KVCache | None = None):
+        dev = model.device
+        self.model, self.batch = model, batch
+        self.kv = cache if cache is not None else KVCache(model.config, len(model.model.layers), batch,
+                                                          model.max_ctx, dev)
+        if self.kv.batch < batch:
+            raise ValueError(f"cache holds {self.kv.batch} sequences, need {batch}")
+        self.ws = Workspace(model, batch)
+        self.next_tok = torch.zeros(batch, dtype=torch.int32, device=dev)
+        self.score = torch.zeros(batch, dtype=torch.float32, device=dev)
+        self._desc = model.descriptor()
+        self._kvd = self.kv.descriptor()
+
+    def step(self, tokens: torch.Tensor, positions: torch.Tensor,
+             logits: torch.Tensor | None = None) -> tuple[torch.Tensor, torch.Tensor]:
+        """tokens, positions: device int32 [batch].  Appends K/V at each
+        sequence's position and returns (next tokens, winning logits)."""
+        for t, name in ((tokens, "tokens"), (positions, "positions")):
+            if t.dtype != torch.int32 or t.numel() != self.batch or not t.is_cuda or not t.is_contiguous():
+                raise ValueError(f"{name} must be a contiguous device int32 tensor of {self.batch} elements")
+        if logits is not None and (logits.dtype != torch.float32 or
+                                   logits.numel() != self.batch * self.model.config.vocab_size):
+            raise ValueError("logits must be fp32 [batch, vocab]")
+        check(_lib.load().q4d_decode_batch(ctypes.byref(self._desc), tokens.data_ptr(), positions.data_ptr(),
+                                           self.batch, ctypes.byref(self._kvd), self.next_tok.data_ptr(),
+                                           self.score.data_ptr(), logits.data_ptr() if logits is not None else None,
+                                           self.ws.ptr, self.ws.nbytes, current_stream()), "q4d_decode_batch")
+        return self.next_tok, self.score
+
+    def status(self) -> int:
+        out = ctypes.c_int32(0)
+        check(_lib.load().q4d_read_status(self.ws.ptr, self.ws.nbytes, ctypes.byref(self._desc), self.batch,
+                                          ctypes.byref(out), current_stream()), "q4d_read_status")
+        return out.value

@@ -113,6 +113,36 @@ def test_model_validation_codes(lib):
                                  None) == -7
 
 
+def test_batched_entry_validation_codes(lib):
+    arr = _layers(2)
+    m = _model(arr)
+    kv = Q4dKVCache(data=FAKE, num_layers=2, batch=2, num_kv_heads=8, max_ctx=512, head_dim=128)
+    # cache holds 2 sequences, 4 requested
+    assert lib.q4d_decode_batch(ctypes.byref(m), FAKE, FAKE, 4, ctypes.byref(kv), FAKE, FAKE, None, FAKE, 1 << 30,
+                                None) == -9
+    # workspace too small for the batch
+    assert lib.q4d_decode_batch(ctypes.byref(m), FAKE, FAKE, 2, ctypes.byref(kv), FAKE, FAKE, None, FAKE, 4096,
+                                None) == -9
+    assert lib.q4d_decode_batch(ctypes.byref(m), FAKE, FAKE, 0, ctypes.byref(kv), FAKE, FAKE, None, FAKE, 1 << 30,
+                                None) == -11
+    assert lib.q4d_decode_batch(ctypes.byref(m), None, FAKE, 2, ctypes.byref(kv), FAKE, FAKE, None, FAKE, 1 << 30,
+                                None) == -7
+    # vocabulary not a multiple of the 128-column GEMM tile
+    m2 = _model(arr, vocab_size=1000)
+    m2.embed_tokens = Q4dMatrix(FAKE, FAKE, 1000, 1024)
+    assert lib.q4d_lm_head_argmax_batch(ctypes.byref(m2), FAKE, 2, FAKE, FAKE, None, FAKE, 1 << 30, None) == -11
+    # GEMM shapes: rows % 128, cols % 64, dtype
+    w = Q4dMatrix(FAKE, FAKE, 200, 1024)
+    assert lib.q4d_gemm(ctypes.byref(w), FAKE, 4, FAKE, 1, None, None) == -11
+    w = Q4dMatrix(FAKE, FAKE, 256, 1000)
+    assert lib.q4d_gemm(ctypes.byref(w), FAKE, 4, FAKE, 1, None, None) != 0
+    w = Q4dMatrix(FAKE, FAKE, 256, 1024)
+    assert lib.q4d_gemm(ctypes.byref(w), FAKE, 4, FAKE, 7, None, None) == -13
+    assert lib.q4d_gemm(ctypes.byref(w), FAKE, 4, FAKE, 0, FAKE, None) == -13  # resid needs fp32 y
+    assert lib.q4d_gemm(ctypes.byref(w), FAKE, 0, FAKE, 1, None, None) == -11
+    assert lib.q4d_gemm(ctypes.byref(w), FAKE + 2, 4, FAKE, 1, None, None) == -4
+
+
 def test_activation_precision_setter(lib):
     assert lib.q4d_set_activation_precision(3) == -13
     assert lib.q4d_set_activation_precision(2) == 0

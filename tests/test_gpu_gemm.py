@@ -1,0 +1,228 @@
+"""MFMA Q4 GEMM (prefill / batched decode path) on the GPU vs the oracle.
+
+The GEMM multiplies fp16 activations by Q4 tiles dequantised to fp16
+(W16 = fp16(q * fp16(code / 2^14))) with fp32 accumulation.
+
+Tolerances (stated):
+- integer-exact cases (|q * code| < 2^11, small-integer x) are exact in every
+  step, so the output must equal the float64 product bit for bit; this pins
+  the MFMA operand layout, the nibble order and the scale indexing;
+- real Qwen3 weights (the reference's exported gate/down projections) against
+  the float64 product with the same fp16 operands: |err| <= 2^-16 * sum|x w|
+  (fp32 accumulation only); against the exact Q4 weights:
+  |err| <= 2^-10 * sum|x w| (two fp16 roundings of each weight);
+- argmax indices must be bit-exact, lowest index on ties;
+- batched decode (all layers, fp16 activations into every projection) against
+  the oracle run per sequence: logits max-abs <= 5e-3 * max|ref|, next tokens
+  identical unless the oracle's top-2 gap is within the measured error.
+"""
+
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+import oracle as o
+from gpu_helpers import abs_dot_bound, head_model, q4, report
+from llm_accelerator_amd import _lib
+from llm_accelerator_amd._lib import Q4D_F16, Q4D_F32, check
+from llm_accelerator_amd.decode import BatchedDecoder
+from llm_accelerator_amd.model import KVCache, Qwen3Config, build_model, current_stream, random_host_weights
+
+pytestmark = pytest.mark.gpu
+
+
+def gemm(w, x: torch.Tensor, y_dtype=Q4D_F32, resid: torch.Tensor | None = None) -> torch.Tensor:
+    rows, cols = w.shape
+    M = x.shape[0]
+    assert x.dtype == torch.float16 and x.shape[1] == cols and x.is_contiguous()
+    y = torch.empty((M, rows), dtype=torch.float16 if y_dtype == Q4D_F16 else torch.float32, device=x.device)
+    desc = w.descriptor()
+    check(_lib.load().q4d_gemm(ctypes.byref(desc), x.data_ptr(), M, y.data_ptr(), y_dtype,
+                               resid.data_ptr() if resid is not None else None, current_stream()), "q4d_gemm")
+    torch.cuda.synchronize()
+    return y
+
+
+def exact_case(rng, N, K, M):
+    q = rng.integers(-8, 8, size=(N, K))
+    packed = o.pack_signed_int4(q)
+    scale = rng.integers(1, 128, size=(N, K // 64)).astype(np.uint16)
+    x = rng.integers(-4, 5, size=(M, K)).astype(np.float16)
+    W = o.dequantize_q4(packed, scale, np.float64)
+    ref = x.astype(np.float64) @ W.T
+    # every partial sum is a multiple of 2^-14 below 2^10: exact in fp32
+    assert (np.abs(x.astype(np.float64)) @ np.abs(W).T).max() < 1024
+    return packed, scale, x, ref
+
+
+def w16_of(packed, scale, K):
+    q = o.unpack_signed_int4(packed, K).astype(np.float16)
+    s16 = (scale.astype(np.float64) / 16384.0).astype(np.float16)
+    return (q * np.repeat(s16, 64, axis=1)).astype(np.float16)  # fp16 product, one rounding
+
+
+@pytest.mark.parametrize("N,K", [(256, 1024), (128, 3072), (384, 2048)])
+@pytest.mark.parametrize("M", [1, 7, 64, 65, 130, 256])
+def test_gemm_integer_exact(dev, N, K, M):
+    rng = np.random.default_rng(N * 7 + K + M)
+    packed, scale, x, ref = exact_case(rng, N, K, M)
+    print(f"[gemm exact] M={M} N={N} K={K}", flush=True)
+    y = gemm(q4(packed, scale), torch.from_numpy(x).to(dev)).cpu().numpy()
+    np.testing.assert_array_equal(y, ref.astype(np.float32))
+
+
+def test_gemm_epilogues_exact(dev):
+    rng = np.random.default_rng(11)
+    packed, scale, x, ref = exact_case(rng, 256, 1024, 70)
+    w = q4(packed, scale)
+    xd = torch.from_numpy(x).to(dev)
+    y16 = gemm(w, xd, Q4D_F16).cpu().numpy()
+    np.testing.assert_array_equal(y16, ref.astype(np.float32).astype(np.float16))
+    resid = rng.normal(size=ref.shape).astype(np.float32)
+    r = torch.from_numpy(resid).to(dev)
+    y = gemm(w, xd, Q4D_F32, resid=r).cpu().numpy()
+    np.testing.assert_array_equal(y, resid + ref.astype(np.float32))
+    # in place: y aliases resid (the decoder's residual stream)
+    desc = w.descriptor()
+    check(_lib.load().q4d_gemm(ctypes.byref(desc), xd.data_ptr(), 70, r.data_ptr(), Q4D_F32, r.data_ptr(),
+                               current_stream()), "q4d_gemm")
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(r.cpu().numpy(), resid + ref.astype(np.float32))
+
+
+@pytest.mark.parametrize("name,M", [("mlp_gate_proj_real", 64), ("mlp_down_proj_real", 33)])
+def test_gemm_real_weights(dev, golden, name, M):
+    f = golden(name)
+    packed, scale = f["weight_packed"], f["scale_q2_14"]
+    N, K = packed.shape[0], packed.shape[1] * 2
+    rng = np.random.default_rng(5)
+    x = np.empty((M, K), dtype=np.float16)
+    x[0] = (f["activation"] / 4096.0).astype(np.float16)  # the exported Q12.12 activation
+    x[1:] = rng.normal(size=(M - 1, K)).astype(np.float16)
+    y = gemm(q4(packed, scale), torch.from_numpy(x).to(dev)).cpu().numpy().astype(np.float64)
+    W16 = w16_of(packed, scale, K).astype(np.float64)
+    ref16 = x.astype(np.float64) @ W16.T
+    Wex = o.dequantize_q4(packed, scale, np.float64)
+    ref = x.astype(np.float64) @ Wex.T
+    bound = np.abs(x.astype(np.float64)) @ np.abs(Wex).T
+    report(f"{name} vs fp16-operand product", y, ref16)
+    report(f"{name} vs exact Q4 product", y, ref)
+    assert np.all(np.abs(y - ref16) <= 2.0 ** -16 * bound + 1e-30)
+    assert np.all(np.abs(y - ref) <= 2.0 ** -10 * bound)
+    # row 0 against the reference's own GEMV vector (Q26 = 2^26 * value); the
+    # bound adds what rounding the exported activation to fp16 can move
+    exp0 = f["expected_q26"].astype(np.float64) / 2.0 ** 26
+    dx = np.abs(f["activation"] / 4096.0 - x[0].astype(np.float64))
+    assert np.all(np.abs(y[0] - exp0) <= 2.0 ** -10 * bound[0] + abs_dot_bound(Wex, dx) + 1e-9)
+
+
+def lm_head_batch(table, hidden: torch.Tensor, final_norm: torch.Tensor):
+    lib = _lib.load()
+    m = head_model(table, final_norm)
+    B = hidden.shape[0]
+    nbytes = int(lib.q4d_workspace_bytes(ctypes.byref(m), B))
+    ws = torch.zeros(nbytes, dtype=torch.uint8, device=hidden.device)
+    tok = torch.full((B,), -1, dtype=torch.int32, device=hidden.device)
+    score = torch.zeros(B, dtype=torch.float32, device=hidden.device)
+    logits = torch.empty((B, table.shape[0]), dtype=torch.float32, device=hidden.device)
+    check(lib.q4d_lm_head_argmax_batch(ctypes.byref(m), hidden.contiguous().data_ptr(), B, tok.data_ptr(),
+                                       score.data_ptr(), logits.data_ptr(), ws.data_ptr(), nbytes,
+                                       current_stream()), "q4d_lm_head_argmax_batch")
+    torch.cuda.synchronize()
+    return tok.cpu().numpy(), score.cpu().numpy(), logits.cpu().numpy()
+
+
+def test_lm_head_batch_argmax_and_ties(dev):
+    """Planted duplicate rows make exact ties; the lower index must win, also
+    across 128-column blocks and across the two waves of one block."""
+    rng = np.random.default_rng(21)
+    V, H, B = 4096, 1024, 9
+    q = rng.integers(-8, 8, size=(V, H))
+    scale = rng.integers(100, 400, size=(V, H // 64)).astype(np.uint16)
+    hidden = rng.normal(size=(B, H)).astype(np.float32)
+    gamma = np.ones(H, dtype=np.float32)
+    xn = o.manual_rms_norm(hidden.astype(np.float64), gamma, 1e-6, np.float64)
+    # per row b: make row w_b the winner by aligning it with xn[b], duplicate it later
+    # same lane group, next block, same wave, cross-wave (2100 | 2150), cross-tile (64 | 100)
+    winners = [7, 127, 128, 1000, 2047, 2100, 3000, 4000, 64]
+    dups = [4095, 255, 129, 1001, 3071, 2150, 3001, 4094, 100]
+    for b, (wi, di) in enumerate(zip(winners, dups)):
+        sgn = np.sign(xn[b]).astype(np.int64)
+        q[wi] = np.where(sgn >= 0, 7, -8) * (sgn != 0)
+        scale[wi] = 400
+    for b, (wi, di) in enumerate(zip(winners, dups)):
+        q[di] = q[wi]
+        scale[di] = scale[wi]
+    packed = o.pack_signed_int4(q)
+    tok, score, logits = lm_head_batch(q4(packed, scale), torch.from_numpy(hidden).to(dev),
+                                       torch.from_numpy(gamma).to(dev))
+    for b in range(B):
+        first = int(np.argmax(logits[b]))  # numpy argmax returns the first maximum
+        assert tok[b] == first, (b, tok[b], first)
+        assert score[b] == logits[b, first]
+        wi, di = winners[b], dups[b]
+        if wi < di:  # duplicate after the winner: exact tie, lower index wins
+            assert logits[b, wi] == logits[b, di]
+            assert tok[b] == wi, (b, tok[b], wi)
+    # logits against the float64 product of fp16 operands; the device's fp32
+    # RMSNorm may round an element of x to the neighbouring fp16 value
+    x16 = xn.astype(np.float16).astype(np.float64)
+    ref = x16 @ w16_of(packed, scale, H).astype(np.float64).T
+    report("lm head batch logits", logits, ref)
+    bound = np.abs(x16) @ np.abs(o.dequantize_q4(packed, scale, np.float64)).T
+    assert np.all(np.abs(logits - ref) <= 2.0 ** -10 * bound)
+
+
+@pytest.fixture(scope="module")
+def batch_setup(dev):
+    cfg = Qwen3Config(num_hidden_layers=2, vocab_size=2048)
+    host = random_host_weights(cfg, seed=3, num_layers=2)
+    model = build_model(cfg, host, max_ctx=512, device=dev)
+    om = o.OracleModel.from_q4(o.OracleConfig(num_hidden_layers=2, vocab_size=2048), host["layers"],
+                               *host["embed_tokens"], host["norm"], dtype=np.float64)
+    return cfg, model, om
+
+
+@pytest.mark.parametrize("positions", [[0, 1, 63, 64, 300], [511] * 3, list(range(0, 448, 7))])
+def test_decode_batch_vs_oracle(dev, batch_setup, positions):
+    cfg, model, om = batch_setup
+    B = len(positions)
+    rng = np.random.default_rng(B)
+    tokens = rng.integers(0, cfg.vocab_size, B)
+    kv = KVCache(cfg, 2, B, model.max_ctx, dev)
+    pre = rng.normal(size=(2, 2, B, 8, model.max_ctx, 128)).astype(np.float16)
+    for b, p in enumerate(positions):
+        pre[:, :, b, :, p:] = 0
+    kv.data.copy_(torch.from_numpy(pre).to(dev))
+    print(f"[decode batch] B={B} positions={positions[:6]}...", flush=True)
+    dec = BatchedDecoder(model, B, kv)
+    logits = torch.empty((B, cfg.vocab_size), dtype=torch.float32, device=dev)
+    nt, sc = dec.step(torch.tensor(tokens, dtype=torch.int32, device=dev),
+                      torch.tensor(positions, dtype=torch.int32, device=dev), logits)
+    torch.cuda.synchronize()
+    assert dec.status() == 0
+    nt, sc, lg = nt.cpu().numpy(), sc.cpu().numpy(), logits.cpu().numpy().astype(np.float64)
+    kvd = kv.data.float().cpu().numpy()
+    worst, near = 0.0, []
+    for b, p in enumerate(positions):
+        kc = [pre[li, 0, b][None, :, :p].astype(np.float64) for li in range(2)]
+        vc = [pre[li, 1, b][None, :, :p].astype(np.float64) for li in range(2)]
+        rl, rt = o.run_manual_one_token(np.array([[tokens[b]]]), p, om, kc, vc, kv_store_dtype=np.float16)
+        r = rl[0, -1]
+        err = np.abs(lg[b] - r)
+        worst = max(worst, float(err.max() / np.abs(r).max()))
+        first = int(np.argmax(lg[b]))
+        assert nt[b] == first and sc[b] == np.float32(lg[b, first])
+        if nt[b] != rt[0, 0]:
+            gap = r[rt[0, 0]] - r[nt[b]]
+            assert gap <= err[rt[0, 0]] + err[nt[b]], (b, gap)
+            near.append((b, int(rt[0, 0]), int(nt[b]), float(gap)))
+        for li in range(2):  # appended K/V rows
+            for kind, ref_c in ((0, kc[li]), (1, vc[li])):
+                want = ref_c[0, :, p]
+                got = kvd[li, kind, b, :, p]
+                assert np.all(np.abs(got - want) <= 2e-2 * np.abs(want).max(axis=-1, keepdims=True)), (b, li, kind)
+    print(f"[decode batch] B={B} max rel logit err={worst:.3e} near_ties={near}", flush=True)
+    assert worst < 5e-3
