@@ -21,7 +21,7 @@ inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s);
 int check_matrix(const q4d_matrix_t* m, int rows, int cols) {
   if (!m || !m->w || !m->s) return Q4D_ERR_NULL;
   if (m->rows != rows || m->cols != cols) return Q4D_ERR_BAD_TABLE;
-  if (!aligned(m->w, 16) || !aligned(m->s, 2)) return Q4D_ERR_BAD_ADDR;
+  if (!aligned(m->w, 16) || !aligned(m->s, 4)) return Q4D_ERR_BAD_ADDR;
   return Q4D_OK;
 }
 
@@ -186,7 +186,7 @@ int run_lm_head(const q4d_model_t* m, const float* hidden, int32_t* tok, float* 
   a.gamma = m->final_norm;
   a.eps = m->rms_norm_eps;
   a.logits = logits;
-  a.lm_part = ws_ptr<void>(ws, W.lm_part);
+  a.lm_key = ws_ptr<unsigned long long>(ws, W.lm_key);
   a.counter = ws_ptr<int>(ws, W.counters) + W.lm_counter_index;
   a.out_token = tok;
   a.out_score = score;

@@ -1,19 +1,44 @@
 // Fused Q4 dequant-GEMV for gfx950 (wave64).
 //
-// One wave owns a "row group": the smallest set of whole rows whose 16-byte
-// chunks tile an exact multiple of 64 lanes (K=1024: 2 rows, one 16 B load
-// per lane; K=2048: 1 row; K=3072: 2 rows, three loads per lane).  Because a
-// lane always sees the same column chunks, its activations are unpacked into
-// registers once (XChunk) and reused for every row group the wave visits.
-// Waves stride over row groups, issuing U groups of 128-bit loads before
-// consuming any, so each lane keeps U*LG loads in flight.
+// Tile: one wave covers 2 rows x 1024 columns of the Q4 matrix.  Lane l
+// reads the 16-byte chunk (l % 32) of row (l / 32) of its tile, i.e. 32
+// columns, and the 32-bit word holding that chunk's Q2.14 scale, so every
+// lane issues one 128-bit weight load per tile and always sees the same 32
+// columns: its activations live in registers (XChunk) for every tile the
+// wave visits.  A matrix with K = 2048 or 3072 gives each row pair KS =
+// K / 1024 waves of one block (one 1024-column slice each); their row sums
+// are added through LDS in slice order (deterministic).  The gate/up pair of
+// the MLP is two tiles per wave (the same two rows of each matrix).
 //
-// Prologues: fp16 x, fp32 x (rounded to fp16, or split hi+lo into two fp16
-// halves for ~22-bit activations), or RMSNorm of an fp32 hidden vector
-// (reference common.py:129-134) computed by every block.
-// Epilogues: fp16/fp32 store, residual add (common.py:284,297), SwiGLU over a
-// gate/up row pair (common.py:293-295), and LM-head argmax with the
-// lowest-index tie rule (56_export_persistent_multitoken_layer_golden.py:860).
+// Loads are buffer loads: the matrix base is a wave-uniform resource, the
+// tile's row offset a scalar, and the lane's offset a per-lane constant, so
+// no per-load address arithmetic is spent.  Wave indices are scalar
+// (readfirstlane) and tile indices are clamped into the matrix instead of
+// guarded, so no load sits behind a divergent branch.  Activation loads go
+// out first (vmcnt retires in issue order, so waiting for the activations
+// leaves the weights in flight).
+//
+// Activations are prepared once per block in LDS: the block stages x (and
+// gamma), computes the RMSNorm where asked, and converts the vector into the
+// fp16 pair order the dequant trick consumes (hi, and lo = x - hi for ~22-bit
+// activations), with per-chunk sums; each lane then reads its ready chunk.
+// Doing this conversion per lane instead costs ~400 VALU instructions per
+// wave and dominated the decode-size GEMVs.
+//
+// One-shot kernels (the decode-layer projections) give each wave U tiles.
+// The streaming kernel (the LM head) runs one resident grid; each wave walks
+// its tiles grid-stride in stages of U tiles with two stages in flight
+// (ping-pong register sets, unconditional reloads in the steady state).
+//
+// Prologues: fp16 x, fp32 x, or RMSNorm of an fp32 hidden vector (reference
+// common.py:129-134).  Epilogues: fp16/fp32 store, residual add
+// (common.py:284,297), SwiGLU over the gate/up pair (common.py:293-295), and
+// LM-head argmax with the lowest-index tie rule
+// (56_export_persistent_multitoken_layer_golden.py:860).  The argmax is
+// finished without fences: each block folds its best (score, index) into one
+// 64-bit key with a device-scope atomicMax, waits for it to complete, then
+// counts in; the last block to count in reads the key back with another
+// atomic, so every read goes to the coherence point.
 #include <math.h>
 
 #include "q4d_device.h"
@@ -21,38 +46,63 @@
 
 namespace q4d {
 
-constexpr int gcd_c(int a, int b) { return b == 0 ? a : gcd_c(b, a % b); }
+namespace {
 
-template <int K>
-struct Geo {
-  static constexpr int C = K / 32;                       // 16-byte chunks per row
-  static constexpr int G = K / 64;                       // scale groups per row
-  static constexpr int L = C / gcd_c(C, 64) * 64;        // lcm(C, 64)
-  static constexpr int RG = L / C;                       // rows per row group
-  static constexpr int LG = L / 64;                      // loads per lane per group
+constexpr int kSlice = 1024;       // columns per wave tile
+constexpr int kLmBlocksPerCU = 4;  // resident blocks per CU for the streaming kernel
+constexpr int kRsrcFlags = 0x00020000;
+
+typedef __amdgpu_buffer_rsrc_t Rsrc;
+
+__device__ __forceinline__ Rsrc make_rsrc(const void* p, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, kRsrcFlags);
+}
+
+// One tile's weight chunk and the 32-bit word holding this lane's scale code
+// (two consecutive Q2.14 codes; the lane's half is chosen by the shift).
+struct TileData {
+  u32x4 w;
+  uint32_t s;
 };
 
-// Build hi (and optionally lo) XChunks from 32 fp32 activations.
-template <int XP>
-__device__ __forceinline__ void xchunks_from_f32(const float (&v)[32], XChunk& hi, XChunk& lo) {
-  float sh = 0.f, sl = 0.f;
-#pragma unroll
-  for (int m = 0; m < 4; ++m) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const float a = v[8 * m + i], b = v[8 * m + i + 4];
-      const _Float16 ah = (_Float16)a, bh = (_Float16)b;
-      hi.p[4 * m + i] = make_h2(ah, bh);
-      sh += (float)ah + (float)bh;
-      if constexpr (XP == 2) {
-        const _Float16 al = (_Float16)(a - (float)ah), bl = (_Float16)(b - (float)bh);
-        lo.p[4 * m + i] = make_h2(al, bl);
-        sl += (float)al + (float)bl;
-      }
-    }
-  }
-  hi.sum8 = 8.f * sh;
-  if constexpr (XP == 2) lo.sum8 = 8.f * sl;
+// Per-lane constant parts of a tile load.
+struct LaneOff {
+  uint32_t w;  // byte offset of the lane's chunk inside the tile's row pair
+  uint32_t s;  // byte offset of the lane's scale word
+  int sshift;  // bit offset of the lane's scale code inside that word
+};
+
+template <int K>
+__device__ __forceinline__ LaneOff lane_off(int ks, int lane) {
+  const int r = lane >> 5;
+  const int c = ks * 32 + (lane & 31);  // 16-byte chunk within the row
+  LaneOff o;
+  o.w = (uint32_t)(r * (K / 2) + c * 16);
+  o.s = (uint32_t)(r * (K / 32) + (c >> 2) * 4);
+  o.sshift = ((c >> 1) & 1) * 16;
+  return o;
+}
+
+// Load tile rows (lrow0, lrow0 + 1) of one matrix (lrow0 uniform).
+template <int K>
+__device__ __forceinline__ TileData load_rows(Rsrc rw, Rsrc rs, int lrow0, const LaneOff& o) {
+  TileData d;
+  d.w = __builtin_amdgcn_raw_buffer_load_b128(rw, o.w, (uint32_t)lrow0 * (K / 2), 0);
+  d.s = __builtin_amdgcn_raw_buffer_load_b32(rs, o.s, (uint32_t)lrow0 * (K / 32), 0);
+  return d;
+}
+
+// Segment resources are separate scalars selected with uniform conditions:
+// held in an array, the select becomes a dynamic index into a private copy.
+#define SEG_RS rw0, rw1, rw2, rs0, rs1, rs2, e0, e1
+template <int K>
+__device__ __forceinline__ TileData load_tile(int t, const LaneOff& o, Rsrc rw0, Rsrc rw1, Rsrc rw2, Rsrc rs0,
+                                              Rsrc rs1, Rsrc rs2, int e0, int e1) {
+  const int row0 = 2 * t;
+  const bool in0 = row0 < e0, in1 = row0 < e1;
+  const Rsrc rw = in0 ? rw0 : (in1 ? rw1 : rw2);
+  const Rsrc rs = in0 ? rs0 : (in1 ? rs1 : rs2);
+  return load_rows<K>(rw, rs, row0 - (in0 ? 0 : (in1 ? e0 : e1)), o);
 }
 
 // hi/lo variant of chunk_dot sharing the dequant masks.
@@ -77,424 +127,499 @@ __device__ __forceinline__ float chunk_dot_hl(const u32x4 w, const XChunk& h, co
          fmaf(c, 16777216.f, fmaf(d, 1048576.f, -l.sum8));
 }
 
-// Issue the loads of U row groups starting at gbase (wave-uniform guards).
-template <int K, int U, bool PAIR>
-__device__ __forceinline__ void load_batch(int gbase, int nw, int NG, int lane, const uint8_t* w0,
-                                           const uint8_t* w1, const uint8_t* w2, const uint16_t* s0,
-                                           const uint16_t* s1, const uint16_t* s2, int e0, int e1,
-                                           u32x4 (&wv)[U][Geo<K>::LG], uint32_t (&sv)[U][Geo<K>::LG]) {
-  constexpr int C = Geo<K>::C, RG = Geo<K>::RG, LG = Geo<K>::LG, G = Geo<K>::G;
-#pragma unroll
-  for (int u = 0; u < U; ++u) {
-    const int g = gbase + u * nw;
-    if (g < NG) {
-      int seg = 0, local0 = g;
-      if constexpr (!PAIR) {
-        const int row0 = g * RG;
-        seg = (row0 < e0) ? 0 : ((row0 < e1) ? 1 : 2);
-        local0 = row0 - (seg == 0 ? 0 : (seg == 1 ? e0 : e1));
-      }
-#pragma unroll
-      for (int j = 0; j < LG; ++j) {
-        const int f = j * 64 + lane;
-        const int r = f / C, c = f % C;
-        const int sg = PAIR ? r : seg;
-        const int row = PAIR ? g : local0 + r;
-        const uint8_t* wb = sg == 0 ? w0 : (sg == 1 ? w1 : w2);
-        const uint16_t* sb = sg == 0 ? s0 : (sg == 1 ? s1 : s2);
-        wv[u][j] = *reinterpret_cast<const u32x4*>(wb + (size_t)row * (K / 2) + c * 16);
-        sv[u][j] = sb[(size_t)row * G + (c >> 1)];
-      }
-    }
-  }
+// Row sums of one tile: lanes 16-31 hold row 0, lanes 48-63 row 1.
+template <int XP>
+__device__ __forceinline__ float tile_rows(const TileData& d, int sshift, const XChunk& xh, const XChunk& xl) {
+  float p;
+  if constexpr (XP == 2)
+    p = chunk_dot_hl(d.w, xh, xl);
+  else
+    p = chunk_dot(d.w, xh);
+  p *= scale_q2_14((d.s >> sshift) & 0xFFFFu);
+  return half_wave_sum_dpp(p);
 }
 
-template <int K, int U, int XM, int XP, int EP, bool PAIR>
-__global__ __launch_bounds__(256) void gemv_kernel(const GemvArgs a) {
-  using Gm = Geo<K>;
-  constexpr int C = Gm::C, RG = Gm::RG, LG = Gm::LG;
-  static_assert(!PAIR || RG == 2, "row-pair epilogue needs two rows per group");
+// Order-preserving 64-bit argmax key: higher score first, then lower index.
+// NaN never wins (as with the reference's strict greater-than scan) and
+// -0 compares equal to +0.
+__device__ __forceinline__ unsigned long long argmax_key(float s, int idx) {
+  if (!(s == s)) s = -INFINITY;
+  s = s + 0.0f;
+  const uint32_t b = __float_as_uint(s);
+  const uint32_t o = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+  return ((unsigned long long)o << 32) | (uint32_t)(0xFFFFFFFFu - (uint32_t)idx);
+}
+
+__device__ __forceinline__ void argmax_unkey(unsigned long long k, float* s, int* idx) {
+  const uint32_t o = (uint32_t)(k >> 32);
+  const uint32_t b = (o & 0x80000000u) ? (o & 0x7FFFFFFFu) : ~o;
+  *s = __uint_as_float(b);
+  *idx = (int)(0xFFFFFFFFu - (uint32_t)k);
+}
+
+__device__ __forceinline__ uint32_t pack_h2(_Float16 lo, _Float16 hi) {
+  return __builtin_bit_cast(uint32_t, make_h2(lo, hi));
+}
+
+template <int KS, int NWB, int XM, int XP, int EP, bool PAIR, int U, bool STREAM>
+__global__ __launch_bounds__(NWB * 64) void gemv_kernel(const GemvArgs a) {
+  constexpr int K = KS * kSlice;
+  constexpr int NT = NWB * 64;
+  constexpr int TEAMS = NWB / KS;
+  constexpr int CH = K / 32;  // 32-column chunks
+  static_assert(NWB % KS == 0, "a block holds whole teams");
+  static_assert(!STREAM || (KS == 1 && !PAIR), "streaming kernel covers one K = 1024 matrix");
+  static_assert(!PAIR || KS == 1, "gate/up pairs need K = 1024");
+  static_assert(XM != X_F16 || XP == 1, "fp16 activations have no lo part");
   const int lane = threadIdx.x & 63;
-  const int wid = threadIdx.x >> 6;
+  const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int team = wid / KS;
+  const int ks = wid % KS;
   const int bat = blockIdx.y;
 
-  __shared__ float s_red[4];
-  __shared__ int s_idx[4];
-  __shared__ int s_last;
-  __shared__ f32x4 s_x[XM == X_RMS ? K / 4 : 1];
+  constexpr int XV = (XM == X_F16) ? K / 8 : K / 4;  // 16-byte vectors of x
+  constexpr int XPT = (XV + NT - 1) / NT;            // vectors per thread
+  __shared__ f32x4 s_x[XV];
+  __shared__ f32x4 s_g[XM == X_RMS ? XV : 1];
+  __shared__ float s_red[NWB];
+  __shared__ uint32_t s_ph[CH * 16];                // hi pairs, dequant order
+  __shared__ uint32_t s_pl[XP == 2 ? CH * 16 : 1];  // lo pairs
+  __shared__ float2 s_sm[CH];                       // 8 * chunk sums (hi, lo)
+  __shared__ float s_part[STREAM ? 1 : U * TEAMS * KS * 2];
+  __shared__ unsigned long long s_key[NWB];
 
-  // Segment pointers are read with constant indices (scalar kernel-argument
-  // loads) and selected in registers: indexing a.w[] with a runtime value
-  // turns every weight load into a dependent load from the argument block.
-  const uint8_t* const w0 = a.w[0];
-  const uint8_t* const w1 = a.w[1];
-  const uint8_t* const w2 = a.w[2];
-  const uint16_t* const s0 = a.s[0];
-  const uint16_t* const s1 = a.s[1];
-  const uint16_t* const s2 = a.s[2];
+  const int NP = a.rows / 2;  // tiles (row pairs; PAIR: of each matrix)
+
+  // ---- activation loads go out first ----------------------------------------
+  f32x4 xr[XPT];
+  f32x4 gr[XM == X_RMS ? XPT : 1];
+#pragma unroll
+  for (int i = 0; i < XPT; ++i) {
+    const int v = threadIdx.x + i * NT;
+    if (v < XV) {
+      xr[i] = reinterpret_cast<const f32x4*>(static_cast<const char*>(a.x) +
+                                             (size_t)bat * K * (XM == X_F16 ? 2 : 4))[v];
+      if constexpr (XM == X_RMS) gr[i] = reinterpret_cast<const f32x4*>(a.gamma)[v];
+    }
+  }
+
+  // ---- then every weight load this wave can have in flight ------------------
   const int e0 = a.seg_end[0], e1 = a.seg_end[1];
-  const int NG = PAIR ? a.rows : a.rows / RG;
-  const int gw = blockIdx.x * 4 + wid;
-  const int nw = gridDim.x * 4;
+  const Rsrc rw0 = make_rsrc(a.w[0], (uint32_t)e0 * (K / 2));
+  const Rsrc rs0 = make_rsrc(a.s[0], (uint32_t)e0 * (K / 32));
+  const Rsrc rw1 = make_rsrc(a.w[1], (uint32_t)(PAIR ? e0 : e1 - e0) * (K / 2));
+  const Rsrc rs1 = make_rsrc(a.s[1], (uint32_t)(PAIR ? e0 : e1 - e0) * (K / 32));
+  const Rsrc rw2 = make_rsrc(a.w[2], (uint32_t)(a.seg_end[2] - e1) * (K / 2));
+  const Rsrc rs2 = make_rsrc(a.s[2], (uint32_t)(a.seg_end[2] - e1) * (K / 32));
+  const LaneOff lo = lane_off<K>(ks, lane);
 
-  // ---- activation loads go out first --------------------------------------
-  // vmcnt drains in issue order, so anything issued after the weight prefetch
-  // could only be waited for together with the weights.
-  f32x4 hreg = f32x4{0.f, 0.f, 0.f, 0.f};
-  f32x4 gam[XM == X_RMS ? LG : 1][8];
-  u32x4 xr16[XM == X_F16 ? LG : 1][4];
-  f32x4 xr32[XM == X_F32 ? LG : 1][8];
-  if constexpr (XM == X_RMS) {
-    static_assert(K / 4 <= 256, "RMS prologue stages one 16-byte vector per thread");
-    if (threadIdx.x < K / 4)
-      hreg = reinterpret_cast<const f32x4*>(static_cast<const float*>(a.x) + (size_t)bat * K)[threadIdx.x];
-#pragma unroll
-    for (int j = 0; j < LG; ++j) {
-      const int c = (j * 64 + lane) % C;
-#pragma unroll
-      for (int q = 0; q < 8; ++q) gam[j][q] = reinterpret_cast<const f32x4*>(a.gamma + c * 32)[q];
-    }
-  } else if constexpr (XM == X_F16) {
-#pragma unroll
-    for (int j = 0; j < LG; ++j) {
-      const int c = (j * 64 + lane) % C;
-      const u32x4* xp = reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(a.x) + (size_t)bat * K + c * 32);
-#pragma unroll
-      for (int q = 0; q < 4; ++q) xr16[j][q] = xp[q];
-    }
+  TileData A[U], B[STREAM ? U : 1], G[PAIR ? U : 1];
+  int base, step;
+  if constexpr (STREAM) {
+    base = blockIdx.x * NWB + wid;
+    step = gridDim.x * NWB;
   } else {
+    base = blockIdx.x * TEAMS + team;
+    step = gridDim.x * TEAMS;
+  }
 #pragma unroll
-    for (int j = 0; j < LG; ++j) {
-      const int c = (j * 64 + lane) % C;
-      const f32x4* xp = reinterpret_cast<const f32x4*>(static_cast<const float*>(a.x) + (size_t)bat * K + c * 32);
-#pragma unroll
-      for (int q = 0; q < 8; ++q) xr32[j][q] = xp[q];
+  for (int u = 0; u < U; ++u) {
+    int t = base + u * step;
+    t = t < NP ? t : NP - 1;
+    if constexpr (PAIR) {
+      A[u] = load_rows<K>(rw0, rs0, 2 * t, lo);  // gate rows
+      G[u] = load_rows<K>(rw1, rs1, 2 * t, lo);  // up rows
+    } else {
+      A[u] = load_tile<K>(t, lo, SEG_RS);
     }
   }
-
-  // ---- first batch of weights in flight while the activations are prepared ---
-  u32x4 wv[U][LG];
-  uint32_t sv[U][LG];
-  load_batch<K, U, PAIR>(gw, nw, NG, lane, w0, w1, w2, s0, s1, s2, e0, e1, wv, sv);
-
-  XChunk xh[LG];
-  XChunk xl[XP == 2 ? LG : 1];
-  if constexpr (XM == X_RMS) {
-    // stage the fp32 hidden vector in LDS and reduce sum(x^2) in a fixed order
-    // (identical in every block); LDS-only barriers keep the weights in flight
-    float ss = 0.f;
-    if (threadIdx.x < K / 4) {
-      s_x[threadIdx.x] = hreg;
-      ss = fmaf(hreg[0], hreg[0], ss);
-      ss = fmaf(hreg[1], hreg[1], ss);
-      ss = fmaf(hreg[2], hreg[2], ss);
-      ss = fmaf(hreg[3], hreg[3], ss);
-    }
-    ss = wave_sum_dpp(ss);
-    if (lane == 63) s_red[wid] = ss;
-    block_sync_lds();
-    const float inv_rms = 1.0f / sqrtf(((s_red[0] + s_red[1]) + (s_red[2] + s_red[3])) / (float)K + a.eps);
-#pragma unroll
-    for (int j = 0; j < LG; ++j) {
-      const int c = (j * 64 + lane) % C;
-      float v[32];
-#pragma unroll
-      for (int q = 0; q < 8; ++q) {
-        const f32x4 t = s_x[c * 8 + q];
-        const f32x4 g = gam[j][q];
-        v[4 * q + 0] = (t[0] * inv_rms) * g[0];
-        v[4 * q + 1] = (t[1] * inv_rms) * g[1];
-        v[4 * q + 2] = (t[2] * inv_rms) * g[2];
-        v[4 * q + 3] = (t[3] * inv_rms) * g[3];
-      }
-      xchunks_from_f32<XP>(v, xh[j], xl[XP == 2 ? j : 0]);
-    }
-  } else if constexpr (XM == X_F16) {
-#pragma unroll
-    for (int j = 0; j < LG; ++j) {
-      uint32_t xw[16];
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const u32x4 t = xr16[j][q];
-        xw[4 * q + 0] = t[0];
-        xw[4 * q + 1] = t[1];
-        xw[4 * q + 2] = t[2];
-        xw[4 * q + 3] = t[3];
-      }
-      xchunk_from_words(xw, xh[j]);
-    }
-  } else {
-#pragma unroll
-    for (int j = 0; j < LG; ++j) {
-      float v[32];
-#pragma unroll
-      for (int q = 0; q < 8; ++q) {
-        const f32x4 t = xr32[j][q];
-        v[4 * q + 0] = t[0];
-        v[4 * q + 1] = t[1];
-        v[4 * q + 2] = t[2];
-        v[4 * q + 3] = t[3];
-      }
-      xchunks_from_f32<XP>(v, xh[j], xl[XP == 2 ? j : 0]);
-    }
-  }
-
-  // ---- stream row groups (software-pipelined: next batch in flight) -----------
-  float best = -INFINITY;
-  int besti = 0x7fffffff;
-
-  for (int g0 = gw; g0 < NG; g0 += nw * U) {
-    u32x4 cw[U][LG];
-    uint32_t cs[U][LG];
-#pragma unroll
-    for (int u = 0; u < U; ++u)
-#pragma unroll
-      for (int j = 0; j < LG; ++j) {
-        cw[u][j] = wv[u][j];
-        cs[u][j] = sv[u][j];
-      }
-    if (g0 + nw * U < NG)
-      load_batch<K, U, PAIR>(g0 + nw * U, nw, NG, lane, w0, w1, w2, s0, s1, s2, e0, e1, wv, sv);
+  if constexpr (STREAM) {
+    // stage 1 goes out unconditionally (clamped): a conditional issue makes
+    // the wait-count pass assume at every later merge that it may be missing
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const int g = g0 + u * nw;
-      if (g < NG) {
-      float acc0 = 0.f, acc1 = 0.f;
+      const int t = base + (U + u) * step;
+      B[u] = load_tile<K>(t < NP ? t : NP - 1, lo, SEG_RS);
+    }
+  }
+  // the residual rows this lane may own, fetched with the weights rather than
+  // after the reduction (that would add a dependent memory round trip)
+  float res_pre[EP == EP_RESID && !STREAM ? U : 1];
+  if constexpr (EP == EP_RESID && !STREAM) {
 #pragma unroll
-      for (int j = 0; j < LG; ++j) {
-        const int r = (j * 64 + lane) / C;
-        float p;
-        if constexpr (XP == 2)
-          p = chunk_dot_hl(cw[u][j], xh[j], xl[j]);
-        else
-          p = chunk_dot(cw[u][j], xh[j]);
-        p *= scale_q2_14(cs[u][j]);
-        if (RG == 1 || r == 0)
-          acc0 += p;
-        else
-          acc1 += p;
+    for (int u = 0; u < U; ++u) {
+      const int t = base + u * step;
+      res_pre[u] = a.resid[(size_t)bat * a.rows + 2 * (t < NP ? t : NP - 1) + (lane >> 5)];
+    }
+  }
+
+  // ---- stage x (and gamma) in LDS; RMS partial sums ---------------------------
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < XPT; ++i) {
+    const int v = threadIdx.x + i * NT;
+    if (v < XV) {
+      s_x[v] = xr[i];
+      if constexpr (XM == X_RMS) {
+        s_g[v] = gr[i];
+        ss = fmaf(xr[i][0], xr[i][0], ss);
+        ss = fmaf(xr[i][1], xr[i][1], ss);
+        ss = fmaf(xr[i][2], xr[i][2], ss);
+        ss = fmaf(xr[i][3], xr[i][3], ss);
       }
-      // DPP reductions: lane 63 ends up with row g*RG (RG == 1) or, for
-      // RG == 2, lane 31 with row 2g and lane 63 with row 2g+1
-      float v;
-      if constexpr (RG == 1) {
-        v = wave_sum_dpp(acc0);
-      } else if constexpr (K == 1024) {
-        // lanes 0-31 only hold row 0, lanes 32-63 only row 1
-        v = half_wave_sum_dpp(lane < 32 ? acc0 : acc1);
+    }
+  }
+  if constexpr (XM == X_RMS) {
+    ss = wave_sum_dpp(ss);
+    if (lane == 63) s_red[wid] = ss;
+  }
+  block_sync_lds();  // LDS-only: the weights stay in flight
+
+  // ---- block-cooperative conversion into the dequant pair order ---------------
+  // Chunk c holds columns 32c..32c+31; pair p = 4m + i of the chunk is
+  // (x[32c + 8m + i], x[32c + 8m + i + 4]).  Thread q handles pairs
+  // 4m + i0 and 4m + i0 + 1 of chunk q / 8 (m = (q % 8) / 2, i0 = 2 (q % 2)),
+  // so the 8 threads of a chunk are 8 consecutive lanes.
+  {
+    float inv_rms = 1.f;
+    if constexpr (XM == X_RMS) {
+      float tot = 0.f;
+#pragma unroll
+      for (int w = 0; w < NWB; ++w) tot += s_red[w];
+      inv_rms = 1.0f / sqrtf(tot / (float)K + a.eps);
+    }
+    const float* sxf = reinterpret_cast<const float*>(s_x);
+    const float* sgf = reinterpret_cast<const float*>(s_g);
+    const _Float16* sxh = reinterpret_cast<const _Float16*>(s_x);
+    for (int q = threadIdx.x; q < CH * 8; q += NT) {
+      const int c = q >> 3, m = (q & 7) >> 1, i0 = (q & 1) * 2;
+      const int ea = c * 32 + m * 8 + i0, eb = ea + 4;
+      _Float16 h[4];  // pairs (h[0], h[1]) and (h[2], h[3])
+      _Float16 l[4];
+      if constexpr (XM == X_F16) {
+        h[0] = sxh[ea];
+        h[1] = sxh[eb];
+        h[2] = sxh[ea + 1];
+        h[3] = sxh[eb + 1];
       } else {
-        // both rows spread over all lanes: full-wave sums, then lane 31
-        // takes row 0 from lane 63's neighbourhood via a row broadcast
-        const float r0 = wave_sum_dpp(acc0);
-        const float r1 = wave_sum_dpp(acc1);
-        // the permute must run with every lane active: an inactive source
-        // lane reads as zero
-        const float r0_all = __shfl(r0, 63, kWave);
-        v = lane < 32 ? r0_all : r1;
-      }
-      const bool owner = (RG == 1) ? (lane == 63) : ((lane & 31) == 31);
-      const int row = (RG == 1) ? g : (g * 2 + (lane >> 5));
-      if constexpr (EP == EP_SWIGLU) {
-        // lane 63 holds up; row_bcast31 brings the gate from lane 31
-        const float gate = dpp_f<kDppRowBcast31, 0xC>(v);
-        if (lane == 63) {
-          const float act = (gate / (1.0f + expf(-gate))) * v;
-          static_cast<float*>(a.y)[(size_t)bat * a.rows + g] = act;
+        float v[4] = {sxf[ea], sxf[eb], sxf[ea + 1], sxf[eb + 1]};
+        if constexpr (XM == X_RMS) {
+          v[0] = (v[0] * inv_rms) * sgf[ea];
+          v[1] = (v[1] * inv_rms) * sgf[eb];
+          v[2] = (v[2] * inv_rms) * sgf[ea + 1];
+          v[3] = (v[3] * inv_rms) * sgf[eb + 1];
         }
-      } else if (owner) {
-        const size_t o = (size_t)bat * a.rows + row;
-        if constexpr (EP == EP_F16) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          h[j] = (_Float16)v[j];
+          if constexpr (XP == 2) l[j] = (_Float16)(v[j] - (float)h[j]);
+        }
+      }
+      float sh = ((float)h[0] + (float)h[1]) + ((float)h[2] + (float)h[3]);
+      float sl = 0.f;
+      *reinterpret_cast<u32x2*>(&s_ph[c * 16 + m * 4 + i0]) = u32x2{pack_h2(h[0], h[1]), pack_h2(h[2], h[3])};
+      if constexpr (XP == 2) {
+        sl = ((float)l[0] + (float)l[1]) + ((float)l[2] + (float)l[3]);
+        *reinterpret_cast<u32x2*>(&s_pl[c * 16 + m * 4 + i0]) = u32x2{pack_h2(l[0], l[1]), pack_h2(l[2], l[3])};
+      }
+      // chunk sums over its 8 consecutive lanes
+      sh += dpp_f<kDppQuadSwap1>(sh);
+      sh += dpp_f<kDppQuadSwap2>(sh);
+      sh += dpp_f<kDppRowHalfMirror>(sh);
+      if constexpr (XP == 2) {
+        sl += dpp_f<kDppQuadSwap1>(sl);
+        sl += dpp_f<kDppQuadSwap2>(sl);
+        sl += dpp_f<kDppRowHalfMirror>(sl);
+      }
+      if ((q & 7) == 0) s_sm[c] = make_float2(8.f * sh, 8.f * sl);
+    }
+  }
+  block_sync_lds();
+
+  XChunk xh, xl;
+  {
+    const int c = ks * 32 + (lane & 31);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const u32x4 t = reinterpret_cast<const u32x4*>(&s_ph[c * 16])[j];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) xh.p[4 * j + e] = __builtin_bit_cast(h2, (uint32_t)t[e]);
+      if constexpr (XP == 2) {
+        const u32x4 t2 = reinterpret_cast<const u32x4*>(&s_pl[c * 16])[j];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) xl.p[4 * j + e] = __builtin_bit_cast(h2, (uint32_t)t2[e]);
+      }
+    }
+    const float2 sm = s_sm[c];
+    xh.sum8 = sm.x;
+    xl.sum8 = sm.y;
+  }
+  // keep the activation reads ahead of the first weight use
+  __builtin_amdgcn_sched_barrier(0);
+
+  const bool owner = (lane & 31) == 31;
+  const int r = lane >> 5;
+  const int sshift = lo.sshift;
+
+  if constexpr (!STREAM) {
+    // ---- one-shot: U tiles, slices combined through LDS when KS > 1 ---------
+    float rs[U], rg[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      rs[u] = tile_rows<XP>(A[u], sshift, xh, xl);
+      if constexpr (PAIR) rg[u] = tile_rows<XP>(G[u], sshift, xh, xl);
+    }
+    if constexpr (KS > 1) {
+      if (owner) {
+#pragma unroll
+        for (int u = 0; u < U; ++u) s_part[((u * TEAMS + team) * KS + ks) * 2 + r] = rs[u];
+      }
+      __syncthreads();
+      if (ks != 0) return;
+      if (owner) {
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          float v = s_part[((u * TEAMS + team) * KS) * 2 + r];
+#pragma unroll
+          for (int k = 1; k < KS; ++k) v += s_part[((u * TEAMS + team) * KS + k) * 2 + r];
+          rs[u] = v;
+        }
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int t = base + u * step;
+      if (t >= NP) break;
+      const float v = rs[u];
+      if (owner) {
+        const size_t o = (size_t)bat * a.rows + 2 * t + r;
+        if constexpr (EP == EP_SWIGLU) {
+          static_cast<float*>(a.y)[o] = (v / (1.0f + expf(-v))) * rg[u];
+        } else if constexpr (EP == EP_F16) {
           static_cast<_Float16*>(a.y)[o] = (_Float16)v;
         } else if constexpr (EP == EP_F32) {
           static_cast<float*>(a.y)[o] = v;
         } else if constexpr (EP == EP_RESID) {
-          static_cast<float*>(a.y)[o] = a.resid[o] + v;
-        } else if constexpr (EP == EP_ARGMAX) {
-          if (a.logits) a.logits[row] = v;
-          if (arg_better(v, row, best, besti)) {
-            best = v;
-            besti = row;
+          static_cast<float*>(a.y)[o] = res_pre[u] + v;
+        }
+      }
+    }
+  } else {
+    // ---- streaming: two stages of U tiles in flight (A, B ping-pong) --------
+    float best = -INFINITY;
+    int besti = 0x7fffffff;
+    auto consume = [&](const TileData (&D)[U], int first) {
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int t = first + u * step;
+        const float v = tile_rows<XP>(D[u], sshift, xh, xl);
+        if (t < NP && owner) {
+          const int row = 2 * t + r;
+          if constexpr (EP == EP_ARGMAX) {
+            if (a.logits) a.logits[row] = v;
+            // rows rise along a lane's sequence: strict > keeps the lowest
+            // index among equal scores
+            if (v > best) {
+              best = v;
+              besti = row;
+            }
+          } else {
+            const size_t o = (size_t)bat * a.rows + row;
+            if constexpr (EP == EP_F16)
+              static_cast<_Float16*>(a.y)[o] = (_Float16)v;
+            else
+              static_cast<float*>(a.y)[o] = v;
           }
         }
       }
-      }  // g < NG
-    }
-  }
-
-  if constexpr (EP == EP_ARGMAX) {
-    // wave -> block -> grid (last block to finish reduces all block results)
+    };
+    // S stages of U tiles per wave (uniform over the grid; the host sizes the
+    // grid so that S >= 2 wherever the matrix allows).  Steady state: both
+    // reloads are unconditional, so each consume waits only for its own stage.
+    const int S = (NP + U * step - 1) / (U * step);
+    auto reload = [&](TileData (&D)[U], int st) {
 #pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) {
-      const float ob = shfl_xor_f(best, m);
-      const int oi = __shfl_xor(besti, m, kWave);
-      if (arg_better(ob, oi, best, besti)) {
-        best = ob;
-        besti = oi;
+      for (int u = 0; u < U; ++u) {
+        const int t = base + (st * U + u) * step;
+        D[u] = load_tile<K>(t < NP ? t : NP - 1, lo, SEG_RS);
       }
+    };
+    int st = 0;
+    for (; st + 3 < S; st += 2) {
+      consume(A, base + st * U * step);
+      reload(A, st + 2);
+      consume(B, base + (st + 1) * U * step);
+      reload(B, st + 3);
     }
-    __syncthreads();  // s_red may still be read by the RMS prologue
-    if (lane == 0) {
-      s_red[wid] = best;
-      s_idx[wid] = besti;
+    consume(A, base + st * U * step);
+    if (st + 2 < S) {
+      reload(A, st + 2);
+      consume(B, base + (st + 1) * U * step);
+      consume(A, base + (st + 2) * U * step);
+    } else {
+      consume(B, base + (st + 1) * U * step);  // may lie wholly past the matrix
     }
-    __syncthreads();
-    float* part = static_cast<float*>(a.lm_part);
-    if (threadIdx.x == 0) {
-      float bb = s_red[0];
-      int bi = s_idx[0];
-      for (int w = 1; w < 4; ++w)
-        if (arg_better(s_red[w], s_idx[w], bb, bi)) {
-          bb = s_red[w];
-          bi = s_idx[w];
-        }
-      part[2 * blockIdx.x] = bb;
-      reinterpret_cast<int*>(part)[2 * blockIdx.x + 1] = bi;
-      // release this thread's partial before counting in (agent scope)
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-      const int done = atomicAdd(a.counter, 1);
-      s_last = (done == (int)gridDim.x - 1);
-    }
-    __syncthreads();
-    if (s_last) {
-      // acquire the partials released by every other block
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-      float bb = -INFINITY;
-      int bi = 0x7fffffff;
-      for (int i = threadIdx.x; i < (int)gridDim.x; i += 256) {
-        const float sc = part[2 * i];
-        const int ix = reinterpret_cast<int*>(part)[2 * i + 1];
-        if (arg_better(sc, ix, bb, bi)) {
-          bb = sc;
-          bi = ix;
-        }
-      }
+
+    if constexpr (EP == EP_ARGMAX) {
+      unsigned long long key = argmax_key(best, besti);
 #pragma unroll
       for (int m = 32; m >= 1; m >>= 1) {
-        const float ob = shfl_xor_f(bb, m);
-        const int oi = __shfl_xor(bi, m, kWave);
-        if (arg_better(ob, oi, bb, bi)) {
-          bb = ob;
-          bi = oi;
-        }
+        const unsigned long long o = __shfl_xor(key, m, kWave);
+        key = o > key ? o : key;
       }
-      __syncthreads();
-      if (lane == 0) {
-        s_red[wid] = bb;
-        s_idx[wid] = bi;
-      }
+      if (lane == 0) s_key[wid] = key;
       __syncthreads();
       if (threadIdx.x == 0) {
-        for (int w = 1; w < 4; ++w)
-          if (arg_better(s_red[w], s_idx[w], s_red[0], s_idx[0])) {
-            s_red[0] = s_red[w];
-            s_idx[0] = s_idx[w];
-          }
-        a.out_token[0] = s_idx[0];
-        a.out_score[0] = s_red[0];
-        *a.counter = 0;  // ready for the next launch
+        unsigned long long bk = s_key[0];
+#pragma unroll
+        for (int w = 1; w < NWB; ++w) bk = s_key[w] > bk ? s_key[w] : bk;
+        // fold in, wait for the atomic to be performed, then count in
+        const unsigned long long old =
+            __hip_atomic_fetch_max(a.lm_key, bk, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        asm volatile("" ::"v"((uint32_t)old), "v"((uint32_t)(old >> 32)) : "memory");
+        const int done = __hip_atomic_fetch_add(a.counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (done == (int)gridDim.x - 1) {
+          const unsigned long long fin =
+              __hip_atomic_fetch_max(a.lm_key, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          float sc;
+          int ix;
+          argmax_unkey(fin, &sc, &ix);
+          a.out_token[0] = ix;
+          a.out_score[0] = sc;
+          // ready for the next launch (stream order makes these visible to it)
+          __hip_atomic_store(a.lm_key, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          __hip_atomic_store(a.counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
       }
     }
   }
 }
 
 // ---------------------------------------------------------------------------
-// Blocks of one kernel instance that fit on the device at once (queried once
-// per instance); large GEMVs launch one resident wave set that loops, so the
-// per-block activation prologue is paid once per resident block.
 template <class F>
-static int resident_blocks(F kernel) {
+int resident_blocks(F kernel, int threads) {
   static int cached = 0;
   if (cached == 0) {
     int dev = 0, cus = 0, per_cu = 0;
     if (hipGetDevice(&dev) != hipSuccess ||
         hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, 256, 0) != hipSuccess || per_cu < 1)
-      return 1024;  // conservative fallback, recomputed next call
-    cached = cus * per_cu;
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, threads, 0) != hipSuccess || per_cu < 1)
+      return 256;  // conservative fallback, recomputed next call
+    cached = cus * (per_cu < kLmBlocksPerCU ? per_cu : kLmBlocksPerCU);
   }
   return cached;
 }
 
-template <int K, int U, int XM, int XP, int EP, bool PAIR>
-static int launch_inst(const GemvArgs& a, int max_blocks, hipStream_t stream) {
-  using Gm = Geo<K>;
-  const int NG = PAIR ? a.rows : a.rows / Gm::RG;
-  int waves = (NG + U - 1) / U;
-  int blocks = (waves + 3) / 4;
-  const int res = resident_blocks(gemv_kernel<K, U, XM, XP, EP, PAIR>);
-  if (blocks > res) blocks = res;
-  if (blocks > max_blocks) blocks = max_blocks;
+template <int KS, int NWB, int XM, int XP, int EP, bool PAIR, int U, bool STREAM>
+int launch_inst(const GemvArgs& a, hipStream_t stream) {
+  constexpr int TEAMS = NWB / KS;
+  const int NP = a.rows / 2;
+  int blocks;
+  if constexpr (STREAM) {
+    // stages per wave over the resident grid (at least 2), then the smallest
+    // grid covering the matrix in that many stages (few clamped tail tiles)
+    const int res = resident_blocks(gemv_kernel<KS, NWB, XM, XP, EP, PAIR, U, STREAM>, NWB * 64);
+    const long per_stage = (long)res * NWB * U;
+    int S = (int)((NP + per_stage - 1) / per_stage);
+    if (S < 2) S = 2;
+    blocks = (int)((NP + (long)NWB * U * S - 1) / ((long)NWB * U * S));
+  } else {
+    blocks = (NP + TEAMS * U - 1) / (TEAMS * U);
+  }
   if (blocks < 1) blocks = 1;
   dim3 grid(blocks, a.batch);
-  hipLaunchKernelGGL((gemv_kernel<K, U, XM, XP, EP, PAIR>), grid, dim3(256), 0, stream, a);
+  hipLaunchKernelGGL((gemv_kernel<KS, NWB, XM, XP, EP, PAIR, U, STREAM>), grid, dim3(NWB * 64), 0, stream, a);
   return check_launch();
 }
 
-template <int K, int XM, int XP, int EP, bool PAIR>
-static int launch_u(const GemvArgs& a, hipStream_t stream) {
-  if constexpr (EP == EP_ARGMAX) return launch_inst<K, 4, XM, XP, EP, PAIR>(a, kLmMaxBlocks, stream);
-  const int rg = Geo<K>::RG;
-  const int NG = PAIR ? a.rows : a.rows / rg;
-  // three chunks per lane: one row group per batch keeps VGPRs below 256
-  if constexpr (K == 3072) return launch_inst<K, 1, XM, XP, EP, PAIR>(a, 4096, stream);
-  if (NG <= 16384) return launch_inst<K, 2, XM, XP, EP, PAIR>(a, 4096, stream);
-  return launch_inst<K, 4, XM, XP, EP, PAIR>(a, 4096, stream);
+// Block shapes: K = 1024 -> 4 one-slice waves; K = 2048 -> 2 teams of 2;
+// K = 3072 -> 2 teams of 3 (384 threads).
+template <int KS>
+constexpr int nwb_of() {
+  return KS == 3 ? 6 : 4;
 }
 
-template <int K>
-static int dispatch_k(const GemvArgs& a, int xm, int xp, int ep, bool pair, hipStream_t st) {
+template <int KS, int XM, int XP, int EP, bool PAIR>
+int launch_sel(const GemvArgs& a, hipStream_t st) {
+  if constexpr (EP == EP_ARGMAX) {
+    return launch_inst<1, 4, XM, XP, EP, false, 4, true>(a, st);
+  } else {
+    return launch_inst<KS, nwb_of<KS>(), XM, XP, EP, PAIR, 1, false>(a, st);
+  }
+}
+
+template <int KS>
+int dispatch_k(const GemvArgs& a, int xm, int xp, int ep, bool pair, hipStream_t st) {
   // primitive linear: fp16 / fp32 in, fp16 / fp32 out
   if (!pair && (ep == EP_F16 || ep == EP_F32)) {
-    if (xm == X_F16) return ep == EP_F16 ? launch_u<K, X_F16, 1, EP_F16, false>(a, st)
-                                         : launch_u<K, X_F16, 1, EP_F32, false>(a, st);
-    if (xm == X_F32 && xp == 1) return ep == EP_F16 ? launch_u<K, X_F32, 1, EP_F16, false>(a, st)
-                                                    : launch_u<K, X_F32, 1, EP_F32, false>(a, st);
-    if (xm == X_F32 && xp == 2) return ep == EP_F16 ? launch_u<K, X_F32, 2, EP_F16, false>(a, st)
-                                                    : launch_u<K, X_F32, 2, EP_F32, false>(a, st);
+    if (xm == X_F16) return ep == EP_F16 ? launch_sel<KS, X_F16, 1, EP_F16, false>(a, st)
+                                         : launch_sel<KS, X_F16, 1, EP_F32, false>(a, st);
+    if (xm == X_F32 && xp == 1) return ep == EP_F16 ? launch_sel<KS, X_F32, 1, EP_F16, false>(a, st)
+                                                    : launch_sel<KS, X_F32, 1, EP_F32, false>(a, st);
+    if (xm == X_F32 && xp == 2) return ep == EP_F16 ? launch_sel<KS, X_F32, 2, EP_F16, false>(a, st)
+                                                    : launch_sel<KS, X_F32, 2, EP_F32, false>(a, st);
   }
-  if constexpr (K == 1024) {
+  if constexpr (KS == 1) {
     if (xm == X_RMS && ep == EP_F32 && !pair)
-      return xp == 2 ? launch_u<K, X_RMS, 2, EP_F32, false>(a, st) : launch_u<K, X_RMS, 1, EP_F32, false>(a, st);
+      return xp == 2 ? launch_sel<1, X_RMS, 2, EP_F32, false>(a, st) : launch_sel<1, X_RMS, 1, EP_F32, false>(a, st);
     if (xm == X_RMS && ep == EP_SWIGLU && pair)
-      return xp == 2 ? launch_u<K, X_RMS, 2, EP_SWIGLU, true>(a, st) : launch_u<K, X_RMS, 1, EP_SWIGLU, true>(a, st);
+      return xp == 2 ? launch_sel<1, X_RMS, 2, EP_SWIGLU, true>(a, st)
+                     : launch_sel<1, X_RMS, 1, EP_SWIGLU, true>(a, st);
     if (xm == X_RMS && ep == EP_ARGMAX && !pair)
-      return xp == 2 ? launch_u<K, X_RMS, 2, EP_ARGMAX, false>(a, st) : launch_u<K, X_RMS, 1, EP_ARGMAX, false>(a, st);
-  }
-  if constexpr (K == 2048 || K == 3072) {
+      return xp == 2 ? launch_sel<1, X_RMS, 2, EP_ARGMAX, false>(a, st)
+                     : launch_sel<1, X_RMS, 1, EP_ARGMAX, false>(a, st);
+  } else {
     if (xm == X_F32 && ep == EP_RESID && !pair)
-      return xp == 2 ? launch_u<K, X_F32, 2, EP_RESID, false>(a, st) : launch_u<K, X_F32, 1, EP_RESID, false>(a, st);
+      return xp == 2 ? launch_sel<KS, X_F32, 2, EP_RESID, false>(a, st)
+                     : launch_sel<KS, X_F32, 1, EP_RESID, false>(a, st);
   }
   return Q4D_ERR_SHAPE;
 }
 
-// Environment-free default: fp32 activations enter the GEMV as hi+lo fp16 pairs.
+}  // namespace
+
+// Validates geometry and launches.  fp32 activations enter the GEMV as fp16
+// hi + lo pairs when xp == 2, rounded to fp16 when xp == 1.
 int launch_gemv_xp(const GemvArgs& a, int xm, int xp, int ep, bool pair, hipStream_t st) {
   if (a.cols != 1024 && a.cols != 2048 && a.cols != 3072) return Q4D_ERR_SHAPE;
-  if (a.nseg < 1 || a.nseg > 3 || a.rows <= 0 || a.batch <= 0) return Q4D_ERR_SHAPE;
-  const int rg = (a.cols == 2048) ? 1 : 2;
+  if (a.nseg < 1 || a.nseg > 3 || a.rows <= 0 || (a.rows % 2) || a.batch <= 0 || a.batch > 65535)
+    return Q4D_ERR_SHAPE;
+  // buffer resources hold 32-bit byte counts
+  if ((long long)a.rows * (a.cols / 2) >= (1ll << 31)) return Q4D_ERR_SHAPE;
   if (pair) {
     if (a.cols != 1024 || a.nseg != 2) return Q4D_ERR_SHAPE;
   } else {
-    if (a.rows % rg) return Q4D_ERR_SHAPE;
     for (int i = 0; i < a.nseg; ++i)
-      if (a.seg_end[i] % rg) return Q4D_ERR_SHAPE;
+      if (a.seg_end[i] % 2 || (i > 0 && a.seg_end[i] < a.seg_end[i - 1])) return Q4D_ERR_SHAPE;
     if (a.seg_end[a.nseg - 1] != a.rows) return Q4D_ERR_SHAPE;
   }
   for (int i = 0; i < a.nseg; ++i) {
     if (!a.w[i] || !a.s[i]) return Q4D_ERR_NULL;
-    if (!aligned(a.w[i], 16) || !aligned(a.s[i], 2)) return Q4D_ERR_BAD_ADDR;
+    if (!aligned(a.w[i], 16) || !aligned(a.s[i], 4)) return Q4D_ERR_BAD_ADDR;
   }
   if (!a.x || (!a.y && ep != EP_ARGMAX)) return Q4D_ERR_NULL;
   if (!aligned(a.x, 16)) return Q4D_ERR_BAD_ADDR;
   if (xm == X_RMS && (!a.gamma || !aligned(a.gamma, 16))) return Q4D_ERR_NULL;
   if (ep == EP_RESID && !a.resid) return Q4D_ERR_NULL;
-  if (ep == EP_ARGMAX && (!a.lm_part || !a.counter || !a.out_token || !a.out_score || a.batch != 1))
+  if (ep == EP_ARGMAX && (!a.lm_key || !a.counter || !a.out_token || !a.out_score || a.batch != 1))
     return Q4D_ERR_NULL;
+  if (ep == EP_ARGMAX && !aligned(a.lm_key, 8)) return Q4D_ERR_BAD_ADDR;
   if (xm == X_F16 && xp != 1) return Q4D_ERR_DTYPE;
+  // unused segments: empty ranges on segment 0's memory, never selected
+  GemvArgs b = a;
+  if (pair) {
+    b.seg_end[0] = b.rows;
+    b.seg_end[1] = b.rows;
+  }
+  for (int i = b.nseg; i < 3; ++i) {
+    b.w[i] = b.w[0];
+    b.s[i] = b.s[0];
+    b.seg_end[i] = b.seg_end[i - 1];
+  }
   switch (a.cols) {
-    case 1024: return dispatch_k<1024>(a, xm, xp, ep, pair, st);
-    case 2048: return dispatch_k<2048>(a, xm, xp, ep, pair, st);
-    default: return dispatch_k<3072>(a, xm, xp, ep, pair, st);
+    case 1024: return dispatch_k<1>(b, xm, xp, ep, pair, st);
+    case 2048: return dispatch_k<2>(b, xm, xp, ep, pair, st);
+    default: return dispatch_k<3>(b, xm, xp, ep, pair, st);
   }
 }
 

@@ -20,6 +20,7 @@ inline size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 struct WsLayout {
   size_t status;     // int32[64]: [0] = status bits
   size_t counters;   // int32[batch * kv_heads] attention split counters, then 1 LM counter
+  size_t lm_key;     // u64 packed (score, index) running LM-head argmax (zeroed with the counters)
   size_t hidden;     // f32 [batch, hidden]          residual stream
   size_t qkv;        // f32 [batch, (qh + 2 kvh) * d] raw q|k|v projections
   size_t qrope;      // f32 [batch, qh * d]          q after norm + RoPE (primitive path)
@@ -27,7 +28,6 @@ struct WsLayout {
   size_t act;        // f32 [batch, intermediate]    silu(gate) * up
   size_t part_ml;    // f32 [batch, qh, nsplit, 2]   split max / sum
   size_t part_acc;   // f32 [batch, qh, nsplit, d]   split partial outputs
-  size_t lm_part;    // {f32 score, i32 idx}[kLmMaxBlocks]
   size_t xh;         // f16 [batch, max(hidden, qh*d, intermediate)]  MFMA-path activations
   size_t row_score;  // f32 [batch, vocab/128]  batched LM-head argmax partials
   size_t row_idx;    // i32 [batch, vocab/128]
@@ -45,6 +45,7 @@ inline WsLayout ws_layout(const q4d_model_t* m, int batch) {
   L.status = o;   o = align_up(o + 64 * 4, A);
   L.counters = o; o = align_up(o + (size_t)(batch * kvh + 1) * 4, A);
   L.lm_counter_index = batch * kvh;
+  L.lm_key = o;   o = align_up(o + 8, A);
   L.hidden = o;   o = align_up(o + (size_t)batch * m->hidden_size * 4, A);
   L.qkv = o;      o = align_up(o + (size_t)batch * (qh + 2 * kvh) * d * 4, A);
   L.qrope = o;    o = align_up(o + (size_t)batch * qh * d * 4, A);
@@ -52,7 +53,6 @@ inline WsLayout ws_layout(const q4d_model_t* m, int batch) {
   L.act = o;      o = align_up(o + (size_t)batch * m->intermediate_size * 4, A);
   L.part_ml = o;  o = align_up(o + (size_t)batch * qh * L.nsplit_max * 2 * 4, A);
   L.part_acc = o; o = align_up(o + (size_t)batch * qh * L.nsplit_max * d * 4, A);
-  L.lm_part = o;  o = align_up(o + (size_t)kLmMaxBlocks * 8, A);
   int wmax = m->hidden_size;
   if (qh * d > wmax) wmax = qh * d;
   if (m->intermediate_size > wmax) wmax = m->intermediate_size;
@@ -99,7 +99,7 @@ struct GemvArgs {
   const float* resid;   // EP_RESID: y = resid + W x
   // EP_ARGMAX.
   float* logits;        // optional
-  void* lm_part;
+  unsigned long long* lm_key;  // zero before the first launch; reset by the last block
   int* counter;
   int* out_token;
   float* out_score;
