@@ -6,22 +6,29 @@
 // out = softmax . v.  The cache plane of one layer is
 // [batch][kv_head][max_ctx][head_dim] fp16 so each head streams contiguously.
 //
-// Two kernels (split-K over the context, flash-decoding style):
-//  1. attn_split_kernel, grid (split, kv_head, batch), 256 threads: the two q
-//     heads of one kv head over kAttnChunk (= 64) positions.  Thread t owns
-//     dims 8*(t%16)..+7 of positions t/16 + 16*i (i < 4) for both K and V and
-//     issues its eight 16-byte loads together, so a chunk costs one memory
-//     round trip.  Scores are 8-dim partial dots reduced over the 16 lanes of
-//     a position; the chunk softmax runs in one wave per head (exp2, log2e
-//     folded into q); P.V accumulates 16 values per thread.  The chunk's
-//     (max, sum, partial output) goes to the workspace.
-//  2. attn_merge_kernel, grid (kv_head, batch): rescales and sums the chunk
-//     partials.  The kernel boundary orders the two, so no device-scope fence
-//     (an L2 write-back on this part) is needed.
-// With fused = 1 the split kernel first applies the per-head q/k RMSNorm and
-// RoPE of common.py:258-268 to the raw projections; the block owning the
-// last chunk appends the new K/V row (append_cache, common.py:186-189) and
-// takes that position from LDS instead of reading back its own global write.
+// One kernel, split-K over the context (flash-decoding style): grid
+// (chunk, kv_head, batch), 256 threads per block; a block takes the two q
+// heads of one kv head over kAttnChunk (= 64) positions.
+//  - Thread t owns dims 8*(t%16)..+7 of positions t/16 + 16*i (i < 4) for
+//    both K and V and issues its eight 16-byte loads first, so a chunk costs
+//    one memory round trip.
+//  - Waves 0/1 prepare q head 2j / 2j+1, waves 2/3 the new k / v row: lane l
+//    holds dims l and l + 64, which are also each other's rotate-half
+//    partner, so the per-head RMSNorm (common.py:258-262) and RoPE
+//    (common.py:264-268) need no block-wide exchange.  With fused = 0 the q
+//    heads arrive ready.
+//  - Scores are 8-dim partial dots reduced over the 16 lanes of a position
+//    (DPP); the chunk softmax runs in one wave per head (exp2, log2e folded
+//    into q); P.V partials are reduced over positions through LDS.
+//  - The chunk's (max, sum, partial output) is published with device-scope
+//    atomic stores; after they complete the block counts in on a per-(kv
+//    head, sequence) counter, and the block that completes the count merges
+//    all chunks, reading them back with device-scope atomic loads.  The
+//    counter atomic is issued only after the stores are performed, so no
+//    fence (an L2 write-back on this part) and no second launch is needed.
+// The block owning the new position appends its K/V row (append_cache,
+// common.py:186-189) and takes that row from LDS rather than from its own
+// global write.
 #include <math.h>
 
 #include "q4d_device.h"
@@ -30,6 +37,8 @@
 namespace q4d {
 
 static_assert(kAttnChunk == 64, "thread mapping assumes 64 positions per chunk");
+
+namespace {
 
 __device__ __forceinline__ void unpack8(const u32x4 w, float (&f)[8]) {
 #pragma unroll
@@ -41,10 +50,39 @@ __device__ __forceinline__ void unpack8(const u32x4 w, float (&f)[8]) {
   }
 }
 
-__global__ __launch_bounds__(256) void attn_split_kernel(const AttnArgs a) {
+// Max over each 16-lane row (every lane of the row receives it).
+__device__ __forceinline__ float row16_max(float v) {
+  v = fmaxf(v, dpp_f<kDppQuadSwap1>(v));
+  v = fmaxf(v, dpp_f<kDppQuadSwap2>(v));
+  v = fmaxf(v, dpp_f<kDppRowHalfMirror>(v));
+  return fmaxf(v, dpp_f<kDppRowMirror>(v));
+}
+
+// Whole-wave sum / max, returned in every lane.
+__device__ __forceinline__ float wave_sum_all(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wave_sum_dpp(v)), 63));
+}
+__device__ __forceinline__ float wave_max_all(float v) {
+  v = row16_max(v);
+  const float r0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 0));
+  const float r1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 16));
+  const float r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 32));
+  const float r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 48));
+  return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
+}
+
+__device__ __forceinline__ void store_dev(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float load_dev(const float* p) {
+  return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__global__ __launch_bounds__(256) void attn_kernel(const AttnArgs a) {
   constexpr int D = 128;
   const int s = blockIdx.x, j = blockIdx.y, b = blockIdx.z;
-  const int t = threadIdx.x, lane = t & 63, wid = t >> 6;
+  const int t = threadIdx.x, lane = t & 63;
+  const int wid = __builtin_amdgcn_readfirstlane(t >> 6);
   const int pos = a.positions[b];
   if (pos < 0 || pos >= a.max_ctx) {
     if (s == 0 && j == 0 && t == 0) atomicOr(a.status, Q4D_STATUS_BAD_POSITION);
@@ -58,20 +96,52 @@ __global__ __launch_bounds__(256) void attn_split_kernel(const AttnArgs a) {
   // positions below `cached` are read from the cache; in fused mode the new
   // position pos is produced here
   const int cached = a.fused ? pos : T;
+  const bool last = (s == nsplit - 1);  // block-uniform: holds pos
 
   __shared__ float sq[2][D];
-  __shared__ float sk[D];
   __shared__ uint16_t snew[2][D];  // fp16 bits of the appended k (roped) and v
-  __shared__ float sred[8];
   __shared__ float ssc[2][kAttnChunk];
   __shared__ float sml[2][2];
-  __shared__ float spv[4][2][D];
+  __shared__ float spv[16][2][D];  // P.V partials per position row group
+  __shared__ int s_last;
 
   const size_t plane_off = ((size_t)(b * a.kvh + j) * a.max_ctx) * D;
   uint16_t* kb = a.kcache + plane_off;
   uint16_t* vb = a.vcache + plane_off;
 
-  // ---- issue every K/V load of this chunk first ------------------------------
+  // ---- the q / new k / new v inputs of this wave go out first ---------------
+  // (vmcnt retires in issue order: issued after the K/V loads, the RMSNorm and
+  // RoPE below could not start before the K/V chunk had arrived)
+  // Waves 0/1 take q head 2j / 2j+1, wave 2 the new k row, wave 3 the new v
+  // row; lane l holds dims l and l + 64.
+  const float qscale = a.scaling * 1.4426950408889634f;  // fold log2(e) for exp2
+  const int qkv_stride = (a.qh + 2 * a.kvh) * D;
+  const bool qk_wave = a.fused ? (wid < 2 || (last && wid == 2)) : (wid < 2);
+  const bool v_wave = a.fused && last && wid == 3;
+  float x0 = 0.f, x1 = 0.f, c = 0.f, sn = 0.f, g0 = 0.f, g1 = 0.f;
+  if (a.fused) {
+    const float* src = a.qkv + (size_t)b * qkv_stride;
+    if (qk_wave) {
+      const float* row = wid < 2 ? src + (j * 2 + wid) * D : src + (a.qh + j) * D;
+      const float* gam = wid < 2 ? a.q_gamma : a.k_gamma;
+      x0 = row[lane];
+      x1 = row[lane + 64];
+      c = a.rope_cos[(size_t)pos * (D / 2) + lane];
+      sn = a.rope_sin[(size_t)pos * (D / 2) + lane];
+      g0 = gam[lane];
+      g1 = gam[lane + 64];
+    } else if (v_wave) {
+      const float* row = src + (a.qh + a.kvh + j) * D;
+      x0 = row[lane];
+      x1 = row[lane + 64];
+    }
+  } else if (qk_wave) {
+    const float* qh = a.q + ((size_t)b * a.qh + j * 2 + wid) * D;
+    x0 = qh[lane];
+    x1 = qh[lane + 64];
+  }
+
+  // ---- then every K/V load of this chunk ------------------------------------
   const int sub = t & 15;  // dims 8*sub .. 8*sub+7
   const int pr = t >> 4;   // positions pr + 16*i
   u32x4 kr[4], vr[4];
@@ -87,55 +157,35 @@ __global__ __launch_bounds__(256) void attn_split_kernel(const AttnArgs a) {
     }
   }
 
-  const int hh = t >> 7;  // which of the two q heads (threads 0-127 / 128-255)
-  const int d = t & (D - 1);
-  const int h = j * 2 + hh;
-  const float qscale = a.scaling * 1.4426950408889634f;  // fold log2(e) for exp2
-  const bool last = (s == nsplit - 1);                   // block-uniform: holds pos
-
-  if (a.fused) {
-    const int qkv_stride = (a.qh + 2 * a.kvh) * D;
-    const float c = a.rope_cos[(size_t)pos * (D / 2) + (d & 63)];
-    const float sn = a.rope_sin[(size_t)pos * (D / 2) + (d & 63)];
-    const float qv = a.qkv[(size_t)b * qkv_stride + h * D + d];
-    // threads 0-127: new k; threads 128-255: new v (only the last chunk)
-    const float kv = last ? a.qkv[(size_t)b * qkv_stride + (a.qh + hh * a.kvh + j) * D + d] : 0.f;
-    // q: per-head RMSNorm (common.py:260) then RoPE (common.py:267-268)
-    const float qs = wave_sum(qv * qv);
-    const float ks = wave_sum(kv * kv);
-    if (lane == 0) {
-      sred[wid] = qs;
-      sred[4 + wid] = ks;
+  // ---- per-head RMSNorm (common.py:258-262) + rotate-half RoPE (264-268) -------
+  if (a.fused && qk_wave) {
+    const float ss = wave_sum_all(fmaf(x0, x0, x1 * x1));
+    const float inv = 1.0f / sqrtf(ss / (float)D + a.eps);
+    const float n0 = (x0 * inv) * g0, n1 = (x1 * inv) * g1;
+    // rotate_half: dim d < 64 takes -x[d + 64], dim d >= 64 takes x[d - 64]
+    const float r0 = n0 * c + (-n1) * sn;
+    const float r1 = n1 * c + n0 * sn;
+    if (wid < 2) {
+      sq[wid][lane] = r0 * qscale;
+      sq[wid][lane + 64] = r1 * qscale;
+    } else {
+      const uint16_t b0 = __builtin_bit_cast(uint16_t, (_Float16)r0);
+      const uint16_t b1 = __builtin_bit_cast(uint16_t, (_Float16)r1);
+      snew[0][lane] = b0;
+      snew[0][lane + 64] = b1;
+      kb[(size_t)pos * D + lane] = b0;
+      kb[(size_t)pos * D + lane + 64] = b1;
     }
-    __syncthreads();
-    const float qinv = 1.0f / sqrtf((sred[2 * hh] + sred[2 * hh + 1]) / (float)D + a.eps);
-    const float qn = (qv * qinv) * a.q_gamma[d];
-    sq[hh][d] = qn;
-    float kn = 0.f;
-    if (last && hh == 0) {
-      const float kinv = 1.0f / sqrtf((sred[4] + sred[5]) / (float)D + a.eps);
-      kn = (kv * kinv) * a.k_gamma[d];
-      sk[d] = kn;
-    }
-    __syncthreads();
-    const float qrot = d < 64 ? -sq[hh][d + 64] : sq[hh][d - 64];
-    const float qrope = qn * c + qrot * sn;
-    if (last) {
-      _Float16 nv;
-      if (hh == 0) {
-        const float krot = d < 64 ? -sk[d + 64] : sk[d - 64];
-        nv = (_Float16)(kn * c + krot * sn);
-      } else {
-        nv = (_Float16)kv;
-      }
-      const uint16_t bits = __builtin_bit_cast(uint16_t, nv);
-      snew[hh][d] = bits;
-      (hh == 0 ? kb : vb)[(size_t)pos * D + d] = bits;
-    }
-    __syncthreads();
-    sq[hh][d] = qrope * qscale;
-  } else {
-    sq[hh][d] = a.q[((size_t)b * a.qh + h) * D + d] * qscale;
+  } else if (v_wave) {
+    const uint16_t b0 = __builtin_bit_cast(uint16_t, (_Float16)x0);
+    const uint16_t b1 = __builtin_bit_cast(uint16_t, (_Float16)x1);
+    snew[1][lane] = b0;
+    snew[1][lane + 64] = b1;
+    vb[(size_t)pos * D + lane] = b0;
+    vb[(size_t)pos * D + lane + 64] = b1;
+  } else if (qk_wave) {
+    sq[wid][lane] = x0 * qscale;
+    sq[wid][lane + 64] = x1 * qscale;
   }
   __syncthreads();
   if (a.fused && last) {
@@ -161,7 +211,6 @@ __global__ __launch_bounds__(256) void attn_split_kernel(const AttnArgs a) {
     q0[e] = sq[0][sub * 8 + e];
     q1[e] = sq[1][sub * 8 + e];
   }
-  float sc0[4], sc1[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     float kf[8];
@@ -172,24 +221,12 @@ __global__ __launch_bounds__(256) void attn_split_kernel(const AttnArgs a) {
       x0 = fmaf(q0[e], kf[e], x0);
       x1 = fmaf(q1[e], kf[e], x1);
     }
-    sc0[i] = x0;
-    sc1[i] = x1;
-  }
-#pragma unroll
-  for (int m = 8; m >= 1; m >>= 1)
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      sc0[i] += shfl_xor_f(sc0[i], m);
-      sc1[i] += shfl_xor_f(sc1[i], m);
-    }
-  if (sub == 0) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int p = pr + 16 * i;
-      if (p < n) {
-        ssc[0][p] = sc0[i];
-        ssc[1][p] = sc1[i];
-      }
+    x0 = row16_sum(x0);
+    x1 = row16_sum(x1);
+    const int p = pr + 16 * i;
+    if (sub == 0 && p < n) {
+      ssc[0][p] = x0;
+      ssc[1][p] = x1;
     }
   }
   __syncthreads();
@@ -197,9 +234,9 @@ __global__ __launch_bounds__(256) void attn_split_kernel(const AttnArgs a) {
   // ---- chunk softmax (one wave per head, one lane per position) -----------------
   if (wid < 2) {
     const float sc = lane < n ? ssc[wid][lane] : -INFINITY;
-    const float m = wave_max(sc);
+    const float m = wave_max_all(sc);
     const float e = lane < n ? exp2f(sc - m) : 0.f;
-    const float l = wave_sum(e);
+    const float l = wave_sum_all(e);
     ssc[wid][lane] = e;
     if (lane == 0) {
       sml[wid][0] = m;
@@ -225,55 +262,64 @@ __global__ __launch_bounds__(256) void attn_split_kernel(const AttnArgs a) {
       o1[e] = fmaf(e1, vf[e], o1[e]);
     }
   }
-  // lanes l, l^16, l^32, l^48 hold the same dims for different positions
 #pragma unroll
-  for (int m = 16; m <= 32; m <<= 1)
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      o0[e] += shfl_xor_f(o0[e], m);
-      o1[e] += shfl_xor_f(o1[e], m);
-    }
-  if (lane < 16) {
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      spv[wid][0][sub * 8 + e] = o0[e];
-      spv[wid][1][sub * 8 + e] = o1[e];
-    }
+  for (int e = 0; e < 8; e += 4) {
+    *reinterpret_cast<f32x4*>(&spv[pr][0][sub * 8 + e]) = f32x4{o0[e], o0[e + 1], o0[e + 2], o0[e + 3]};
+    *reinterpret_cast<f32x4*>(&spv[pr][1][sub * 8 + e]) = f32x4{o1[e], o1[e + 1], o1[e + 2], o1[e + 3]};
   }
   __syncthreads();
-  const float acc = (spv[0][hh][d] + spv[1][hh][d]) + (spv[2][hh][d] + spv[3][hh][d]);
-
-  // ---- publish the chunk partial --------------------------------------------------
-  const size_t pbase = (size_t)(b * a.qh + h) * a.nsplit_max;
-  a.part_acc[(pbase + s) * D + d] = acc;
-  if (d == 0) {
-    a.part_ml[(pbase + s) * 2 + 0] = sml[hh][0];
-    a.part_ml[(pbase + s) * 2 + 1] = sml[hh][1];
-  }
-}
-
-// Merge the chunk partials of the two q heads of one kv head.
-__global__ __launch_bounds__(256) void attn_merge_kernel(const AttnArgs a) {
-  constexpr int D = 128;
-  const int j = blockIdx.x, b = blockIdx.y, t = threadIdx.x;
-  const int pos = a.positions[b];
-  if (pos < 0 || pos >= a.max_ctx) return;  // reported by the split kernel
-  const int nsplit = (pos + kAttnChunk) / kAttnChunk;
   const int hh = t >> 7, d = t & (D - 1), h = j * 2 + hh;
+  float acc = 0.f;
+#pragma unroll
+  for (int g = 0; g < 16; ++g) acc += spv[g][hh][d];
+
+  // ---- publish the chunk partial, count in; the last block merges ---------------
   const size_t pbase = (size_t)(b * a.qh + h) * a.nsplit_max;
-  // single pass with a running maximum; loads of different chunks independent
+  if (nsplit == 1) {
+    const float r = acc / sml[hh][1];
+    const size_t oi = ((size_t)b * a.qh + h) * D + d;
+    if (a.out_dtype == Q4D_F16)
+      static_cast<_Float16*>(a.out)[oi] = (_Float16)r;
+    else
+      static_cast<float*>(a.out)[oi] = r;
+    return;
+  }
+  store_dev(&a.part_acc[(pbase + s) * D + d], acc);
+  if (d == 0) {
+    store_dev(&a.part_ml[(pbase + s) * 2 + 0], sml[hh][0]);
+    store_dev(&a.part_ml[(pbase + s) * 2 + 1], sml[hh][1]);
+  }
+  __builtin_amdgcn_s_waitcnt(0);  // this thread's stores are performed
+  __syncthreads();                 // ... and every other thread's
+  int* counter = a.counters + b * a.kvh + j;
+  if (t == 0) s_last = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == nsplit - 1;
+  __syncthreads();
+  if (!s_last) return;
+
+  // running maximum over the chunk partials; the device-scope loads of up to
+  // kMergeBatch chunks are issued together (atomic loads are not reordered,
+  // so a load-then-use loop would pay one memory round trip per chunk)
+  constexpr int kMergeBatch = 8;
   float M = -INFINITY, L = 0.f, o = 0.f;
-#pragma unroll 4
-  for (int i = 0; i < nsplit; ++i) {
-    const float mi = a.part_ml[(pbase + i) * 2];
-    const float li = a.part_ml[(pbase + i) * 2 + 1];
-    const float ai = a.part_acc[(pbase + i) * D + d];
-    const float Mn = fmaxf(M, mi);
-    const float so = M == -INFINITY ? 0.f : exp2f(M - Mn);
-    const float si = exp2f(mi - Mn);
-    L = L * so + li * si;
-    o = o * so + ai * si;
-    M = Mn;
+  for (int i0 = 0; i0 < nsplit; i0 += kMergeBatch) {
+    float mi[kMergeBatch], li[kMergeBatch], ai[kMergeBatch];
+#pragma unroll
+    for (int k = 0; k < kMergeBatch; ++k) {
+      const int i = min(i0 + k, nsplit - 1);
+      mi[k] = load_dev(&a.part_ml[(pbase + i) * 2]);
+      li[k] = load_dev(&a.part_ml[(pbase + i) * 2 + 1]);
+      ai[k] = load_dev(&a.part_acc[(pbase + i) * D + d]);
+    }
+#pragma unroll
+    for (int k = 0; k < kMergeBatch; ++k) {
+      if (i0 + k >= nsplit) break;
+      const float Mn = fmaxf(M, mi[k]);
+      const float so = M == -INFINITY ? 0.f : exp2f(M - Mn);
+      const float si = exp2f(mi[k] - Mn);
+      L = L * so + li[k] * si;
+      o = o * so + ai[k] * si;
+      M = Mn;
+    }
   }
   const float r = o / L;
   const size_t oi = ((size_t)b * a.qh + h) * D + d;
@@ -281,11 +327,14 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(const AttnArgs a) {
     static_cast<_Float16*>(a.out)[oi] = (_Float16)r;
   else
     static_cast<float*>(a.out)[oi] = r;
+  if (t == 0) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);  // next launch
 }
 
+}  // namespace
+
 int launch_attention(const AttnArgs& a, hipStream_t stream) {
-  hipLaunchKernelGGL(attn_split_kernel, dim3(a.nsplit_max, a.kvh, a.batch), dim3(256), 0, stream, a);
-  hipLaunchKernelGGL(attn_merge_kernel, dim3(a.kvh, a.batch), dim3(256), 0, stream, a);
+  if (!a.counters || !a.part_ml || !a.part_acc) return Q4D_ERR_NULL;
+  hipLaunchKernelGGL(attn_kernel, dim3(a.nsplit_max, a.kvh, a.batch), dim3(256), 0, stream, a);
   return check_launch();
 }
 

@@ -467,6 +467,7 @@ int q4d_decode_batch(const q4d_model_t* model, const int32_t* tokens, const int3
     t.nsplit_max = W.nsplit_max;
     t.part_ml = ws_ptr<float>(ws, W.part_ml);
     t.part_acc = ws_ptr<float>(ws, W.part_acc);
+    t.counters = ws_ptr<int>(ws, W.counters);
     t.out = attn;
     t.out_dtype = Q4D_F16;
     t.status = status;
