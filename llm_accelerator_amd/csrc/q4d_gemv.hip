@@ -1,18 +1,31 @@
 // Fused Q4 dequant-GEMV for gfx950 (wave64).
 //
-// Tile: one wave covers 2 rows x 1024 columns of the Q4 matrix.  Lane l
-// reads the 16-byte chunk (l % 32) of row (l / 32) of its tile, i.e. 32
-// columns, and the 32-bit word holding that chunk's Q2.14 scale, so every
-// lane issues one 128-bit weight load per tile and always sees the same 32
-// columns: its activations live in registers (XChunk) for every tile the
-// wave visits.  A matrix with K = 2048 or 3072 gives each row pair KS =
-// K / 1024 waves of one block (one 1024-column slice each); their row sums
-// are added through LDS in slice order (deterministic).  The gate/up pair of
-// the MLP is two tiles per wave (the same two rows of each matrix).
+// Two kernels share one activation prologue and one dequant trick
+// (q4d_device.h):
+//
+// gemv_kernel (one-shot; the decode-layer projections).  Tile: one wave
+// covers 2 rows x 1024 columns.  Lane l reads the 16-byte chunk (l % 32) of
+// row (l / 32), i.e. 32 columns, and the 32-bit word holding that chunk's
+// Q2.14 scale, so every lane issues one 128-bit weight load per tile.  A
+// matrix with K = 2048 or 3072 gives each row pair KS = K / 1024 waves of one
+// block (one 1024-column slice each); their row sums are added through LDS
+// in slice order (deterministic).  The gate/up pair of the MLP is two tiles
+// per wave (the same two rows of each matrix).  Each wave takes U tiles and
+// issues all their loads before consuming any.
+//
+// lm_kernel (streaming; the 151936 x 1024 LM head with fused argmax).  One
+// resident grid; each wave walks 4-row tiles grid-stride in stages of U
+// tiles with two stages in flight (ping-pong register sets, unconditional
+// reloads in the steady state).  16 lanes cover a row: lane l of row l / 16
+// holds the chunks at columns 32 (l % 16) and 512 + 32 (l % 16), so both
+// loads are fully coalesced and a row is reduced over 16 lanes.  The hi and
+// lo activation products share one accumulator per nibble position.  This
+// halves the reduction and scale work per byte of the 2-row tile, which
+// matters because the streaming kernel is bound by VALU issue, not by HBM.
 //
 // Loads are buffer loads: the matrix base is a wave-uniform resource, the
-// tile's row offset a scalar, and the lane's offset a per-lane constant, so
-// no per-load address arithmetic is spent.  Wave indices are scalar
+// tile's row offset a scalar and the lane's offset a per-lane constant, so no
+// per-load address arithmetic is spent.  Wave indices are scalar
 // (readfirstlane) and tile indices are clamped into the matrix instead of
 // guarded, so no load sits behind a divergent branch.  Activation loads go
 // out first (vmcnt retires in issue order, so waiting for the activations
@@ -21,14 +34,9 @@
 // Activations are prepared once per block in LDS: the block stages x (and
 // gamma), computes the RMSNorm where asked, and converts the vector into the
 // fp16 pair order the dequant trick consumes (hi, and lo = x - hi for ~22-bit
-// activations), with per-chunk sums; each lane then reads its ready chunk.
+// activations), with per-chunk sums; each lane then reads its ready chunks.
 // Doing this conversion per lane instead costs ~400 VALU instructions per
 // wave and dominated the decode-size GEMVs.
-//
-// One-shot kernels (the decode-layer projections) give each wave U tiles.
-// The streaming kernel (the LM head) runs one resident grid; each wave walks
-// its tiles grid-stride in stages of U tiles with two stages in flight
-// (ping-pong register sets, unconditional reloads in the steady state).
 //
 // Prologues: fp16 x, fp32 x, or RMSNorm of an fp32 hidden vector (reference
 // common.py:129-134).  Epilogues: fp16/fp32 store, residual add
@@ -50,6 +58,8 @@ namespace {
 
 constexpr int kSlice = 1024;       // columns per wave tile
 constexpr int kLmBlocksPerCU = 4;  // resident blocks per CU for the streaming kernel
+constexpr int kLmStage = 1;        // 4-row tiles per stage of the streaming kernel
+constexpr int kLmWaves = 16;       // waves per block of the streaming kernel
 constexpr int kRsrcFlags = 0x00020000;
 
 typedef __amdgpu_buffer_rsrc_t Rsrc;
@@ -65,7 +75,7 @@ struct TileData {
   uint32_t s;
 };
 
-// Per-lane constant parts of a tile load.
+// Per-lane constant parts of a one-shot tile load.
 struct LaneOff {
   uint32_t w;  // byte offset of the lane's chunk inside the tile's row pair
   uint32_t s;  // byte offset of the lane's scale word
@@ -110,10 +120,9 @@ __device__ __forceinline__ float chunk_dot_hl(const u32x4 w, const XChunk& h, co
   float a = 0.f, b = 0.f, c = 0.f, d = 0.f;
 #pragma unroll
   for (int m = 0; m < 4; ++m) {
-    const uint32_t v = w[m] ^ 0x88888888u;
-    const uint32_t t = v >> 8;
-    const uint32_t m0 = v & 0x000F000Fu, m1 = v & 0x00F000F0u;
-    const uint32_t m2 = t & 0x000F000Fu, m3 = t & 0x00F000F0u;
+    const uint32_t v = w[m], t = v >> 8;
+    const uint32_t m0 = (v ^ 0x88888888u) & 0x000F000Fu, m1 = (v ^ 0x88888888u) & 0x00F000F0u;
+    const uint32_t m2 = (t ^ 0x00888888u) & 0x000F000Fu, m3 = (t ^ 0x00888888u) & 0x00F000F0u;
     a = dot2(m0, h.p[4 * m + 0], a);
     b = dot2(m1, h.p[4 * m + 1], b);
     a = dot2(m2, h.p[4 * m + 2], a);
@@ -161,49 +170,175 @@ __device__ __forceinline__ uint32_t pack_h2(_Float16 lo, _Float16 hi) {
   return __builtin_bit_cast(uint32_t, make_h2(lo, hi));
 }
 
-template <int KS, int NWB, int XM, int XP, int EP, bool PAIR, int U, bool STREAM>
+// ---- activation prologue ------------------------------------------------------
+// LDS a block needs for K columns of activations.
+template <int K, int NWB, int XM, int XP>
+struct ActLds {
+  static constexpr int XV = (XM == X_F16) ? K / 8 : K / 4;  // 16-byte vectors of x
+  static constexpr int CH = K / 32;                         // 32-column chunks
+  f32x4 x[XV];
+  f32x4 g[XM == X_RMS ? XV : 1];
+  alignas(16) uint32_t ph[CH * 16];                // hi pairs, dequant order
+  alignas(16) uint32_t pl[XP == 2 ? CH * 16 : 4];  // lo pairs
+  float2 sm[CH];                                   // 8 * chunk sums (hi, lo)
+  float red[NWB];
+};
+
+template <int K, int NWB, int XM, int XP>
+struct ActRegs {
+  static constexpr int XV = ActLds<K, NWB, XM, XP>::XV;
+  static constexpr int XPT = (XV + NWB * 64 - 1) / (NWB * 64);  // vectors per thread
+  f32x4 x[XPT];
+  f32x4 g[XM == X_RMS ? XPT : 1];
+};
+
+// Issue this thread's activation (and gamma) loads.
+template <int K, int NWB, int XM, int XP>
+__device__ __forceinline__ void act_load(const GemvArgs& a, int bat, ActRegs<K, NWB, XM, XP>& r) {
+  using R = ActRegs<K, NWB, XM, XP>;
+#pragma unroll
+  for (int i = 0; i < R::XPT; ++i) {
+    const int v = threadIdx.x + i * NWB * 64;
+    if (v < R::XV) {
+      r.x[i] = reinterpret_cast<const f32x4*>(static_cast<const char*>(a.x) +
+                                              (size_t)bat * K * (XM == X_F16 ? 2 : 4))[v];
+      if constexpr (XM == X_RMS) r.g[i] = reinterpret_cast<const f32x4*>(a.gamma)[v];
+    }
+  }
+}
+
+// Stage x (and gamma) in LDS, reduce sum(x^2) for the RMSNorm, and convert
+// the vector into the dequant pair order.  Chunk c holds columns
+// 32c..32c+31; pair p = 4m + i of the chunk is (x[32c + 8m + i],
+// x[32c + 8m + i + 4]).  Thread q handles pairs 4m + i0 and 4m + i0 + 1 of
+// chunk q / 8 (m = (q % 8) / 2, i0 = 2 (q % 2)), so the 8 threads of a chunk
+// are 8 consecutive lanes.  Both barriers are LDS-only: the weight loads
+// issued before this stay in flight.
+template <int K, int NWB, int XM, int XP>
+__device__ __forceinline__ void act_prepare(const GemvArgs& a, const ActRegs<K, NWB, XM, XP>& r,
+                                            ActLds<K, NWB, XM, XP>& s) {
+  using R = ActRegs<K, NWB, XM, XP>;
+  constexpr int NT = NWB * 64, CH = K / 32;
+  const int lane = threadIdx.x & 63;
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < R::XPT; ++i) {
+    const int v = threadIdx.x + i * NT;
+    if (v < R::XV) {
+      s.x[v] = r.x[i];
+      if constexpr (XM == X_RMS) {
+        s.g[v] = r.g[i];
+        ss = fmaf(r.x[i][0], r.x[i][0], ss);
+        ss = fmaf(r.x[i][1], r.x[i][1], ss);
+        ss = fmaf(r.x[i][2], r.x[i][2], ss);
+        ss = fmaf(r.x[i][3], r.x[i][3], ss);
+      }
+    }
+  }
+  if constexpr (XM == X_RMS) {
+    ss = wave_sum_dpp(ss);
+    if (lane == 63) s.red[threadIdx.x >> 6] = ss;
+  }
+  block_sync_lds();
+
+  float inv_rms = 1.f;
+  if constexpr (XM == X_RMS) {
+    float tot = 0.f;
+#pragma unroll
+    for (int w = 0; w < NWB; ++w) tot += s.red[w];
+    inv_rms = 1.0f / sqrtf(tot / (float)K + a.eps);
+  }
+  const float* sxf = reinterpret_cast<const float*>(s.x);
+  const float* sgf = reinterpret_cast<const float*>(s.g);
+  const _Float16* sxh = reinterpret_cast<const _Float16*>(s.x);
+  for (int q = threadIdx.x; q < CH * 8; q += NT) {
+    const int c = q >> 3, m = (q & 7) >> 1, i0 = (q & 1) * 2;
+    const int ea = c * 32 + m * 8 + i0, eb = ea + 4;
+    _Float16 h[4];  // pairs (h[0], h[1]) and (h[2], h[3])
+    _Float16 l[4];
+    if constexpr (XM == X_F16) {
+      h[0] = sxh[ea];
+      h[1] = sxh[eb];
+      h[2] = sxh[ea + 1];
+      h[3] = sxh[eb + 1];
+    } else {
+      float v[4] = {sxf[ea], sxf[eb], sxf[ea + 1], sxf[eb + 1]};
+      if constexpr (XM == X_RMS) {
+        v[0] = (v[0] * inv_rms) * sgf[ea];
+        v[1] = (v[1] * inv_rms) * sgf[eb];
+        v[2] = (v[2] * inv_rms) * sgf[ea + 1];
+        v[3] = (v[3] * inv_rms) * sgf[eb + 1];
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        h[j] = (_Float16)v[j];
+        if constexpr (XP == 2) l[j] = (_Float16)(v[j] - (float)h[j]);
+      }
+    }
+    float sh = ((float)h[0] + (float)h[1]) + ((float)h[2] + (float)h[3]);
+    float sl = 0.f;
+    *reinterpret_cast<u32x2*>(&s.ph[c * 16 + m * 4 + i0]) = u32x2{pack_h2(h[0], h[1]), pack_h2(h[2], h[3])};
+    if constexpr (XP == 2) {
+      sl = ((float)l[0] + (float)l[1]) + ((float)l[2] + (float)l[3]);
+      *reinterpret_cast<u32x2*>(&s.pl[c * 16 + m * 4 + i0]) = u32x2{pack_h2(l[0], l[1]), pack_h2(l[2], l[3])};
+    }
+    // chunk sums over its 8 consecutive lanes
+    sh += dpp_f<kDppQuadSwap1>(sh);
+    sh += dpp_f<kDppQuadSwap2>(sh);
+    sh += dpp_f<kDppRowHalfMirror>(sh);
+    if constexpr (XP == 2) {
+      sl += dpp_f<kDppQuadSwap1>(sl);
+      sl += dpp_f<kDppQuadSwap2>(sl);
+      sl += dpp_f<kDppRowHalfMirror>(sl);
+    }
+    if ((q & 7) == 0) s.sm[c] = make_float2(8.f * sh, 8.f * sl);
+  }
+  block_sync_lds();
+}
+
+// The prepared hi (and lo) chunk c.
+template <int K, int NWB, int XM, int XP>
+__device__ __forceinline__ void act_chunk(const ActLds<K, NWB, XM, XP>& s, int c, XChunk& xh, XChunk& xl) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const u32x4 t = reinterpret_cast<const u32x4*>(&s.ph[c * 16])[j];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) xh.p[4 * j + e] = __builtin_bit_cast(h2, (uint32_t)t[e]);
+    if constexpr (XP == 2) {
+      const u32x4 t2 = reinterpret_cast<const u32x4*>(&s.pl[c * 16])[j];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) xl.p[4 * j + e] = __builtin_bit_cast(h2, (uint32_t)t2[e]);
+    }
+  }
+  const float2 sm = s.sm[c];
+  xh.sum8 = sm.x;
+  xl.sum8 = sm.y;
+}
+
+// ---- one-shot kernel ----------------------------------------------------------
+template <int KS, int NWB, int XM, int XP, int EP, bool PAIR, int U>
 __global__ __launch_bounds__(NWB * 64) void gemv_kernel(const GemvArgs a) {
   constexpr int K = KS * kSlice;
-  constexpr int NT = NWB * 64;
   constexpr int TEAMS = NWB / KS;
-  constexpr int CH = K / 32;  // 32-column chunks
   static_assert(NWB % KS == 0, "a block holds whole teams");
-  static_assert(!STREAM || (KS == 1 && !PAIR), "streaming kernel covers one K = 1024 matrix");
   static_assert(!PAIR || KS == 1, "gate/up pairs need K = 1024");
   static_assert(XM != X_F16 || XP == 1, "fp16 activations have no lo part");
+  static_assert(EP != EP_ARGMAX, "the argmax epilogue lives in lm_kernel");
   const int lane = threadIdx.x & 63;
   const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int team = wid / KS;
   const int ks = wid % KS;
   const int bat = blockIdx.y;
 
-  constexpr int XV = (XM == X_F16) ? K / 8 : K / 4;  // 16-byte vectors of x
-  constexpr int XPT = (XV + NT - 1) / NT;            // vectors per thread
-  __shared__ f32x4 s_x[XV];
-  __shared__ f32x4 s_g[XM == X_RMS ? XV : 1];
-  __shared__ float s_red[NWB];
-  __shared__ uint32_t s_ph[CH * 16];                // hi pairs, dequant order
-  __shared__ uint32_t s_pl[XP == 2 ? CH * 16 : 1];  // lo pairs
-  __shared__ float2 s_sm[CH];                       // 8 * chunk sums (hi, lo)
-  __shared__ float s_part[STREAM ? 1 : U * TEAMS * KS * 2];
-  __shared__ unsigned long long s_key[NWB];
+  __shared__ ActLds<K, NWB, XM, XP> s_act;
+  __shared__ float s_part[U * TEAMS * KS * 2];
 
   const int NP = a.rows / 2;  // tiles (row pairs; PAIR: of each matrix)
 
-  // ---- activation loads go out first ----------------------------------------
-  f32x4 xr[XPT];
-  f32x4 gr[XM == X_RMS ? XPT : 1];
-#pragma unroll
-  for (int i = 0; i < XPT; ++i) {
-    const int v = threadIdx.x + i * NT;
-    if (v < XV) {
-      xr[i] = reinterpret_cast<const f32x4*>(static_cast<const char*>(a.x) +
-                                             (size_t)bat * K * (XM == X_F16 ? 2 : 4))[v];
-      if constexpr (XM == X_RMS) gr[i] = reinterpret_cast<const f32x4*>(a.gamma)[v];
-    }
-  }
+  // ---- activation loads go out first, then every weight load -----------------
+  ActRegs<K, NWB, XM, XP> ar;
+  act_load(a, bat, ar);
 
-  // ---- then every weight load this wave can have in flight ------------------
   const int e0 = a.seg_end[0], e1 = a.seg_end[1];
   const Rsrc rw0 = make_rsrc(a.w[0], (uint32_t)e0 * (K / 2));
   const Rsrc rs0 = make_rsrc(a.s[0], (uint32_t)e0 * (K / 32));
@@ -213,15 +348,9 @@ __global__ __launch_bounds__(NWB * 64) void gemv_kernel(const GemvArgs a) {
   const Rsrc rs2 = make_rsrc(a.s[2], (uint32_t)(a.seg_end[2] - e1) * (K / 32));
   const LaneOff lo = lane_off<K>(ks, lane);
 
-  TileData A[U], B[STREAM ? U : 1], G[PAIR ? U : 1];
-  int base, step;
-  if constexpr (STREAM) {
-    base = blockIdx.x * NWB + wid;
-    step = gridDim.x * NWB;
-  } else {
-    base = blockIdx.x * TEAMS + team;
-    step = gridDim.x * TEAMS;
-  }
+  TileData A[U], G[PAIR ? U : 1];
+  const int base = blockIdx.x * TEAMS + team;
+  const int step = gridDim.x * TEAMS;
 #pragma unroll
   for (int u = 0; u < U; ++u) {
     int t = base + u * step;
@@ -233,19 +362,10 @@ __global__ __launch_bounds__(NWB * 64) void gemv_kernel(const GemvArgs a) {
       A[u] = load_tile<K>(t, lo, SEG_RS);
     }
   }
-  if constexpr (STREAM) {
-    // stage 1 goes out unconditionally (clamped): a conditional issue makes
-    // the wait-count pass assume at every later merge that it may be missing
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int t = base + (U + u) * step;
-      B[u] = load_tile<K>(t < NP ? t : NP - 1, lo, SEG_RS);
-    }
-  }
   // the residual rows this lane may own, fetched with the weights rather than
   // after the reduction (that would add a dependent memory round trip)
-  float res_pre[EP == EP_RESID && !STREAM ? U : 1];
-  if constexpr (EP == EP_RESID && !STREAM) {
+  float res_pre[EP == EP_RESID ? U : 1];
+  if constexpr (EP == EP_RESID) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int t = base + u * step;
@@ -253,244 +373,221 @@ __global__ __launch_bounds__(NWB * 64) void gemv_kernel(const GemvArgs a) {
     }
   }
 
-  // ---- stage x (and gamma) in LDS; RMS partial sums ---------------------------
-  float ss = 0.f;
-#pragma unroll
-  for (int i = 0; i < XPT; ++i) {
-    const int v = threadIdx.x + i * NT;
-    if (v < XV) {
-      s_x[v] = xr[i];
-      if constexpr (XM == X_RMS) {
-        s_g[v] = gr[i];
-        ss = fmaf(xr[i][0], xr[i][0], ss);
-        ss = fmaf(xr[i][1], xr[i][1], ss);
-        ss = fmaf(xr[i][2], xr[i][2], ss);
-        ss = fmaf(xr[i][3], xr[i][3], ss);
-      }
-    }
-  }
-  if constexpr (XM == X_RMS) {
-    ss = wave_sum_dpp(ss);
-    if (lane == 63) s_red[wid] = ss;
-  }
-  block_sync_lds();  // LDS-only: the weights stay in flight
-
-  // ---- block-cooperative conversion into the dequant pair order ---------------
-  // Chunk c holds columns 32c..32c+31; pair p = 4m + i of the chunk is
-  // (x[32c + 8m + i], x[32c + 8m + i + 4]).  Thread q handles pairs
-  // 4m + i0 and 4m + i0 + 1 of chunk q / 8 (m = (q % 8) / 2, i0 = 2 (q % 2)),
-  // so the 8 threads of a chunk are 8 consecutive lanes.
-  {
-    float inv_rms = 1.f;
-    if constexpr (XM == X_RMS) {
-      float tot = 0.f;
-#pragma unroll
-      for (int w = 0; w < NWB; ++w) tot += s_red[w];
-      inv_rms = 1.0f / sqrtf(tot / (float)K + a.eps);
-    }
-    const float* sxf = reinterpret_cast<const float*>(s_x);
-    const float* sgf = reinterpret_cast<const float*>(s_g);
-    const _Float16* sxh = reinterpret_cast<const _Float16*>(s_x);
-    for (int q = threadIdx.x; q < CH * 8; q += NT) {
-      const int c = q >> 3, m = (q & 7) >> 1, i0 = (q & 1) * 2;
-      const int ea = c * 32 + m * 8 + i0, eb = ea + 4;
-      _Float16 h[4];  // pairs (h[0], h[1]) and (h[2], h[3])
-      _Float16 l[4];
-      if constexpr (XM == X_F16) {
-        h[0] = sxh[ea];
-        h[1] = sxh[eb];
-        h[2] = sxh[ea + 1];
-        h[3] = sxh[eb + 1];
-      } else {
-        float v[4] = {sxf[ea], sxf[eb], sxf[ea + 1], sxf[eb + 1]};
-        if constexpr (XM == X_RMS) {
-          v[0] = (v[0] * inv_rms) * sgf[ea];
-          v[1] = (v[1] * inv_rms) * sgf[eb];
-          v[2] = (v[2] * inv_rms) * sgf[ea + 1];
-          v[3] = (v[3] * inv_rms) * sgf[eb + 1];
-        }
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          h[j] = (_Float16)v[j];
-          if constexpr (XP == 2) l[j] = (_Float16)(v[j] - (float)h[j]);
-        }
-      }
-      float sh = ((float)h[0] + (float)h[1]) + ((float)h[2] + (float)h[3]);
-      float sl = 0.f;
-      *reinterpret_cast<u32x2*>(&s_ph[c * 16 + m * 4 + i0]) = u32x2{pack_h2(h[0], h[1]), pack_h2(h[2], h[3])};
-      if constexpr (XP == 2) {
-        sl = ((float)l[0] + (float)l[1]) + ((float)l[2] + (float)l[3]);
-        *reinterpret_cast<u32x2*>(&s_pl[c * 16 + m * 4 + i0]) = u32x2{pack_h2(l[0], l[1]), pack_h2(l[2], l[3])};
-      }
-      // chunk sums over its 8 consecutive lanes
-      sh += dpp_f<kDppQuadSwap1>(sh);
-      sh += dpp_f<kDppQuadSwap2>(sh);
-      sh += dpp_f<kDppRowHalfMirror>(sh);
-      if constexpr (XP == 2) {
-        sl += dpp_f<kDppQuadSwap1>(sl);
-        sl += dpp_f<kDppQuadSwap2>(sl);
-        sl += dpp_f<kDppRowHalfMirror>(sl);
-      }
-      if ((q & 7) == 0) s_sm[c] = make_float2(8.f * sh, 8.f * sl);
-    }
-  }
-  block_sync_lds();
-
+  act_prepare(a, ar, s_act);
   XChunk xh, xl;
-  {
-    const int c = ks * 32 + (lane & 31);
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const u32x4 t = reinterpret_cast<const u32x4*>(&s_ph[c * 16])[j];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) xh.p[4 * j + e] = __builtin_bit_cast(h2, (uint32_t)t[e]);
-      if constexpr (XP == 2) {
-        const u32x4 t2 = reinterpret_cast<const u32x4*>(&s_pl[c * 16])[j];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) xl.p[4 * j + e] = __builtin_bit_cast(h2, (uint32_t)t2[e]);
-      }
-    }
-    const float2 sm = s_sm[c];
-    xh.sum8 = sm.x;
-    xl.sum8 = sm.y;
-  }
-  // keep the activation reads ahead of the first weight use
+  act_chunk(s_act, ks * 32 + (lane & 31), xh, xl);
+  // keep the activation reads ahead of the first weight use: left to itself
+  // the scheduler hoists weight arithmetic above them, so the wave would wait
+  // for the weights first and build the activations afterwards
   __builtin_amdgcn_sched_barrier(0);
 
   const bool owner = (lane & 31) == 31;
   const int r = lane >> 5;
-  const int sshift = lo.sshift;
+  float rs[U], rg[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    rs[u] = tile_rows<XP>(A[u], lo.sshift, xh, xl);
+    if constexpr (PAIR) rg[u] = tile_rows<XP>(G[u], lo.sshift, xh, xl);
+  }
+  if constexpr (KS > 1) {
+    if (owner) {
+#pragma unroll
+      for (int u = 0; u < U; ++u) s_part[((u * TEAMS + team) * KS + ks) * 2 + r] = rs[u];
+    }
+    __syncthreads();
+    if (ks != 0) return;
+    if (owner) {
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        float v = s_part[((u * TEAMS + team) * KS) * 2 + r];
+#pragma unroll
+        for (int k = 1; k < KS; ++k) v += s_part[((u * TEAMS + team) * KS + k) * 2 + r];
+        rs[u] = v;
+      }
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int t = base + u * step;
+    if (t >= NP) break;
+    const float v = rs[u];
+    if (owner) {
+      const size_t o = (size_t)bat * a.rows + 2 * t + r;
+      if constexpr (EP == EP_SWIGLU) {
+        static_cast<float*>(a.y)[o] = (v / (1.0f + expf(-v))) * rg[u];
+      } else if constexpr (EP == EP_F16) {
+        static_cast<_Float16*>(a.y)[o] = (_Float16)v;
+      } else if constexpr (EP == EP_F32) {
+        static_cast<float*>(a.y)[o] = v;
+      } else if constexpr (EP == EP_RESID) {
+        static_cast<float*>(a.y)[o] = res_pre[u] + v;
+      }
+    }
+  }
+}
 
-  if constexpr (!STREAM) {
-    // ---- one-shot: U tiles, slices combined through LDS when KS > 1 ---------
-    float rs[U], rg[U];
+// ---- streaming LM-head kernel -------------------------------------------------
+// One 4-row tile for one lane: two weight chunks (512 columns apart) and the
+// scale word of one of their groups (the neighbour lane holds the other).
+struct Tile4 {
+  u32x4 w0, w1;
+  uint32_t s;
+};
+
+// sum_j q_j x_j over one 32-column chunk times the chunk's scale code, hi and
+// lo products in shared accumulators.  s8 = (8 * sum of hi + lo) * 2^-14.
+template <int XP>
+__device__ __forceinline__ float chunk_scaled(const u32x4 w, const XChunk& h, const XChunk& l, float s8,
+                                              float code) {
+  float a = 0.f, b = 0.f;
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    // shift first, then xor+and in one 3-input op each (5 VALU per word)
+    const uint32_t v = w[m], t = v >> 8;
+    const uint32_t m0 = (v ^ 0x88888888u) & 0x000F000Fu, m1 = (v ^ 0x88888888u) & 0x00F000F0u;
+    const uint32_t m2 = (t ^ 0x00888888u) & 0x000F000Fu, m3 = (t ^ 0x00888888u) & 0x00F000F0u;
+    a = dot2(m0, h.p[4 * m + 0], a);
+    b = dot2(m1, h.p[4 * m + 1], b);
+    a = dot2(m2, h.p[4 * m + 2], a);
+    b = dot2(m3, h.p[4 * m + 3], b);
+    if constexpr (XP == 2) {
+      a = dot2(m0, l.p[4 * m + 0], a);
+      b = dot2(m1, l.p[4 * m + 1], b);
+      a = dot2(m2, l.p[4 * m + 2], a);
+      b = dot2(m3, l.p[4 * m + 3], b);
+    }
+  }
+  // (2^24 a + 2^20 b - 8 sum x) * code * 2^-14
+  return code * fmaf(fmaf(a, 16.f, b), 64.f, -s8);
+}
+
+template <int XP, int U, int NWB>
+__global__ __launch_bounds__(NWB * 64) void lm_kernel(const GemvArgs a) {
+  constexpr int K = 1024;
+  const int lane = threadIdx.x & 63;
+  const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+
+  __shared__ ActLds<K, NWB, X_RMS, XP> s_act;
+  __shared__ unsigned long long s_key[NWB];
+
+  const int R = a.rows;
+  const int NT4 = (R + 3) / 4;  // 4-row tiles; the last one is moved back to rows R-4..R-1
+
+  ActRegs<K, NWB, X_RMS, XP> ar;
+  act_load(a, 0, ar);
+
+  const Rsrc rw = make_rsrc(a.w[0], (uint32_t)R * (K / 2));
+  const Rsrc rsc = make_rsrc(a.s[0], (uint32_t)R * (K / 32));
+  const int r = lane >> 4, sub = lane & 15;
+  const uint32_t vw = (uint32_t)(r * (K / 2) + sub * 16);
+  const int g0 = sub >> 1;  // group of chunk 0; chunk 1 is in group 8 + g0
+  const uint32_t vs = (uint32_t)(r * (K / 32) + 4 * ((lane & 1) ? 4 + (g0 >> 1) : (g0 >> 1)));
+  const int sshift = (g0 & 1) * 16;
+  const bool even = (lane & 1) == 0;
+
+  auto load4 = [&](int t) {
+    t = t < NT4 ? t : NT4 - 1;
+    const int row0 = min(4 * t, R - 4);
+    Tile4 d;
+    d.w0 = __builtin_amdgcn_raw_buffer_load_b128(rw, vw, (uint32_t)row0 * (K / 2), 0);
+    d.w1 = __builtin_amdgcn_raw_buffer_load_b128(rw, vw + 256, (uint32_t)row0 * (K / 2), 0);
+    d.s = __builtin_amdgcn_raw_buffer_load_b32(rsc, vs, (uint32_t)row0 * (K / 32), 0);
+    return d;
+  };
+
+  const int base = blockIdx.x * NWB + wid;
+  const int step = gridDim.x * NWB;
+  Tile4 A[U], B[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) A[u] = load4(base + u * step);
+  // stage 1 goes out unconditionally (clamped): a conditional issue makes the
+  // wait-count pass assume at every later merge that it may be missing
+#pragma unroll
+  for (int u = 0; u < U; ++u) B[u] = load4(base + (U + u) * step);
+
+  act_prepare(a, ar, s_act);
+  XChunk xh0, xl0, xh1, xl1;
+  act_chunk(s_act, sub, xh0, xl0);
+  act_chunk(s_act, 16 + sub, xh1, xl1);
+  const float s80 = (xh0.sum8 + (XP == 2 ? xl0.sum8 : 0.f)) * (1.0f / 16384.0f);
+  const float s81 = (xh1.sum8 + (XP == 2 ? xl1.sum8 : 0.f)) * (1.0f / 16384.0f);
+  __builtin_amdgcn_sched_barrier(0);
+
+  float best = -INFINITY;
+  int besti = 0x7fffffff;
+  auto consume = [&](const Tile4 (&D)[U], int first) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      rs[u] = tile_rows<XP>(A[u], sshift, xh, xl);
-      if constexpr (PAIR) rg[u] = tile_rows<XP>(G[u], sshift, xh, xl);
-    }
-    if constexpr (KS > 1) {
-      if (owner) {
-#pragma unroll
-        for (int u = 0; u < U; ++u) s_part[((u * TEAMS + team) * KS + ks) * 2 + r] = rs[u];
-      }
-      __syncthreads();
-      if (ks != 0) return;
-      if (owner) {
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-          float v = s_part[((u * TEAMS + team) * KS) * 2 + r];
-#pragma unroll
-          for (int k = 1; k < KS; ++k) v += s_part[((u * TEAMS + team) * KS + k) * 2 + r];
-          rs[u] = v;
+      const int t = first + u * step;
+      // the even lane of a pair loaded chunk 0's scale word, the odd lane chunk 1's
+      const uint32_t other = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)D[u].s, kDppQuadSwap1, 0xF, 0xF, false);
+      const uint32_t w0s = even ? D[u].s : other, w1s = even ? other : D[u].s;
+      const float c0 = (float)((w0s >> sshift) & 0xFFFFu);
+      const float c1 = (float)((w1s >> sshift) & 0xFFFFu);
+      float p = chunk_scaled<XP>(D[u].w0, xh0, xl0, s80, c0) + chunk_scaled<XP>(D[u].w1, xh1, xl1, s81, c1);
+      p = row16_sum(p);
+      if (t < NT4 && sub == 15) {
+        const int row = min(4 * t, R - 4) + r;
+        if (a.logits) a.logits[row] = p;
+        // rows rise along a lane's sequence: strict > keeps the lowest index
+        // among equal scores
+        if (p > best) {
+          best = p;
+          besti = row;
         }
       }
     }
+  };
+  // S stages of U tiles per wave (uniform over the grid; the host sizes the
+  // grid so that S >= 2 wherever the matrix allows).  Steady state: both
+  // reloads are unconditional, so each consume waits only for its own stage.
+  const int S = (NT4 + U * step - 1) / (U * step);
+  auto reload = [&](Tile4 (&D)[U], int st) {
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int t = base + u * step;
-      if (t >= NP) break;
-      const float v = rs[u];
-      if (owner) {
-        const size_t o = (size_t)bat * a.rows + 2 * t + r;
-        if constexpr (EP == EP_SWIGLU) {
-          static_cast<float*>(a.y)[o] = (v / (1.0f + expf(-v))) * rg[u];
-        } else if constexpr (EP == EP_F16) {
-          static_cast<_Float16*>(a.y)[o] = (_Float16)v;
-        } else if constexpr (EP == EP_F32) {
-          static_cast<float*>(a.y)[o] = v;
-        } else if constexpr (EP == EP_RESID) {
-          static_cast<float*>(a.y)[o] = res_pre[u] + v;
-        }
-      }
-    }
-  } else {
-    // ---- streaming: two stages of U tiles in flight (A, B ping-pong) --------
-    float best = -INFINITY;
-    int besti = 0x7fffffff;
-    auto consume = [&](const TileData (&D)[U], int first) {
-#pragma unroll
-      for (int u = 0; u < U; ++u) {
-        const int t = first + u * step;
-        const float v = tile_rows<XP>(D[u], sshift, xh, xl);
-        if (t < NP && owner) {
-          const int row = 2 * t + r;
-          if constexpr (EP == EP_ARGMAX) {
-            if (a.logits) a.logits[row] = v;
-            // rows rise along a lane's sequence: strict > keeps the lowest
-            // index among equal scores
-            if (v > best) {
-              best = v;
-              besti = row;
-            }
-          } else {
-            const size_t o = (size_t)bat * a.rows + row;
-            if constexpr (EP == EP_F16)
-              static_cast<_Float16*>(a.y)[o] = (_Float16)v;
-            else
-              static_cast<float*>(a.y)[o] = v;
-          }
-        }
-      }
-    };
-    // S stages of U tiles per wave (uniform over the grid; the host sizes the
-    // grid so that S >= 2 wherever the matrix allows).  Steady state: both
-    // reloads are unconditional, so each consume waits only for its own stage.
-    const int S = (NP + U * step - 1) / (U * step);
-    auto reload = [&](TileData (&D)[U], int st) {
-#pragma unroll
-      for (int u = 0; u < U; ++u) {
-        const int t = base + (st * U + u) * step;
-        D[u] = load_tile<K>(t < NP ? t : NP - 1, lo, SEG_RS);
-      }
-    };
-    int st = 0;
-    for (; st + 3 < S; st += 2) {
-      consume(A, base + st * U * step);
-      reload(A, st + 2);
-      consume(B, base + (st + 1) * U * step);
-      reload(B, st + 3);
-    }
+    for (int u = 0; u < U; ++u) D[u] = load4(base + (st * U + u) * step);
+  };
+  int st = 0;
+  for (; st + 3 < S; st += 2) {
     consume(A, base + st * U * step);
-    if (st + 2 < S) {
-      reload(A, st + 2);
-      consume(B, base + (st + 1) * U * step);
-      consume(A, base + (st + 2) * U * step);
-    } else {
-      consume(B, base + (st + 1) * U * step);  // may lie wholly past the matrix
-    }
+    reload(A, st + 2);
+    consume(B, base + (st + 1) * U * step);
+    reload(B, st + 3);
+  }
+  consume(A, base + st * U * step);
+  if (st + 2 < S) {
+    reload(A, st + 2);
+    consume(B, base + (st + 1) * U * step);
+    consume(A, base + (st + 2) * U * step);
+  } else {
+    consume(B, base + (st + 1) * U * step);  // may lie wholly past the matrix
+  }
 
-    if constexpr (EP == EP_ARGMAX) {
-      unsigned long long key = argmax_key(best, besti);
+  unsigned long long key = argmax_key(best, besti);
 #pragma unroll
-      for (int m = 32; m >= 1; m >>= 1) {
-        const unsigned long long o = __shfl_xor(key, m, kWave);
-        key = o > key ? o : key;
-      }
-      if (lane == 0) s_key[wid] = key;
-      __syncthreads();
-      if (threadIdx.x == 0) {
-        unsigned long long bk = s_key[0];
+  for (int m = 32; m >= 1; m >>= 1) {
+    const unsigned long long o = __shfl_xor(key, m, kWave);
+    key = o > key ? o : key;
+  }
+  if (lane == 0) s_key[wid] = key;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    unsigned long long bk = s_key[0];
 #pragma unroll
-        for (int w = 1; w < NWB; ++w) bk = s_key[w] > bk ? s_key[w] : bk;
-        // fold in, wait for the atomic to be performed, then count in
-        const unsigned long long old =
-            __hip_atomic_fetch_max(a.lm_key, bk, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        asm volatile("" ::"v"((uint32_t)old), "v"((uint32_t)(old >> 32)) : "memory");
-        const int done = __hip_atomic_fetch_add(a.counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if (done == (int)gridDim.x - 1) {
-          const unsigned long long fin =
-              __hip_atomic_fetch_max(a.lm_key, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-          float sc;
-          int ix;
-          argmax_unkey(fin, &sc, &ix);
-          a.out_token[0] = ix;
-          a.out_score[0] = sc;
-          // ready for the next launch (stream order makes these visible to it)
-          __hip_atomic_store(a.lm_key, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-          __hip_atomic_store(a.counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
-      }
+    for (int w = 1; w < NWB; ++w) bk = s_key[w] > bk ? s_key[w] : bk;
+    // fold in, wait for the atomic to be performed, then count in
+    const unsigned long long old = __hip_atomic_fetch_max(a.lm_key, bk, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    asm volatile("" ::"v"((uint32_t)old), "v"((uint32_t)(old >> 32)) : "memory");
+    const int done = __hip_atomic_fetch_add(a.counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (done == (int)gridDim.x - 1) {
+      const unsigned long long fin = __hip_atomic_fetch_max(a.lm_key, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      float sc;
+      int ix;
+      argmax_unkey(fin, &sc, &ix);
+      a.out_token[0] = ix;
+      a.out_score[0] = sc;
+      // ready for the next launch (stream order makes these visible to it)
+      __hip_atomic_store(a.lm_key, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(a.counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   }
 }
@@ -510,25 +607,31 @@ int resident_blocks(F kernel, int threads) {
   return cached;
 }
 
-template <int KS, int NWB, int XM, int XP, int EP, bool PAIR, int U, bool STREAM>
+template <int XP>
+int launch_lm(const GemvArgs& a, hipStream_t stream) {
+  constexpr int U = kLmStage, NWB = kLmWaves;
+  if (a.rows < 4) return Q4D_ERR_SHAPE;
+  const int NT4 = (a.rows + 3) / 4;
+  // stages per wave over the resident grid (at least 2), then the smallest
+  // grid covering the matrix in that many stages (few clamped tail tiles)
+  const int res = resident_blocks(lm_kernel<XP, U, NWB>, NWB * 64);
+  const long per_stage = (long)res * NWB * U;
+  int S = (int)((NT4 + per_stage - 1) / per_stage);
+  if (S < 2) S = 2;
+  int blocks = (int)((NT4 + (long)NWB * U * S - 1) / ((long)NWB * U * S));
+  if (blocks < 1) blocks = 1;
+  hipLaunchKernelGGL((lm_kernel<XP, U, NWB>), dim3(blocks), dim3(NWB * 64), 0, stream, a);
+  return check_launch();
+}
+
+template <int KS, int NWB, int XM, int XP, int EP, bool PAIR, int U>
 int launch_inst(const GemvArgs& a, hipStream_t stream) {
   constexpr int TEAMS = NWB / KS;
   const int NP = a.rows / 2;
-  int blocks;
-  if constexpr (STREAM) {
-    // stages per wave over the resident grid (at least 2), then the smallest
-    // grid covering the matrix in that many stages (few clamped tail tiles)
-    const int res = resident_blocks(gemv_kernel<KS, NWB, XM, XP, EP, PAIR, U, STREAM>, NWB * 64);
-    const long per_stage = (long)res * NWB * U;
-    int S = (int)((NP + per_stage - 1) / per_stage);
-    if (S < 2) S = 2;
-    blocks = (int)((NP + (long)NWB * U * S - 1) / ((long)NWB * U * S));
-  } else {
-    blocks = (NP + TEAMS * U - 1) / (TEAMS * U);
-  }
+  int blocks = (NP + TEAMS * U - 1) / (TEAMS * U);
   if (blocks < 1) blocks = 1;
   dim3 grid(blocks, a.batch);
-  hipLaunchKernelGGL((gemv_kernel<KS, NWB, XM, XP, EP, PAIR, U, STREAM>), grid, dim3(NWB * 64), 0, stream, a);
+  hipLaunchKernelGGL((gemv_kernel<KS, NWB, XM, XP, EP, PAIR, U>), grid, dim3(NWB * 64), 0, stream, a);
   return check_launch();
 }
 
@@ -542,9 +645,10 @@ constexpr int nwb_of() {
 template <int KS, int XM, int XP, int EP, bool PAIR>
 int launch_sel(const GemvArgs& a, hipStream_t st) {
   if constexpr (EP == EP_ARGMAX) {
-    return launch_inst<1, 4, XM, XP, EP, false, 4, true>(a, st);
+    static_assert(KS == 1 && XM == X_RMS, "LM head: K = 1024 with the final RMSNorm");
+    return launch_lm<XP>(a, st);
   } else {
-    return launch_inst<KS, nwb_of<KS>(), XM, XP, EP, PAIR, 1, false>(a, st);
+    return launch_inst<KS, nwb_of<KS>(), XM, XP, EP, PAIR, 1>(a, st);
   }
 }
 
@@ -603,7 +707,7 @@ int launch_gemv_xp(const GemvArgs& a, int xm, int xp, int ep, bool pair, hipStre
   if (ep == EP_RESID && !a.resid) return Q4D_ERR_NULL;
   if (ep == EP_ARGMAX && (!a.lm_key || !a.counter || !a.out_token || !a.out_score || a.batch != 1))
     return Q4D_ERR_NULL;
-  if (ep == EP_ARGMAX && !aligned(a.lm_key, 8)) return Q4D_ERR_BAD_ADDR;
+  if (ep == EP_ARGMAX && (!aligned(a.lm_key, 8) || a.nseg != 1)) return Q4D_ERR_BAD_ADDR;
   if (xm == X_F16 && xp != 1) return Q4D_ERR_DTYPE;
   // unused segments: empty ranges on segment 0's memory, never selected
   GemvArgs b = a;
