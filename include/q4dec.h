@@ -232,6 +232,19 @@ int q4d_run_one_token(const q4d_model_t* model, const int32_t* tokens, const int
 int q4d_decode_batch(const q4d_model_t* model, const int32_t* tokens, const int32_t* positions,
                      int32_t batch, const q4d_kv_cache_t* kv, int32_t* next_tokens, float* scores,
                      float* logits, void* ws, size_t ws_bytes, void* stream);
+/* Bytes of workspace q4d_prefill needs for up to `max_tokens` tokens per call. */
+size_t q4d_prefill_workspace_bytes(const q4d_model_t* model, int32_t max_tokens);
+/* Prefill: n_tokens tokens (device int32 [n_tokens]) of sequence `seq` of the cache at positions
+ * start_pos .. start_pos + n_tokens - 1, through embedding, all layers and the LM head of the last
+ * token.  Appends the K/V rows of every position (attention over [0, position] for each token) and
+ * writes next_token[0] / score[0] (and logits [vocab] if not NULL) for the last token.  Equals
+ * n_tokens consecutive run_manual_one_token steps
+ * (10_validate_full_run_one_token.py:17-56, driven as in :81-135) with the projections as MFMA
+ * GEMMs (activations rounded to fp16) and causal attention on MFMA (q and probabilities in fp16).
+ * Positions must satisfy start_pos + n_tokens <= max_ctx (Q4D_ERR_CONTEXT otherwise). */
+int q4d_prefill(const q4d_model_t* model, const int32_t* tokens, int32_t n_tokens, int32_t start_pos,
+                int32_t seq, const q4d_kv_cache_t* kv, int32_t* next_token, float* score, float* logits,
+                void* ws, size_t ws_bytes, void* stream);
 /* Advance a device-resident decode loop: tokens[0] = next_token[0], positions[0] += 1, and,
  * if hist_tokens is not NULL and *hist_count < hist_capacity, record next_token[0] and score[0]
  * at index *hist_count and increment it.  Lets a captured graph replay q4d_run_one_token

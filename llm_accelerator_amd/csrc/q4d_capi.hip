@@ -550,6 +550,99 @@ int q4d_run_one_token(const q4d_model_t* model, const int32_t* tokens, const int
   return run_lm_head(model, hidden, next_token, score, logits, ws, W, st);
 }
 
+size_t q4d_prefill_workspace_bytes(const q4d_model_t* model, int32_t max_tokens) {
+  if (!model || max_tokens <= 0) return 0;
+  return prefill_layout(model, max_tokens).total;
+}
+
+int q4d_prefill(const q4d_model_t* model, const int32_t* tokens, int32_t n_tokens, int32_t start_pos,
+                int32_t seq, const q4d_kv_cache_t* kv, int32_t* next_token, float* score, float* logits, void* ws,
+                size_t ws_bytes, void* stream) {
+  if (!tokens || !next_token || !score) return Q4D_ERR_NULL;
+  int rc = check_model(model);
+  if (rc) return rc;
+  if (n_tokens <= 0) return Q4D_ERR_SHAPE;
+  if ((rc = check_kv(kv, model, 1))) return rc;
+  if (seq < 0 || seq >= kv->batch) return Q4D_ERR_CAPACITY;
+  if (start_pos < 0 || (long long)start_pos + n_tokens > model->max_ctx) return Q4D_ERR_CONTEXT;
+  if (!ws) return Q4D_ERR_NULL;
+  if (!aligned(ws, 256)) return Q4D_ERR_BAD_ADDR;
+  const PrefillLayout P = prefill_layout(model, n_tokens);
+  if (ws_bytes < P.total) return Q4D_ERR_CAPACITY;
+  hipStream_t st = as_stream(stream);
+  const int n = n_tokens, H = model->hidden_size, I = model->intermediate_size;
+  const int qh = model->num_q_heads, kvh = model->num_kv_heads, d = model->head_dim;
+  float* hidden = ws_ptr<float>(ws, P.hidden);
+  uint16_t* xh = ws_ptr<uint16_t>(ws, P.xh);
+  float* qkv = ws_ptr<float>(ws, P.qkv);
+  uint16_t* act = ws_ptr<uint16_t>(ws, P.act);
+  if ((rc = launch_embedding(&model->embed_tokens, tokens, n, hidden, ws_ptr<int32_t>(ws, P.base.status), st)))
+    return rc;
+  const size_t seq_off = (size_t)seq * kvh * kv->max_ctx * d;
+  for (int l = 0; l < model->num_layers; ++l) {
+    const q4d_layer_t& L = model->layers[l];
+    // input RMSNorm -> fp16, then q|k|v as one three-segment GEMM
+    if ((rc = launch_rms_norm(hidden, L.input_layernorm, model->rms_norm_eps, n, H, xh, Q4D_F16, st))) return rc;
+    GemmArgs g;
+    memset(&g, 0, sizeof(g));
+    g.w[0] = L.q_proj.w; g.s[0] = L.q_proj.s;
+    g.w[1] = L.k_proj.w; g.s[1] = L.k_proj.s;
+    g.w[2] = L.v_proj.w; g.s[2] = L.v_proj.s;
+    g.seg_end[0] = L.q_proj.rows;
+    g.seg_end[1] = g.seg_end[0] + L.k_proj.rows;
+    g.seg_end[2] = g.seg_end[1] + L.v_proj.rows;
+    g.nseg = 3;
+    g.N = g.seg_end[2]; g.K = H; g.M = n;
+    g.x = xh; g.y = qkv; g.ldy = g.N;
+    if ((rc = launch_gemm(g, EP_F32, false, st))) return rc;
+
+    // q/k RMSNorm + RoPE, K/V append for all n positions, causal GQA attention
+    PrefillArgs pa;
+    memset(&pa, 0, sizeof(pa));
+    pa.qkv = qkv;
+    pa.q_gamma = L.q_norm;
+    pa.k_gamma = L.k_norm;
+    pa.eps = model->rms_norm_eps;
+    pa.qscale = model->attn_scaling * 1.4426950408889634f;
+    pa.rope_cos = model->rope_cos;
+    pa.rope_sin = model->rope_sin;
+    uint16_t *kp, *vp;
+    kv_planes(kv, l, &kp, &vp);
+    pa.kcache = kp + seq_off;
+    pa.vcache = vp + seq_off;
+    pa.q16 = ws_ptr<_Float16>(ws, P.q16);
+    pa.out = ws_ptr<_Float16>(ws, P.attn);
+    pa.n = n; pa.p0 = start_pos; pa.qh = qh; pa.kvh = kvh; pa.max_ctx = model->max_ctx;
+    if ((rc = launch_prefill_rope(pa, st))) return rc;
+    if ((rc = launch_prefill_attention(pa, st))) return rc;
+
+    // o_proj + residual, post-attention RMSNorm, gate/up + SwiGLU, down + residual
+    memset(&g, 0, sizeof(g));
+    g.w[0] = L.o_proj.w; g.s[0] = L.o_proj.s;
+    g.seg_end[0] = H; g.nseg = 1;
+    g.N = H; g.K = qh * d; g.M = n;
+    g.x = ws_ptr<uint16_t>(ws, P.attn); g.y = hidden; g.ldy = H; g.resid = hidden;
+    if ((rc = launch_gemm(g, EP_RESID, false, st))) return rc;
+    if ((rc = launch_rms_norm(hidden, L.post_attention_layernorm, model->rms_norm_eps, n, H, xh, Q4D_F16, st)))
+      return rc;
+    memset(&g, 0, sizeof(g));
+    g.w[0] = L.gate_proj.w; g.s[0] = L.gate_proj.s;
+    g.w[1] = L.up_proj.w;   g.s[1] = L.up_proj.s;
+    g.seg_end[0] = I; g.seg_end[1] = 2 * I; g.nseg = 2;
+    g.N = I; g.K = H; g.M = n;
+    g.x = xh; g.y = act; g.ldy = I;
+    if ((rc = launch_gemm(g, EP_SWIGLU, true, st))) return rc;
+    memset(&g, 0, sizeof(g));
+    g.w[0] = L.down_proj.w; g.s[0] = L.down_proj.s;
+    g.seg_end[0] = H; g.nseg = 1;
+    g.N = H; g.K = I; g.M = n;
+    g.x = act; g.y = hidden; g.ldy = H; g.resid = hidden;
+    if ((rc = launch_gemm(g, EP_RESID, false, st))) return rc;
+  }
+  // final RMSNorm + LM head + argmax for the last token
+  return run_lm_head(model, hidden + (size_t)(n - 1) * H, next_token, score, logits, ws, P.base, st);
+}
+
 int q4d_advance(int32_t* tokens, int32_t* positions, const int32_t* next_token, const float* score,
                 int32_t* hist_tokens, float* hist_scores, int32_t* hist_count, int32_t hist_capacity,
                 void* stream) {

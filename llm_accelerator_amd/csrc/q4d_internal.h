@@ -167,6 +167,54 @@ int launch_gemm(const GemmArgs& a, int ep, bool pair, hipStream_t st);
 int launch_argmax_rows(const float* part_score, const int* part_idx, int nparts, int M, int32_t* out_token,
                        float* out_score, hipStream_t st);
 
+// ---- prefill (many tokens of one sequence) ---------------------------------------
+struct PrefillArgs {
+  const float* qkv;        // [n][qh + 2 kvh][head_dim] fp32 raw projections
+  const float* q_gamma;
+  const float* k_gamma;
+  float eps;
+  float qscale;            // attention scaling * log2(e), folded into q
+  const float* rope_cos;   // [max_ctx][head_dim / 2]
+  const float* rope_sin;
+  uint16_t* kcache;        // K plane of the layer and sequence: [kvh][max_ctx][head_dim] fp16
+  uint16_t* vcache;
+  _Float16* q16;           // [qh][n][head_dim] normed, roped, pre-scaled q
+  _Float16* out;           // [n][qh * head_dim] attention output
+  int n, p0, qh, kvh, max_ctx;
+};
+int launch_prefill_rope(const PrefillArgs& a, hipStream_t st);
+int launch_prefill_attention(const PrefillArgs& a, hipStream_t st);
+
+// Prefill workspace: the single-token layout (status, counters, LM-head argmax)
+// followed by the per-token buffers.
+struct PrefillLayout {
+  WsLayout base;
+  size_t hidden;  // f32 [n][hidden]
+  size_t xh;      // f16 [n][max(hidden, intermediate)]
+  size_t qkv;     // f32 [n][(qh + 2 kvh) * d]
+  size_t q16;     // f16 [qh][n][d]
+  size_t attn;    // f16 [n][qh * d]
+  size_t act;     // f16 [n][intermediate]
+  size_t total;
+};
+
+inline PrefillLayout prefill_layout(const q4d_model_t* m, int n) {
+  PrefillLayout P{};
+  P.base = ws_layout(m, 1);
+  const size_t A = 256;
+  const int d = m->head_dim, qh = m->num_q_heads, kvh = m->num_kv_heads;
+  const int wx = m->hidden_size > m->intermediate_size ? m->hidden_size : m->intermediate_size;
+  size_t o = align_up(P.base.total, A);
+  P.hidden = o; o = align_up(o + (size_t)n * m->hidden_size * 4, A);
+  P.xh = o;     o = align_up(o + (size_t)n * wx * 2, A);
+  P.qkv = o;    o = align_up(o + (size_t)n * (qh + 2 * kvh) * d * 4, A);
+  P.q16 = o;    o = align_up(o + (size_t)qh * n * d * 2, A);
+  P.attn = o;   o = align_up(o + (size_t)n * qh * d * 2, A);
+  P.act = o;    o = align_up(o + (size_t)n * m->intermediate_size * 2, A);
+  P.total = o;
+  return P;
+}
+
 int launch_fill_i32(int32_t* p, int32_t v, size_t n, hipStream_t stream);
 int launch_advance(int32_t* tokens, int32_t* positions, const int32_t* next_token, const float* score,
                    int32_t* hist_tokens, float* hist_scores, int32_t* hist_count, int32_t hist_capacity,

@@ -1,0 +1,247 @@
+// Prefill of many tokens of one sequence (gfx950): the per-token q/k RMSNorm,
+// RoPE and KV-cache append for all tokens, and causal GQA attention on MFMA.
+//
+// The reference's prefill is serial: run_manual_one_token once per prompt
+// token (10_validate_full_run_one_token.py:81-135), each call appending one
+// K/V row and attending over the cache (common.py:231-298).  Here the n new
+// tokens at positions p0 .. p0 + n - 1 go through each layer together; the
+// projections are Q4 GEMMs (q4d_gemm.hip) and this file supplies the rest.
+//
+// prefill_rope_kernel: one wave per (token, row) where the rows of a token
+// are its 16 q heads, 8 k heads and 8 v heads.  Lane l holds dims l and
+// l + 64 (each other's rotate-half partner), so per-head RMSNorm
+// (common.py:258-262) and RoPE (common.py:264-268) are wave-local.  q goes
+// to an fp16 [q_head][token][128] buffer with the softmax scale and log2(e)
+// folded in; k (normed, roped) and v go to the fp16 KV cache at their
+// positions (append_cache, common.py:186-189).
+//
+// prefill_attn_kernel: flash attention forward, causal, one block per
+// (64-query tile, q head), 4 waves of 16 queries.  Per 64-key tile:
+//   S^T = K . Q^T (16x16x32 f16 MFMA; K rows straight from the cache tile
+//   in LDS, Q^T from registers); online softmax per query (exp2);
+//   O^T += V^T . P^T, where the S^T accumulator layout is already the B
+//   operand layout of P^T (each lane holds 4 keys of two 16-key tiles for one
+//   query), so P never leaves registers.  V is transposed into LDS as it is
+//   staged: each thread loads a 4-key x 8-dim block, transposes it in
+//   registers and writes 8-byte rows of V^T.
+// Row strides of the LDS tiles (136 and 72 fp16) put every LDS access at
+// its minimum number of bank passes.
+#include <math.h>
+
+#include "q4d_device.h"
+#include "q4d_internal.h"
+
+namespace q4d {
+
+namespace {
+
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+
+constexpr int kD = 128;
+constexpr int kBQ = 64;   // queries per block
+constexpr int kBK = 64;   // keys per tile
+constexpr int kLdk = kD + 8;    // fp16 row stride of the K tile
+constexpr int kLdv = kBK + 8;   // fp16 row stride of the V^T tile
+
+__device__ __forceinline__ float wave_sum_bcast(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wave_sum_dpp(v)), 63));
+}
+
+__global__ __launch_bounds__(256) void prefill_rope_kernel(const PrefillArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int rows_per_tok = a.qh + 2 * a.kvh;
+  const int tok = row / rows_per_tok, r = row % rows_per_tok;
+  if (tok >= a.n) return;
+  const int pos = a.p0 + tok;
+  const float* src = a.qkv + (size_t)tok * rows_per_tok * kD + (size_t)r * kD;
+  const float x0 = src[lane], x1 = src[lane + 64];
+  if (r >= a.qh + a.kvh) {  // v head: fp16 into the cache
+    const int j = r - a.qh - a.kvh;
+    uint16_t* dst = a.vcache + ((size_t)j * a.max_ctx + pos) * kD;
+    dst[lane] = __builtin_bit_cast(uint16_t, (_Float16)x0);
+    dst[lane + 64] = __builtin_bit_cast(uint16_t, (_Float16)x1);
+    return;
+  }
+  const bool isq = r < a.qh;
+  const float* gam = isq ? a.q_gamma : a.k_gamma;
+  const float c = a.rope_cos[(size_t)pos * (kD / 2) + lane];
+  const float sn = a.rope_sin[(size_t)pos * (kD / 2) + lane];
+  const float ss = wave_sum_bcast(fmaf(x0, x0, x1 * x1));
+  const float inv = 1.0f / sqrtf(ss / (float)kD + a.eps);
+  const float n0 = (x0 * inv) * gam[lane], n1 = (x1 * inv) * gam[lane + 64];
+  // rotate_half: dim d < 64 takes -x[d + 64], dim d >= 64 takes x[d - 64]
+  const float r0 = n0 * c + (-n1) * sn;
+  const float r1 = n1 * c + n0 * sn;
+  if (isq) {
+    _Float16* dst = a.q16 + ((size_t)r * a.n + tok) * kD;
+    dst[lane] = (_Float16)(r0 * a.qscale);
+    dst[lane + 64] = (_Float16)(r1 * a.qscale);
+  } else {
+    uint16_t* dst = a.kcache + ((size_t)(r - a.qh) * a.max_ctx + pos) * kD;
+    dst[lane] = __builtin_bit_cast(uint16_t, (_Float16)r0);
+    dst[lane + 64] = __builtin_bit_cast(uint16_t, (_Float16)r1);
+  }
+}
+
+// Global loads of one K/V tile: thread (kq = t & 15, dc = t >> 4) holds keys
+// 4kq .. 4kq+3, dims 8dc .. 8dc+7 of K and of V.
+struct KVRegs {
+  u32x4 k[4], v[4];
+};
+
+__device__ __forceinline__ void load_kv(const uint16_t* kb, const uint16_t* vb, int key0, int kend, int t,
+                                        KVRegs& R) {
+  const int kq = t & 15, dc = t >> 4;
+#pragma unroll
+  for (int b = 0; b < 4; ++b) {
+    int key = key0 + 4 * kq + b;
+    key = key < kend ? key : kend - 1;  // rows past the end are masked out of the softmax
+    R.k[b] = *reinterpret_cast<const u32x4*>(kb + (size_t)key * kD + dc * 8);
+    R.v[b] = *reinterpret_cast<const u32x4*>(vb + (size_t)key * kD + dc * 8);
+  }
+}
+
+__device__ __forceinline__ void store_kv(const KVRegs& R, int t, _Float16 (*Ks)[kLdk], _Float16 (*Vt)[kLdv]) {
+  const int kq = t & 15, dc = t >> 4;
+#pragma unroll
+  for (int b = 0; b < 4; ++b) *reinterpret_cast<u32x4*>(&Ks[4 * kq + b][dc * 8]) = R.k[b];
+  // transpose the 4-key x 8-dim block: dim e of keys 4kq..4kq+3 -> one 8-byte row piece
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const int wrd = e >> 1, hi = e & 1;
+    const uint32_t sel = hi ? 0x07060302u : 0x05040100u;  // high or low halves of (src0, src1)
+    const uint32_t k01 = __builtin_amdgcn_perm(R.v[1][wrd], R.v[0][wrd], sel);
+    const uint32_t k23 = __builtin_amdgcn_perm(R.v[3][wrd], R.v[2][wrd], sel);
+    *reinterpret_cast<u32x2*>(&Vt[dc * 8 + e][4 * kq]) = u32x2{k01, k23};
+  }
+}
+
+__global__ __launch_bounds__(256) void prefill_attn_kernel(const PrefillArgs a) {
+  __shared__ _Float16 Ks[kBK][kLdk];
+  __shared__ _Float16 Vt[kD][kLdv];
+
+  const int t = threadIdx.x, lane = t & 63;
+  const int w = __builtin_amdgcn_readfirstlane(t >> 6);
+  // heavier (later) query tiles first
+  const int qt = (int)gridDim.x - 1 - (int)blockIdx.x;
+  const int h = blockIdx.y, j = h / (a.qh / a.kvh);
+  const int i0 = qt * kBQ;                 // first query (token index) of the block
+  const int q_lo = i0 + 16 * w;            // first query of this wave
+  const int kend = a.p0 + min(a.n, i0 + kBQ);  // keys [0, kend) can be attended by the block
+  const int ntiles = (kend + kBK - 1) / kBK;
+  const uint16_t* kb = a.kcache + (size_t)j * a.max_ctx * kD;
+  const uint16_t* vb = a.vcache + (size_t)j * a.max_ctx * kD;
+
+  // Q^T operand: lane (n = query q_lo + (l & 15), quarter l >> 4) holds dims 32s + 8q .. +7
+  const int qn = lane & 15, qq = lane >> 4;
+  const int my_q = q_lo + qn;            // token index of this lane's query column
+  const int my_pos = a.p0 + my_q;        // its position
+  h8 qop[4];
+  {
+    const int qrow = my_q < a.n ? my_q : a.n - 1;
+    const _Float16* qp = a.q16 + ((size_t)h * a.n + qrow) * kD;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) qop[s] = *reinterpret_cast<const h8*>(qp + 32 * s + 8 * qq);
+  }
+
+  f32x4 o[8];
+#pragma unroll
+  for (int dt = 0; dt < 8; ++dt) o[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float m_run = -INFINITY, l_run = 0.f;  // per query column (replicated over the 4 quarters)
+
+  KVRegs R;
+  load_kv(kb, vb, 0, kend, t, R);
+  for (int kt = 0; kt < ntiles; ++kt) {
+    __syncthreads();  // the previous tile's LDS reads are done
+    store_kv(R, t, Ks, Vt);
+    __syncthreads();
+    if (kt + 1 < ntiles) load_kv(kb, vb, (kt + 1) * kBK, kend, t, R);
+
+    // S^T tile: 64 keys x 16 queries, 4 D tiles of 16 keys
+    f32x4 st[4];
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) {
+      st[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const h8 kop = *reinterpret_cast<const h8*>(&Ks[16 * mt + qn][32 * s + 8 * qq]);
+        st[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kop, qop[s], st[mt], 0, 0, 0);
+      }
+    }
+    // causal / range mask: lane holds keys kt*64 + 16mt + 4qq + i for query my_pos
+    const int kbase = kt * kBK + 4 * qq;
+    float tmax = -INFINITY;
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int key = kbase + 16 * mt + i;
+        if (key > my_pos || key >= kend) st[mt][i] = -INFINITY;
+        tmax = fmaxf(tmax, st[mt][i]);
+      }
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 16, kWave));
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 32, kWave));
+    const float m_new = fmaxf(m_run, tmax);
+    // m_new is finite once the query has seen key 0 (always in the first tile)
+    const float alpha = exp2f(m_run - m_new);
+    m_run = m_new;
+    float psum = 0.f;
+    h4 p[4];
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float e = exp2f(st[mt][i] - m_new);
+        psum += e;
+        p[mt][i] = (_Float16)e;
+      }
+    l_run = l_run * alpha + psum;
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) o[dt] *= alpha;
+    // O^T += V^T . P^T over two 32-key steps
+#pragma unroll
+    for (int s2 = 0; s2 < 2; ++s2) {
+      const h8 pop = __builtin_shufflevector(p[2 * s2], p[2 * s2 + 1], 0, 1, 2, 3, 4, 5, 6, 7);
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt) {
+        const h4 va = *reinterpret_cast<const h4*>(&Vt[16 * dt + qn][32 * s2 + 4 * qq]);
+        const h4 vb2 = *reinterpret_cast<const h4*>(&Vt[16 * dt + qn][32 * s2 + 16 + 4 * qq]);
+        const h8 vop = __builtin_shufflevector(va, vb2, 0, 1, 2, 3, 4, 5, 6, 7);
+        o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vop, pop, o[dt], 0, 0, 0);
+      }
+    }
+  }
+
+  // ---- normalise and store: lane holds O^T[d = 16dt + 4qq + i][query my_q] ---------
+  float l_tot = l_run;
+  l_tot += __shfl_xor(l_tot, 16, kWave);
+  l_tot += __shfl_xor(l_tot, 32, kWave);
+  if (my_q < a.n) {
+    const float inv = 1.0f / l_tot;
+    _Float16* out = a.out + (size_t)my_q * a.qh * kD + (size_t)h * kD;
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) {
+      h4 v;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) v[i] = (_Float16)(o[dt][i] * inv);
+      *reinterpret_cast<h4*>(out + 16 * dt + 4 * qq) = v;
+    }
+  }
+}
+
+}  // namespace
+
+int launch_prefill_rope(const PrefillArgs& a, hipStream_t st) {
+  const int rows = a.n * (a.qh + 2 * a.kvh);
+  hipLaunchKernelGGL(prefill_rope_kernel, dim3((rows + 3) / 4), dim3(256), 0, st, a);
+  return check_launch();
+}
+
+int launch_prefill_attention(const PrefillArgs& a, hipStream_t st) {
+  hipLaunchKernelGGL(prefill_attn_kernel, dim3((a.n + kBQ - 1) / kBQ, a.qh), dim3(256), 0, st, a);
+  return check_launch();
+}
+
+}  // namespace q4d

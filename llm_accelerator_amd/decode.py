@@ -42,6 +42,7 @@ class GreedyDecoder:
         self._desc = model.descriptor()
         self._kvd = self.kv.descriptor()
         self._lib = _lib.load()
+        self._prefill = None
         self.position = 0
 
     # -- one step, launched on the current stream ---------------------------------
@@ -73,12 +74,28 @@ class GreedyDecoder:
         self._launch_step(logits, record)
         self.position += 1
 
-    def prefill(self, prompt: list[int]) -> None:
-        """Serial prefill: one full step per prompt token; only the step after
-        the last prompt token records its argmax as generated token 0."""
+    def prefill(self, prompt: list[int], parallel: bool = False) -> None:
+        """Serial prefill (default): one full step per prompt token, as the
+        reference does; only the step after the last prompt token records its
+        argmax as generated token 0.  ``parallel=True`` runs all prompt tokens
+        through each layer at once (q4d_prefill: MFMA GEMMs and causal
+        attention), then records the same generated token 0."""
         self.reset()
-        for i, t in enumerate(prompt):
-            self.step(int(t), record=(i == len(prompt) - 1))
+        if not parallel:
+            for i, t in enumerate(prompt):
+                self.step(int(t), record=(i == len(prompt) - 1))
+            return
+        if not prompt or len(prompt) > self.model.max_ctx:
+            raise _lib.Q4DecError(-10, "GreedyDecoder.prefill")
+        if self._prefill is None or self._prefill.max_tokens < len(prompt):
+            self._prefill = Prefill(self.model, self.kv, max(len(prompt), 64))
+        self._prefill.run(prompt, start_pos=0, seq=0, next_token=self.next_tok, score=self.score)
+        # q4d_advance feeds the argmax back at position len(prompt) and records it
+        self.pos.fill_(len(prompt) - 1)
+        check(self._lib.q4d_advance(self.tok.data_ptr(), self.pos.data_ptr(), self.next_tok.data_ptr(),
+                                    self.score.data_ptr(), self.hist_tok.data_ptr(), self.hist_score.data_ptr(),
+                                    self.hist_count.data_ptr(), self.hist_cap, current_stream()), "q4d_advance")
+        self.position = len(prompt)
 
     def _capture(self) -> None:
         s = torch.cuda.Stream()
@@ -120,6 +137,50 @@ class GreedyDecoder:
         check(self._lib.q4d_read_status(self.ws.ptr, self.ws.nbytes, ctypes.byref(self._desc), 1, ctypes.byref(out),
                                         current_stream()), "q4d_read_status")
         return out.value
+
+
+class Prefill:
+    """Many tokens of one sequence through every layer at once (q4d_prefill).
+
+    Per token the result is ``run_manual_one_token`` at that token's position
+    (``10_validate_full_run_one_token.py:17-56``; the reference feeds a prompt
+    through it one token at a time, ``:81-135``): every position's K/V row is
+    appended to the cache and the argmax after the last token is returned.
+    The projections run as MFMA GEMMs over the tokens (activations rounded to
+    fp16) and attention is causal flash attention on MFMA.
+    """
+
+    def __init__(self, model: Q4ForCausalLM, kv: KVCache, max_tokens: int):
+        self.model, self.kv, self.max_tokens = model, kv, int(max_tokens)
+        self._desc = model.descriptor()
+        self._kvd = kv.descriptor()
+        lib = _lib.load()
+        self.nbytes = int(lib.q4d_prefill_workspace_bytes(ctypes.byref(self._desc), self.max_tokens))
+        if self.nbytes == 0:
+            raise _lib.Q4DecError(-11, "q4d_prefill_workspace_bytes")
+        self.buf = torch.empty(self.nbytes, dtype=torch.uint8, device=model.device)
+        check(lib.q4d_workspace_init(self.buf.data_ptr(), self.nbytes, ctypes.byref(self._desc), 1,
+                                     current_stream()), "q4d_workspace_init")
+        self.tokens = torch.zeros(self.max_tokens, dtype=torch.int32, device=model.device)
+
+    def run(self, tokens, start_pos: int = 0, seq: int = 0, next_token: torch.Tensor | None = None,
+            score: torch.Tensor | None = None, logits: torch.Tensor | None = None):
+        """tokens: list of ids or a device int32 tensor.  Returns (next_token, score) device tensors."""
+        n = len(tokens)
+        if n > self.max_tokens:
+            raise _lib.Q4DecError(-9, "Prefill.run")
+        if isinstance(tokens, torch.Tensor) and tokens.is_cuda and tokens.dtype == torch.int32:
+            self.tokens[:n].copy_(tokens)
+        else:
+            self.tokens[:n].copy_(torch.as_tensor([int(t) for t in tokens], dtype=torch.int32))
+        dev = self.model.device
+        next_token = next_token if next_token is not None else torch.zeros(1, dtype=torch.int32, device=dev)
+        score = score if score is not None else torch.zeros(1, dtype=torch.float32, device=dev)
+        check(_lib.load().q4d_prefill(ctypes.byref(self._desc), self.tokens.data_ptr(), n, int(start_pos), int(seq),
+                                      ctypes.byref(self._kvd), next_token.data_ptr(), score.data_ptr(),
+                                      logits.data_ptr() if logits is not None else None, self.buf.data_ptr(),
+                                      self.nbytes, current_stream()), "q4d_prefill")
+        return next_token, score
 
 
 def greedy_generate(model: Q4ForCausalLM, prompt: list[int], max_new_tokens: int, use_graph: bool = True,
