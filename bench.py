@@ -13,10 +13,17 @@ cache-resident rate (one layer repeated) is reported beside it.
 scales, K/V read of 512 positions, new K/V row, hidden in/out) / step time.
 Steps run as HIP-graph replays of ``--copies`` captured layer steps.
 
-Also reported (same run): the 3072x1024 Q4 GEMV (config 1) GB/s flushed and
-resident, full 28-layer greedy decode tok/s (config 3: 64-token prompt, 256
-generated), the roofline of the dominant kernel (gate/up GEMV + SwiGLU)
-from HIP events, and the oracle's CPU rate on the host cores.
+``roofline`` is that of the dominant kernel of the layer step (the stage
+with the largest time, HIP events around graph replays of that stage alone):
+its algorithmic bytes per launch (model.stage_bytes_layer) over its average
+launch time; every stage's rate is listed beside it.
+
+Also reported (same run, under "extras"): the 3072x1024 Q4 GEMV (config 1)
+GB/s flushed and resident; the LM head alone; full 28-layer greedy decode
+tok/s (config 3: 64-token prompt, 256 generated); prefill of one 2048-token
+sequence (config 4: tok/s and TFLOP/s against the dense fp16 MFMA peak);
+batched decode of 64 sequences over 4096 cached positions (config 5: tok/s
+and GB/s of K/V + weights); and the oracle's CPU rate on the host cores.
 """
 
 from __future__ import annotations
@@ -30,7 +37,13 @@ import sys
 import time
 
 METRIC = "Q4 GEMV HBM GB/s (% peak) + batch-1 decode tok/s, Qwen3-0.6B-Q4"
+MFMA_PEAK_TFLOPS = 2500.0  # dense fp16
+STAGE_KERNELS = {"qkv": "input RMSNorm + q|k|v Q4 GEMV", "attention": "q/k norm + RoPE + KV append + split-K GQA attention",
+                 "o_proj": "o_proj Q4 GEMV + residual", "gate_up": "post-norm + gate/up Q4 GEMV + SwiGLU",
+                 "down": "down Q4 GEMV + residual"}
 HBM_PEAK_GBPS = 8000.0
+C4_TOKENS = 2048             # prefill of one 2048-token sequence
+C5_BATCH, C5_CTX = 64, 4096  # batched decode: 64 sequences over 4096 cached positions
 
 
 def log(*a):
@@ -153,10 +166,12 @@ def main():
         g.replay()
         stage_us[sname] = time_graph(g, max(1, args.steps // copies), torch) / copies * 1e3
     log(f"[bench] stage us (flushed): {json.dumps({k: round(v, 2) for k, v in stage_us.items()})}")
-    h, i_sz = 1024, 3072
-    gate_up_bytes = 2 * (i_sz * h // 2 + 2 * i_sz * h // 64) + 2 * h + 2 * i_sz
-    achieved = gate_up_bytes / (stage_us["gate_up"] * 1e-6) / 1e9
-    # HBM bytes per launch of this kernel, measured with rocprofv3 FETCH_SIZE /
+    # roofline of the dominant kernel (the slowest stage of the layer step):
+    # algorithmic bytes per launch in the dtypes each kernel reads and writes
+    stage_bytes = M.stage_bytes_layer(M.Qwen3Config(), ctx)
+    stage_rate = {k: stage_bytes[k] / (stage_us[k] * 1e-6) / 1e9 for k in stage_names}
+    dom = max(stage_names, key=lambda k: stage_us[k])
+    # HBM bytes per launch of that kernel, measured with rocprofv3 FETCH_SIZE /
     # WRITE_SIZE (copy-calibrated) and committed under profiles/
     traffic, traffic_src = None, None
     tfile = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
@@ -164,13 +179,14 @@ def main():
     if os.path.exists(tfile) and args.precision == 2:
         with open(tfile) as f:
             tj = json.load(f)
-        ent = tj["kernels"].get("void q4d::gemv_kernel<1024, 2, 2, 2, 3, true>")
+        ent = tj["stages"].get(dom) if "stages" in tj else None
         if ent:
             traffic, traffic_src = ent["total_bytes"], tj["source"]
-    roofline = {"bound": "hbm", "kernel": "gemv_kernel<1024,2,X_RMS,*,EP_SWIGLU,pair> (post-norm + gate/up + SwiGLU)",
-                "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": traffic, "traffic_source": traffic_src,
-                "bytes_per_launch": gate_up_bytes, "avg_launch_us": round(stage_us["gate_up"], 3)}
+    roofline = {"bound": "hbm", "kernel": f"{dom} stage ({STAGE_KERNELS[dom]})",
+                "achieved": round(stage_rate[dom], 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                "frac": round(stage_rate[dom] / HBM_PEAK_GBPS, 4), "traffic": traffic, "traffic_source": traffic_src,
+                "bytes_per_launch": stage_bytes[dom], "avg_launch_us": round(stage_us[dom], 3),
+                "per_stage_GBps": {k: round(v, 1) for k, v in stage_rate.items()}}
 
     extras = {"c2_resident_GBps": round(resident, 1), "c2_resident_us_per_step": round(res_ms * 1e3, 3),
               "c2_flushed_us_per_step": round(ms_per_step * 1e3, 3), "stage_us_flushed": stage_us}
@@ -209,7 +225,7 @@ def main():
         fcfg = M.Qwen3Config()
         t = time.time()
         fhost = M.random_host_weights(fcfg, seed=0)
-        fmodel = M.build_model(fcfg, fhost, max_ctx=64 + args.decode_gen + 16, device=dev)
+        fmodel = M.build_model(fcfg, fhost, max_ctx=max(64 + args.decode_gen + 16, C5_CTX + 1), device=dev)
         del fhost
         log(f"[bench] C3 setup {time.time() - t:.1f}s")
         prompt = np.random.default_rng(1).integers(0, fcfg.vocab_size, 64).tolist()
@@ -255,7 +271,56 @@ def main():
                                "hbm_frac": round(tok_bytes * tok_s / 1e9 / HBM_PEAK_GBPS, 4),
                                "status": dec.status()}
         log(f"[bench] C3 decode: {json.dumps(extras['c3_decode'])}")
-        del fmodel, dec
+        del dec, lws
+        torch.cuda.empty_cache()
+
+        # -------------------------------------------------------- C4 prefill
+        from llm_accelerator_amd.decode import BatchedDecoder, Prefill
+        T = C4_TOKENS
+        pkv = M.KVCache(fcfg, fcfg.num_hidden_layers, 1, fmodel.max_ctx, dev)
+        pf = Prefill(fmodel, pkv, T)
+        ptok = torch.from_numpy(np.random.default_rng(4).integers(0, fcfg.vocab_size, T).astype(np.int32)).to(dev)
+        pf.run(ptok)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(5):
+            pf.run(ptok)
+        e1.record()
+        torch.cuda.synchronize()
+        pms = e0.elapsed_time(e1) / 5
+        pflops = M.prefill_flops(fcfg, T)
+        extras["c4_prefill"] = {"tokens": T, "ms": round(pms, 3), "tok_s": round(T / pms * 1e3, 1),
+                                "TFLOPs": round(pflops / pms / 1e9, 1), "flops": pflops,
+                                "mfma_frac": round(pflops / pms / 1e9 / MFMA_PEAK_TFLOPS, 4)}
+        log(f"[bench] C4 prefill: {json.dumps(extras['c4_prefill'])}")
+        del pkv, pf
+        torch.cuda.empty_cache()
+
+        # -------------------------------------------------------- C5 batched decode
+        B = C5_BATCH
+        bkv = M.KVCache(fcfg, fcfg.num_hidden_layers, B, C5_CTX + 1, dev)
+        bkv.data[..., :C5_CTX, :].normal_(generator=gen)
+        bd = BatchedDecoder(fmodel, B, bkv)
+        btok = torch.from_numpy(np.random.default_rng(3).integers(0, fcfg.vocab_size, B).astype(np.int32)).to(dev)
+        bpos = torch.full((B,), C5_CTX, dtype=torch.int32, device=dev)
+        bd.step(btok, bpos)
+        torch.cuda.synchronize()
+        e0.record()
+        for _ in range(5):
+            bd.step(btok, bpos)
+        e1.record()
+        torch.cuda.synchronize()
+        bms = e0.elapsed_time(e1) / 5
+        bbytes = M.batched_step_bytes(fcfg, B, C5_CTX)
+        extras["c5_batched_decode"] = {"batch": B, "ctx": C5_CTX, "ms_per_step": round(bms, 3),
+                                       "tok_s": round(B / bms * 1e3, 1), "bytes_per_step": bbytes,
+                                       "GBps": round(bbytes / bms / 1e6, 1),
+                                       "hbm_frac": round(bbytes / bms / 1e6 / HBM_PEAK_GBPS, 4),
+                                       "status": bd.status()}
+        log(f"[bench] C5 batched decode: {json.dumps(extras['c5_batched_decode'])}")
+        del bkv, bd
+        del fmodel
         torch.cuda.empty_cache()
 
     if args.copy_calibration:

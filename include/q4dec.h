@@ -206,8 +206,10 @@ int q4d_decoder_layer(const q4d_model_t* model, int32_t layer, const float* hidd
  * stages follow the per-layer QMAP stage boundaries of the hardware path
  * (qot_layer_qmap_bases_t, qmap_one_token_runtime.h:31-42):
  *   Q4D_STAGE_QKV       input RMSNorm + q|k|v projection      -> workspace qkv
- *   Q4D_STAGE_ATTENTION q/k RMSNorm + RoPE + KV append + GQA attention -> workspace attn
- *   Q4D_STAGE_O_PROJ    o_proj + residual: hidden_out = hidden_in + W_o attn
+ *   Q4D_STAGE_ATTENTION q/k RMSNorm + RoPE + KV append + split-K GQA attention -> workspace
+ *                       chunk partials (max, sum, partial output per 128-position chunk)
+ *   Q4D_STAGE_O_PROJ    merge of the chunk partials + o_proj + residual:
+ *                       hidden_out = hidden_in + W_o attn
  *   Q4D_STAGE_GATE_UP   post-attention RMSNorm(hidden_out) + gate/up + SiLU*up -> workspace act
  *   Q4D_STAGE_DOWN      down_proj + residual: hidden_out += W_d act
  * Running the five stages in order equals one q4d_decoder_layer call. */

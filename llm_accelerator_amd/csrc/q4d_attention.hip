@@ -8,9 +8,9 @@
 //
 // One kernel, split-K over the context (flash-decoding style): grid
 // (chunk, kv_head, batch), 256 threads per block; a block takes the two q
-// heads of one kv head over kAttnChunk (= 64) positions.
-//  - Thread t owns dims 8*(t%16)..+7 of positions t/16 + 16*i (i < 4) for
-//    both K and V and issues its eight 16-byte loads first, so a chunk costs
+// heads of one kv head over CH (64 or 128) positions.
+//  - Thread t owns dims 8*(t%16)..+7 of positions t/16 + 16*i (i < CH/16) for
+//    both K and V and issues all its 16-byte loads first, so a chunk costs
 //    one memory round trip.
 //  - Waves 0/1 prepare q head 2j / 2j+1, waves 2/3 the new k / v row: lane l
 //    holds dims l and l + 64, which are also each other's rotate-half
@@ -20,12 +20,17 @@
 //  - Scores are 8-dim partial dots reduced over the 16 lanes of a position
 //    (DPP); the chunk softmax runs in one wave per head (exp2, log2e folded
 //    into q); P.V partials are reduced over positions through LDS.
-//  - The chunk's (max, sum, partial output) is published with device-scope
-//    atomic stores; after they complete the block counts in on a per-(kv
-//    head, sequence) counter, and the block that completes the count merges
-//    all chunks, reading them back with device-scope atomic loads.  The
-//    counter atomic is issued only after the stores are performed, so no
-//    fence (an L2 write-back on this part) and no second launch is needed.
+//  - merge = 1 (64-position chunks): the chunk's (max, sum, partial output)
+//    is published with device-scope atomic stores; after they complete the
+//    block counts in on a per-(kv head, sequence) counter, and the block that
+//    completes the count merges all chunks, reading them back with
+//    device-scope atomic loads.  The counter atomic is issued only after the
+//    stores are performed, so no fence (an L2 write-back on this part) and no
+//    second launch is needed.
+//  - merge = 0 (128-position chunks, the batch-1 decode layer): the partials
+//    are plain stores and the next kernel (the o_proj GEMV) merges them in its
+//    prologue, which removes the store / count / reload round trips from the
+//    critical path.
 // The block owning the new position appends its K/V row (append_cache,
 // common.py:186-189) and takes that row from LDS rather than from its own
 // global write.
@@ -36,7 +41,7 @@
 
 namespace q4d {
 
-static_assert(kAttnChunk == 64, "thread mapping assumes 64 positions per chunk");
+static_assert(kAttnChunk == 64 && kAttnChunkLong == 128, "thread mapping assumes 64 or 128 positions per chunk");
 
 namespace {
 
@@ -78,8 +83,11 @@ __device__ __forceinline__ float load_dev(const float* p) {
   return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// CH positions per chunk (64 or 128); thread t owns positions t/16 + 16 i, i < CH/16.
+template <int CH>
 __global__ __launch_bounds__(256) void attn_kernel(const AttnArgs a) {
   constexpr int D = 128;
+  constexpr int NPT = CH / 16;  // positions per thread
   const int s = blockIdx.x, j = blockIdx.y, b = blockIdx.z;
   const int t = threadIdx.x, lane = t & 63;
   const int wid = __builtin_amdgcn_readfirstlane(t >> 6);
@@ -89,10 +97,10 @@ __global__ __launch_bounds__(256) void attn_kernel(const AttnArgs a) {
     return;
   }
   const int T = pos + 1;
-  const int nsplit = (T + kAttnChunk - 1) / kAttnChunk;
+  const int nsplit = (T + CH - 1) / CH;
   if (s >= nsplit) return;
-  const int start = s * kAttnChunk;
-  const int n = min(T, start + kAttnChunk) - start;
+  const int start = s * CH;
+  const int n = min(T, start + CH) - start;
   // positions below `cached` are read from the cache; in fused mode the new
   // position pos is produced here
   const int cached = a.fused ? pos : T;
@@ -100,7 +108,7 @@ __global__ __launch_bounds__(256) void attn_kernel(const AttnArgs a) {
 
   __shared__ float sq[2][D];
   __shared__ uint16_t snew[2][D];  // fp16 bits of the appended k (roped) and v
-  __shared__ float ssc[2][kAttnChunk];
+  __shared__ float ssc[2][CH];
   __shared__ float sml[2][2];
   __shared__ float spv[16][2][D];  // P.V partials per position row group
   __shared__ int s_last;
@@ -118,43 +126,46 @@ __global__ __launch_bounds__(256) void attn_kernel(const AttnArgs a) {
   const int qkv_stride = (a.qh + 2 * a.kvh) * D;
   const bool qk_wave = a.fused ? (wid < 2 || (last && wid == 2)) : (wid < 2);
   const bool v_wave = a.fused && last && wid == 3;
-  float x0 = 0.f, x1 = 0.f, c = 0.f, sn = 0.f, g0 = 0.f, g1 = 0.f;
+  // Every wave loads unconditionally (pointers chosen by wave-uniform selects;
+  // unused roles read valid memory): loads behind role branches make the
+  // compiler wait for them at the join, before the K/V loads are issued.
+  const float* row;
+  const float* gam;
+  const float* ctab;
+  const float* stab;
   if (a.fused) {
     const float* src = a.qkv + (size_t)b * qkv_stride;
-    if (qk_wave) {
-      const float* row = wid < 2 ? src + (j * 2 + wid) * D : src + (a.qh + j) * D;
-      const float* gam = wid < 2 ? a.q_gamma : a.k_gamma;
-      x0 = row[lane];
-      x1 = row[lane + 64];
-      c = a.rope_cos[(size_t)pos * (D / 2) + lane];
-      sn = a.rope_sin[(size_t)pos * (D / 2) + lane];
-      g0 = gam[lane];
-      g1 = gam[lane + 64];
-    } else if (v_wave) {
-      const float* row = src + (a.qh + a.kvh + j) * D;
-      x0 = row[lane];
-      x1 = row[lane + 64];
-    }
-  } else if (qk_wave) {
-    const float* qh = a.q + ((size_t)b * a.qh + j * 2 + wid) * D;
-    x0 = qh[lane];
-    x1 = qh[lane + 64];
+    const int ridx = wid < 2 ? j * 2 + wid : (wid == 2 ? a.qh + j : a.qh + a.kvh + j);
+    row = src + (size_t)ridx * D;
+    gam = wid < 2 ? a.q_gamma : a.k_gamma;
+    ctab = a.rope_cos + (size_t)pos * (D / 2);
+    stab = a.rope_sin + (size_t)pos * (D / 2);
+  } else {
+    row = a.q + ((size_t)b * a.qh + j * 2 + (wid < 2 ? wid : 1)) * D;
+    gam = ctab = stab = row;
   }
+  const float x0 = row[lane], x1 = row[lane + 64];
+  const float g0 = gam[lane], g1 = gam[lane + 64];
+  const float c = ctab[lane], sn = stab[lane];
+  // keep these loads ahead of the K/V loads (vmcnt retires in issue order)
+  __builtin_amdgcn_sched_barrier(0);
 
   // ---- then every K/V load of this chunk ------------------------------------
   const int sub = t & 15;  // dims 8*sub .. 8*sub+7
   const int pr = t >> 4;   // positions pr + 16*i
-  u32x4 kr[4], vr[4];
+  // Rows past the cached ones are loaded from the last cached row (or row 0)
+  // instead of being guarded: a guarded load makes the compiler wait for each
+  // load before issuing the next.  Those positions get zero softmax weight
+  // and the row holds finite cached values; position pos (fused mode) is
+  // replaced from LDS below.
+  u32x4 kr[NPT], vr[NPT];
+  const int plast = cached > 0 ? cached - 1 : 0;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int p = start + pr + 16 * i;
-    if (p < cached) {
-      kr[i] = *reinterpret_cast<const u32x4*>(kb + (size_t)p * D + sub * 8);
-      vr[i] = *reinterpret_cast<const u32x4*>(vb + (size_t)p * D + sub * 8);
-    } else {
-      kr[i] = u32x4{0u, 0u, 0u, 0u};
-      vr[i] = u32x4{0u, 0u, 0u, 0u};
-    }
+  for (int i = 0; i < NPT; ++i) {
+    int p = start + pr + 16 * i;
+    p = p < cached ? p : plast;
+    kr[i] = *reinterpret_cast<const u32x4*>(kb + (size_t)p * D + sub * 8);
+    vr[i] = *reinterpret_cast<const u32x4*>(vb + (size_t)p * D + sub * 8);
   }
 
   // ---- per-head RMSNorm (common.py:258-262) + rotate-half RoPE (264-268) -------
@@ -196,7 +207,7 @@ __global__ __launch_bounds__(256) void attn_kernel(const AttnArgs a) {
       const u32x4 kn4 = *reinterpret_cast<const u32x4*>(&snew[0][sub * 8]);
       const u32x4 vn4 = *reinterpret_cast<const u32x4*>(&snew[1][sub * 8]);
 #pragma unroll
-      for (int ii = 0; ii < 4; ++ii)
+      for (int ii = 0; ii < NPT; ++ii)
         if (ii == i) {
           kr[ii] = kn4;
           vr[ii] = vn4;
@@ -212,7 +223,7 @@ __global__ __launch_bounds__(256) void attn_kernel(const AttnArgs a) {
     q1[e] = sq[1][sub * 8 + e];
   }
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
+  for (int i = 0; i < NPT; ++i) {
     float kf[8];
     unpack8(kr[i], kf);
     float x0 = 0.f, x1 = 0.f;
@@ -233,11 +244,24 @@ __global__ __launch_bounds__(256) void attn_kernel(const AttnArgs a) {
 
   // ---- chunk softmax (one wave per head, one lane per position) -----------------
   if (wid < 2) {
-    const float sc = lane < n ? ssc[wid][lane] : -INFINITY;
-    const float m = wave_max_all(sc);
-    const float e = lane < n ? exp2f(sc - m) : 0.f;
-    const float l = wave_sum_all(e);
-    ssc[wid][lane] = e;
+    float sc[CH / 64];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int k = 0; k < CH / 64; ++k) {
+      const int p = lane + 64 * k;
+      sc[k] = p < n ? ssc[wid][p] : -INFINITY;
+      mx = fmaxf(mx, sc[k]);
+    }
+    const float m = wave_max_all(mx);
+    float es = 0.f;
+#pragma unroll
+    for (int k = 0; k < CH / 64; ++k) {
+      const int p = lane + 64 * k;
+      const float e = p < n ? exp2f(sc[k] - m) : 0.f;
+      ssc[wid][p] = e;
+      es += e;
+    }
+    const float l = wave_sum_all(es);
     if (lane == 0) {
       sml[wid][0] = m;
       sml[wid][1] = l;
@@ -250,7 +274,7 @@ __global__ __launch_bounds__(256) void attn_kernel(const AttnArgs a) {
 #pragma unroll
   for (int e = 0; e < 8; ++e) o0[e] = o1[e] = 0.f;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
+  for (int i = 0; i < NPT; ++i) {
     const int p = pr + 16 * i;
     const float e0 = p < n ? ssc[0][p] : 0.f;
     const float e1 = p < n ? ssc[1][p] : 0.f;
@@ -275,6 +299,15 @@ __global__ __launch_bounds__(256) void attn_kernel(const AttnArgs a) {
 
   // ---- publish the chunk partial, count in; the last block merges ---------------
   const size_t pbase = (size_t)(b * a.qh + h) * a.nsplit_max;
+  if (!a.merge) {
+    // partials for the consumer; the kernel boundary makes them visible
+    a.part_acc[(pbase + s) * D + d] = acc;
+    if (d == 0) {
+      a.part_ml[(pbase + s) * 2 + 0] = sml[hh][0];
+      a.part_ml[(pbase + s) * 2 + 1] = sml[hh][1];
+    }
+    return;
+  }
   if (nsplit == 1) {
     const float r = acc / sml[hh][1];
     const size_t oi = ((size_t)b * a.qh + h) * D + d;
@@ -333,8 +366,13 @@ __global__ __launch_bounds__(256) void attn_kernel(const AttnArgs a) {
 }  // namespace
 
 int launch_attention(const AttnArgs& a, hipStream_t stream) {
-  if (!a.counters || !a.part_ml || !a.part_acc) return Q4D_ERR_NULL;
-  hipLaunchKernelGGL(attn_kernel, dim3(a.nsplit_max, a.kvh, a.batch), dim3(256), 0, stream, a);
+  if (!a.part_ml || !a.part_acc || (a.merge && !a.counters)) return Q4D_ERR_NULL;
+  if (a.merge) {
+    hipLaunchKernelGGL(attn_kernel<kAttnChunk>, dim3(a.nsplit_max, a.kvh, a.batch), dim3(256), 0, stream, a);
+  } else {
+    const int ns = (a.max_ctx + kAttnChunkLong - 1) / kAttnChunkLong;
+    hipLaunchKernelGGL(attn_kernel<kAttnChunkLong>, dim3(ns, a.kvh, a.batch), dim3(256), 0, stream, a);
+  }
   return check_launch();
 }
 

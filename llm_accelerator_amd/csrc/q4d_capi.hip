@@ -143,14 +143,19 @@ int run_layer(const q4d_model_t* m, int l, const float* hin, float* hout, const 
   t.out = attn;
   t.out_dtype = Q4D_F32;
   t.status = ws_ptr<int32_t>(ws, W.status);
+  t.merge = 0;  // partials only: merged by the o_proj prologue
   if ((only < 0 || only == Q4D_STAGE_ATTENTION) && (rc = launch_attention(t, st))) return rc;
 
-  // 3. o_proj + residual
+  // 3. merge the attention partials, o_proj + residual
   a = one_matrix(&L.o_proj, 1);
-  a.x = attn;
+  a.part_ml = t.part_ml;
+  a.part_acc = t.part_acc;
+  a.positions = positions;
+  a.nsplit_max = W.nsplit_max;
+  a.attn_chunk = kAttnChunkLong;
   a.y = hout;
   a.resid = hin;
-  if ((only < 0 || only == Q4D_STAGE_O_PROJ) && (rc = launch_gemv_xp(a, X_F32, xp, EP_RESID, false, st)))
+  if ((only < 0 || only == Q4D_STAGE_O_PROJ) && (rc = launch_gemv_xp(a, X_ATTN, xp, EP_RESID, false, st)))
     return rc;
 
   // 4. post-attention RMSNorm + gate/up + SwiGLU
@@ -322,6 +327,7 @@ int q4d_cached_attention(const q4d_model_t* model, const q4d_kv_cache_t* kv, int
   t.out = out;
   t.out_dtype = out_dtype;
   t.status = ws_ptr<int32_t>(ws, W.status);
+  t.merge = 1;
   return launch_attention(t, as_stream(stream));
 }
 
@@ -471,6 +477,7 @@ int q4d_decode_batch(const q4d_model_t* model, const int32_t* tokens, const int3
     t.out = attn;
     t.out_dtype = Q4D_F16;
     t.status = status;
+    t.merge = 1;
     if ((rc = launch_attention(t, st))) return rc;
 
     memset(&g, 0, sizeof(g));

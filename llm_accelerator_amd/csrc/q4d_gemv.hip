@@ -60,6 +60,7 @@ constexpr int kSlice = 1024;       // columns per wave tile
 constexpr int kLmBlocksPerCU = 4;  // resident blocks per CU for the streaming kernel
 constexpr int kLmStage = 1;        // 4-row tiles per stage of the streaming kernel
 constexpr int kLmWaves = 16;       // waves per block of the streaming kernel
+constexpr int kAttnMergeWaves = 8;   // waves per block of the GEMV merging attention partials
 constexpr int kRsrcFlags = 0x00020000;
 
 typedef __amdgpu_buffer_rsrc_t Rsrc;
@@ -196,6 +197,7 @@ struct ActRegs {
 template <int K, int NWB, int XM, int XP>
 __device__ __forceinline__ void act_load(const GemvArgs& a, int bat, ActRegs<K, NWB, XM, XP>& r) {
   using R = ActRegs<K, NWB, XM, XP>;
+  if constexpr (XM == X_ATTN) return;  // loaded after the weights (act_load_attn)
 #pragma unroll
   for (int i = 0; i < R::XPT; ++i) {
     const int v = threadIdx.x + i * NWB * 64;
@@ -204,6 +206,75 @@ __device__ __forceinline__ void act_load(const GemvArgs& a, int bat, ActRegs<K, 
                                               (size_t)bat * K * (XM == X_F16 ? 2 : 4))[v];
       if constexpr (XM == X_RMS) r.g[i] = reinterpret_cast<const f32x4*>(a.gamma)[v];
     }
+  }
+}
+
+// X_ATTN: the attention output for this thread's vectors, merged from the
+// split-K chunk partials of the decode-attention kernel (merge = 0): running
+// maximum M over the chunks' maxima m_i, then sum_i 2^(m_i - M) acc_i over
+// sum_i 2^(m_i - M) l_i (the flash-decoding combine, as the attention kernel's
+// own merge does it).  The loads of up to kMergeBatch chunks go out together.
+constexpr int kMergeBatch = 8;
+
+// One batch of kMergeBatch chunks of partials for dims d..d+3 of one head,
+// folded into the running (M, L, o).
+__device__ __forceinline__ void merge_batch(const GemvArgs& a, size_t base, int d, int c0, int ns, float& M, float& L,
+                                            f32x4& o) {
+  constexpr int D = 128;
+  float2 ml[kMergeBatch];
+  f32x4 ac[kMergeBatch];
+  // addresses clamp to the workspace, not to ns: ns comes from a device
+  // load, and addresses depending on it would wait for that load first
+#pragma unroll
+  for (int k = 0; k < kMergeBatch; ++k) {
+    const int c = c0 + k < a.nsplit_max ? c0 + k : a.nsplit_max - 1;
+    ml[k] = *reinterpret_cast<const float2*>(a.part_ml + (base + c) * 2);
+    ac[k] = *reinterpret_cast<const f32x4*>(a.part_acc + (base + c) * D + d);
+  }
+  // chunks past ns are masked with selects, not branches: a branch lets the
+  // compiler sink their loads into it, behind a wait for everything in flight
+  float mk[kMergeBatch], lk[kMergeBatch];
+  float Mn = M;
+#pragma unroll
+  for (int k = 0; k < kMergeBatch; ++k) {
+    const bool valid = c0 + k < ns;
+    mk[k] = valid ? ml[k].x : -INFINITY;
+    lk[k] = valid ? ml[k].y : 0.f;
+    ac[k] = valid ? ac[k] : f32x4{0.f, 0.f, 0.f, 0.f};
+    Mn = fmaxf(Mn, mk[k]);
+  }
+  const float so = M == -INFINITY ? 0.f : exp2f(M - Mn);
+  L *= so;
+  o *= so;
+#pragma unroll
+  for (int k = 0; k < kMergeBatch; ++k) {
+    const float wgt = exp2f(mk[k] - Mn);  // 0 for masked chunks
+    L = fmaf(wgt, lk[k], L);
+    o += wgt * ac[k];
+  }
+  M = Mn;
+}
+
+template <int K, int NWB>
+__device__ __forceinline__ void act_load_attn(const GemvArgs& a, int bat, f32x4 (&xr)[(K / 4 + NWB * 64 - 1) /
+                                                                                          (NWB * 64)]) {
+  constexpr int XV = K / 4, NT = NWB * 64, XPT = (XV + NT - 1) / NT, D = 128;
+  const int pos = a.positions[bat];
+  int ns = (pos + a.attn_chunk) / a.attn_chunk;  // chunks holding positions 0..pos
+  ns = ns < 1 ? 1 : (ns > a.nsplit_max ? a.nsplit_max : ns);
+#pragma unroll
+  for (int i = 0; i < XPT; ++i) {
+    const int v = threadIdx.x + i * NT;
+    if (XV % NT != 0 && v >= XV) continue;
+    const int h = (4 * v) / D, d = (4 * v) % D;
+    const size_t base = ((size_t)bat * (K / D) + h) * a.nsplit_max;
+    float M = -INFINITY, L = 0.f;
+    f32x4 o = f32x4{0.f, 0.f, 0.f, 0.f};
+    // the first batch is straight-line code, so its loads go out right after
+    // the weights' (a loop here makes the compiler wait for those first)
+    merge_batch(a, base, d, 0, ns, M, L, o);
+    for (int c0 = kMergeBatch; c0 < ns; c0 += kMergeBatch) merge_batch(a, base, d, c0, ns, M, L, o);
+    xr[i] = o * (1.0f / L);
   }
 }
 
@@ -371,6 +442,13 @@ __global__ __launch_bounds__(NWB * 64) void gemv_kernel(const GemvArgs a) {
       const int t = base + u * step;
       res_pre[u] = a.resid[(size_t)bat * a.rows + 2 * (t < NP ? t : NP - 1) + (lane >> 5)];
     }
+  }
+  // attention partials go out after the weights: both round trips overlap
+  // (the barrier keeps the scheduler from moving the weight loads behind the
+  // merge arithmetic, which waits for the partials)
+  if constexpr (XM == X_ATTN) {
+    __builtin_amdgcn_sched_barrier(0);
+    act_load_attn<K, NWB>(a, bat, ar.x);
   }
 
   act_prepare(a, ar, s_act);
@@ -647,6 +725,10 @@ int launch_sel(const GemvArgs& a, hipStream_t st) {
   if constexpr (EP == EP_ARGMAX) {
     static_assert(KS == 1 && XM == X_RMS, "LM head: K = 1024 with the final RMSNorm");
     return launch_lm<XP>(a, st);
+  } else if constexpr (XM == X_ATTN) {
+    // every block merges the whole attention output: fewer, fatter blocks
+    // (same waves in total) cut that re-read
+    return launch_inst<KS, KS * (kAttnMergeWaves / KS), XM, XP, EP, PAIR, 1>(a, st);
   } else {
     return launch_inst<KS, nwb_of<KS>(), XM, XP, EP, PAIR, 1>(a, st);
   }
@@ -676,6 +758,9 @@ int dispatch_k(const GemvArgs& a, int xm, int xp, int ep, bool pair, hipStream_t
     if (xm == X_F32 && ep == EP_RESID && !pair)
       return xp == 2 ? launch_sel<KS, X_F32, 2, EP_RESID, false>(a, st)
                      : launch_sel<KS, X_F32, 1, EP_RESID, false>(a, st);
+    if (xm == X_ATTN && ep == EP_RESID && !pair)
+      return xp == 2 ? launch_sel<KS, X_ATTN, 2, EP_RESID, false>(a, st)
+                     : launch_sel<KS, X_ATTN, 1, EP_RESID, false>(a, st);
   }
   return Q4D_ERR_SHAPE;
 }
@@ -701,8 +786,14 @@ int launch_gemv_xp(const GemvArgs& a, int xm, int xp, int ep, bool pair, hipStre
     if (!a.w[i] || !a.s[i]) return Q4D_ERR_NULL;
     if (!aligned(a.w[i], 16) || !aligned(a.s[i], 4)) return Q4D_ERR_BAD_ADDR;
   }
-  if (!a.x || (!a.y && ep != EP_ARGMAX)) return Q4D_ERR_NULL;
-  if (!aligned(a.x, 16)) return Q4D_ERR_BAD_ADDR;
+  if (xm == X_ATTN) {
+    if (!a.part_ml || !a.part_acc || !a.positions || a.nsplit_max <= 0 || a.attn_chunk <= 0) return Q4D_ERR_NULL;
+    if (a.cols % 128 || !aligned(a.part_acc, 16) || !aligned(a.part_ml, 8)) return Q4D_ERR_SHAPE;
+  } else if (!a.x) {
+    return Q4D_ERR_NULL;
+  }
+  if (!a.y && ep != EP_ARGMAX) return Q4D_ERR_NULL;
+  if (xm != X_ATTN && !aligned(a.x, 16)) return Q4D_ERR_BAD_ADDR;
   if (xm == X_RMS && (!a.gamma || !aligned(a.gamma, 16))) return Q4D_ERR_NULL;
   if (ep == EP_RESID && !a.resid) return Q4D_ERR_NULL;
   if (ep == EP_ARGMAX && (!a.lm_key || !a.counter || !a.out_token || !a.out_score || a.batch != 1))

@@ -9,8 +9,11 @@
 
 namespace q4d {
 
-// Decode attention splits the context into chunks of this many positions.
+// Decode attention splits the context into chunks of this many positions
+// (kAttnChunkLong when the consumer merges the partials); workspace partials
+// are sized for the shorter chunk.
 constexpr int kAttnChunk = 64;
+constexpr int kAttnChunkLong = 128;
 // Upper bound on the LM-head grid (one partial argmax per block).
 constexpr int kLmMaxBlocks = 2048;
 
@@ -79,7 +82,9 @@ inline int check_launch() {
 }
 
 // ---- GEMV launcher ---------------------------------------------------------
-enum XMode { X_F16 = 0, X_F32 = 1, X_RMS = 2 };
+// X_ATTN: fp32 activations merged in the prologue from split-K decode-attention
+// partials (part_ml / part_acc of the attention kernel run with merge = 0).
+enum XMode { X_F16 = 0, X_F32 = 1, X_RMS = 2, X_ATTN = 3 };
 enum EpMode { EP_F16 = 0, EP_F32 = 1, EP_RESID = 2, EP_SWIGLU = 3, EP_ARGMAX = 4 };
 
 struct GemvArgs {
@@ -104,6 +109,12 @@ struct GemvArgs {
   int* out_token;
   float* out_score;
   int batch;
+  // X_ATTN: chunk partials [batch][heads][nsplit_max] of (max, sum) and [head_dim]
+  const float* part_ml;
+  const float* part_acc;
+  const int32_t* positions;  // device [batch]: the attended positions are 0 .. positions[b]
+  int nsplit_max;
+  int attn_chunk;            // positions per chunk
 };
 
 // Validates geometry, picks the kernel instance and launches.  Returns Q4D_*.
@@ -125,6 +136,10 @@ struct AttnArgs {
   // kernel applies q/k RMSNorm + RoPE and appends k/v to the cache.
   // fused = 0: q is ready ([batch, qh*d], normed, roped); cache already holds pos.
   int fused;
+  // merge = 1: the last block of each (kv head, sequence) merges the chunk
+  // partials into `out`.  merge = 0: partials only (128-position chunks), merged
+  // by the consumer (the o_proj GEMV with X_ATTN).
+  int merge;
   const float* qkv;
   const float* q;
   const float* q_gamma;

@@ -324,6 +324,48 @@ def algorithmic_bytes_layer(cfg: Qwen3Config, ctx: int) -> int:
     return weights + kv_read + kv_write + 2 * h * 2
 
 
+def stage_bytes_layer(cfg: Qwen3Config, ctx: int) -> dict:
+    """Algorithmic bytes per launch of each decode-layer stage at context
+    ``ctx``, in the dtypes the kernels read and write: Q4 codes + Q2.14
+    scales, fp32 activations (and fp32 gammas for the RMSNorm prologues),
+    fp16 K/V."""
+    h, i, d = cfg.hidden_size, cfg.intermediate_size, cfg.head_dim
+    qh, kvh = cfg.num_attention_heads, cfg.num_key_value_heads
+
+    def w(rows, cols):
+        return rows * cols // 2 + 2 * rows * (cols // GROUP_SIZE)
+    qkv_rows = (qh + 2 * kvh) * d
+    return {
+        "qkv": w(qkv_rows, h) + 4 * h + 4 * h + 4 * qkv_rows,
+        "attention": 2 * kvh * ctx * d * 2 + 2 * kvh * d * 2 + 4 * qkv_rows + 4 * qh * d + 4 * 2 * d,
+        "o_proj": w(h, qh * d) + 4 * qh * d + 4 * h + 4 * h,
+        "gate_up": 2 * w(i, h) + 4 * h + 4 * h + 4 * i,
+        "down": w(h, i) + 4 * i + 4 * h + 4 * h,
+    }
+
+
+def prefill_flops(cfg: Qwen3Config, n: int) -> int:
+    """Flops of prefilling n tokens from position 0: the projections
+    (2 per weight per token), causal attention (q.k and p.v over positions
+    0..t for token t) and the LM head of the last token."""
+    h, i, d = cfg.hidden_size, cfg.intermediate_size, cfg.head_dim
+    qh, kvh, L = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.num_hidden_layers
+    per_layer = qh * d * h + 2 * kvh * d * h + h * qh * d + 2 * i * h + h * i
+    linear = 2 * n * per_layer * L
+    attention = 2 * 2 * d * qh * L * (n * (n + 1) // 2)
+    return linear + attention + 2 * cfg.vocab_size * h
+
+
+def batched_step_bytes(cfg: Qwen3Config, batch: int, ctx: int) -> int:
+    """HBM bytes of one batched decode step: every sequence's fp16 K/V over
+    ``ctx`` positions in every layer plus all Q4 weights once."""
+    h, i, d = cfg.hidden_size, cfg.intermediate_size, cfg.head_dim
+    qh, kvh, L = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.num_hidden_layers
+    elems = qh * d * h + 2 * kvh * d * h + h * qh * d + 2 * i * h + h * i
+    weights = L * (elems // 2 + 2 * (elems // GROUP_SIZE)) + cfg.vocab_size * h // 2 + 2 * cfg.vocab_size * (h // GROUP_SIZE)
+    return batch * L * 2 * kvh * ctx * d * 2 + weights
+
+
 def gemv_bytes(rows: int, cols: int, x_bytes: int = 2, y_bytes: int = 2) -> int:
     return rows * cols // 2 + 2 * rows * (cols // GROUP_SIZE) + x_bytes * cols + y_bytes * rows
 
@@ -334,4 +376,5 @@ def ceil_div(a: int, b: int) -> int:
 
 __all__ = ["Qwen3Config", "Q4Tensor", "Q4ForCausalLM", "Q4DecoderLayer", "Q4Backbone", "RotaryEmbedding",
            "KVCache", "Workspace", "random_q4", "random_gamma", "random_host_weights", "build_model",
-           "algorithmic_bytes_layer", "gemv_bytes", "current_stream", "ceil_div"]
+           "algorithmic_bytes_layer", "stage_bytes_layer", "prefill_flops", "batched_step_bytes", "gemv_bytes",
+           "current_stream", "ceil_div"]
