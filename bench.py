@@ -58,7 +58,10 @@ def parse():
     ap.add_argument("--ctx", type=int, default=512)
     ap.add_argument("--copies", type=int, default=40)
     ap.add_argument("--precision", type=int, default=2, choices=(1, 2))
-    ap.add_argument("--no-extras", action="store_true", help="skip the GEMV / full-decode / CPU legs")
+    ap.add_argument("--no-extras", action="store_true", help="skip every leg beside the layer step")
+    ap.add_argument("--extras", default="c1,c3,c4,c5",
+                    help="comma list of the legs to run beside the layer step: c1 GEMV, c3 decode + LM head, "
+                         "c4 prefill, c5 batched decode")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--decode-gen", type=int, default=256)
@@ -193,7 +196,10 @@ def main():
     del model, kv, ws, g_flush, g_res
     torch.cuda.empty_cache()
 
-    if not args.no_extras:
+    legs = set() if args.no_extras else {x.strip() for x in args.extras.split(",") if x.strip()}
+    if legs - {"c1", "c3", "c4", "c5"}:
+        sys.exit(f"unknown legs {sorted(legs - {'c1', 'c3', 'c4', 'c5'})}")
+    if "c1" in legs:
         # -------------------------------------------------------- C1 GEMV
         from llm_accelerator_amd.model import Q4Tensor, gemv_bytes, random_q4
         rng = np.random.default_rng(0)
@@ -220,14 +226,16 @@ def main():
         del P, S, g1, g2
         torch.cuda.empty_cache()
 
-        # -------------------------------------------------------- C3 decode tok/s
-        from llm_accelerator_amd.decode import GreedyDecoder
+    if legs & {"c3", "c4", "c5"}:
         fcfg = M.Qwen3Config()
         t = time.time()
         fhost = M.random_host_weights(fcfg, seed=0)
         fmodel = M.build_model(fcfg, fhost, max_ctx=max(64 + args.decode_gen + 16, C5_CTX + 1), device=dev)
         del fhost
-        log(f"[bench] C3 setup {time.time() - t:.1f}s")
+        log(f"[bench] 28-layer model setup {time.time() - t:.1f}s")
+    if "c3" in legs:
+        # -------------------------------------------------------- C3 decode tok/s
+        from llm_accelerator_amd.decode import GreedyDecoder
         prompt = np.random.default_rng(1).integers(0, fcfg.vocab_size, 64).tolist()
         dec = GreedyDecoder(fmodel, steps_per_graph=16, use_graph=True)
         dec.prefill(prompt)
@@ -274,8 +282,9 @@ def main():
         del dec, lws
         torch.cuda.empty_cache()
 
+    if "c4" in legs:
         # -------------------------------------------------------- C4 prefill
-        from llm_accelerator_amd.decode import BatchedDecoder, Prefill
+        from llm_accelerator_amd.decode import Prefill
         T = C4_TOKENS
         pkv = M.KVCache(fcfg, fcfg.num_hidden_layers, 1, fmodel.max_ctx, dev)
         pf = Prefill(fmodel, pkv, T)
@@ -297,7 +306,9 @@ def main():
         del pkv, pf
         torch.cuda.empty_cache()
 
+    if "c5" in legs:
         # -------------------------------------------------------- C5 batched decode
+        from llm_accelerator_amd.decode import BatchedDecoder
         B = C5_BATCH
         bkv = M.KVCache(fcfg, fcfg.num_hidden_layers, B, C5_CTX + 1, dev)
         bkv.data[..., :C5_CTX, :].normal_(generator=gen)
@@ -306,6 +317,7 @@ def main():
         bpos = torch.full((B,), C5_CTX, dtype=torch.int32, device=dev)
         bd.step(btok, bpos)
         torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record()
         for _ in range(5):
             bd.step(btok, bpos)
@@ -320,6 +332,7 @@ def main():
                                        "status": bd.status()}
         log(f"[bench] C5 batched decode: {json.dumps(extras['c5_batched_decode'])}")
         del bkv, bd
+    if legs & {"c3", "c4", "c5"}:
         del fmodel
         torch.cuda.empty_cache()
 
@@ -335,7 +348,7 @@ def main():
         del src, dst
 
     cpu = None
-    if not args.no_cpu and not args.no_extras:
+    if not args.no_cpu and legs:
         cpu = cpu_baseline(args.cpu_seconds, ctx, step_bytes)
         log(f"[bench] CPU baseline: {json.dumps(cpu)}")
 

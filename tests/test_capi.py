@@ -143,6 +143,34 @@ def test_batched_entry_validation_codes(lib):
     assert lib.q4d_gemm(ctypes.byref(w), FAKE + 2, 4, FAKE, 1, None, None) == -4
 
 
+def test_prefill_validation_codes(lib):
+    arr = _layers(2)
+    m = _model(arr)
+    kv = Q4dKVCache(data=FAKE, num_layers=2, batch=2, num_kv_heads=8, max_ctx=512, head_dim=128)
+    need = lib.q4d_prefill_workspace_bytes(ctypes.byref(m), 64)
+    assert need > lib.q4d_workspace_bytes(ctypes.byref(m), 1)
+    assert lib.q4d_prefill_workspace_bytes(ctypes.byref(m), 128) > need
+    assert lib.q4d_prefill_workspace_bytes(ctypes.byref(m), 0) == 0
+    assert lib.q4d_prefill_workspace_bytes(None, 64) == 0
+
+    def prefill(n=64, start=0, seq=0, ws=FAKE, nbytes=need, tokens=FAKE, model=m, cache=kv):
+        return lib.q4d_prefill(ctypes.byref(model), tokens, n, start, seq, ctypes.byref(cache), FAKE, FAKE, None, ws,
+                               nbytes, None)
+    assert prefill(tokens=None) == -7
+    assert prefill(ws=None) == -7
+    assert prefill(n=0) == -11
+    assert prefill(start=500, n=13) == -10   # 500 + 13 > max_ctx 512
+    assert prefill(start=-1) == -10
+    assert prefill(seq=2) == -9              # the cache holds sequences 0 and 1
+    assert prefill(nbytes=need - 1) == -9
+    assert prefill(n=65) == -9               # the workspace was sized for 64 tokens
+    assert prefill(ws=FAKE + 64) == -4       # workspace must be 256-byte aligned
+    kv_bad = Q4dKVCache(data=FAKE, num_layers=2, batch=2, num_kv_heads=8, max_ctx=256, head_dim=128)
+    assert prefill(cache=kv_bad) == -11
+    arr[0].q_proj = Q4dMatrix(FAKE, FAKE, 2048, 512)
+    assert prefill(model=_model(arr)) == -2
+
+
 def test_activation_precision_setter(lib):
     assert lib.q4d_set_activation_precision(3) == -13
     assert lib.q4d_set_activation_precision(2) == 0
