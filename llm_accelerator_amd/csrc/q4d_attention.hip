@@ -33,7 +33,8 @@
 //    critical path.
 // The block owning the new position appends its K/V row (append_cache,
 // common.py:186-189) and takes that row from LDS rather than from its own
-// global write.
+// global write.  Barriers that only order LDS traffic are LDS-only, so no
+// wave waits for the append stores to be acknowledged.
 #include <math.h>
 
 #include "q4d_device.h"
@@ -198,7 +199,7 @@ __global__ __launch_bounds__(256) void attn_kernel(const AttnArgs a) {
     sq[wid][lane] = x0 * qscale;
     sq[wid][lane + 64] = x1 * qscale;
   }
-  __syncthreads();
+  block_sync_lds();
   if (a.fused && last) {
     // the appended position comes from LDS (same fp16 bits as stored)
     const int ip = pos - start - pr;
@@ -240,7 +241,7 @@ __global__ __launch_bounds__(256) void attn_kernel(const AttnArgs a) {
       ssc[1][p] = x1;
     }
   }
-  __syncthreads();
+  block_sync_lds();
 
   // ---- chunk softmax (one wave per head, one lane per position) -----------------
   if (wid < 2) {
@@ -267,7 +268,7 @@ __global__ __launch_bounds__(256) void attn_kernel(const AttnArgs a) {
       sml[wid][1] = l;
     }
   }
-  __syncthreads();
+  block_sync_lds();
 
   // ---- P.V on the registers loaded at the start --------------------------------
   float o0[8], o1[8];
@@ -291,7 +292,7 @@ __global__ __launch_bounds__(256) void attn_kernel(const AttnArgs a) {
     *reinterpret_cast<f32x4*>(&spv[pr][0][sub * 8 + e]) = f32x4{o0[e], o0[e + 1], o0[e + 2], o0[e + 3]};
     *reinterpret_cast<f32x4*>(&spv[pr][1][sub * 8 + e]) = f32x4{o1[e], o1[e + 1], o1[e + 2], o1[e + 3]};
   }
-  __syncthreads();
+  block_sync_lds();
   const int hh = t >> 7, d = t & (D - 1), h = j * 2 + hh;
   float acc = 0.f;
 #pragma unroll
