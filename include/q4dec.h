@@ -204,6 +204,15 @@ int q4d_lm_head_argmax_batch(const q4d_model_t* model, const float* hidden, int3
  * (one rounding of q*scale) and accumulated in fp32.  rows % 128 == 0, cols % 64 == 0. */
 int q4d_gemm(const q4d_matrix_t* w, const uint16_t* x, int32_t M, void* y, int32_t y_dtype,
              const float* resid, void* stream);
+/* q4d_gemm with the K dimension split over `ksplit` blocks per output tile
+ * (1..16, at most cols / 64; 0 = chosen for the shape), for few activation
+ * rows where the output tiles alone leave the device idle: each split's fp32
+ * tile goes to `part` (ksplit x M x rows floats, 16-byte aligned), then the
+ * splits are added in order.  Same result as q4d_gemm up to the grouping of
+ * the fp32 sums.  No counterpart in the reference; it is the batched-decode
+ * projection path of q4d_decode_batch, exported for callers with scratch. */
+int q4d_gemm_splitk(const q4d_matrix_t* w, const uint16_t* x, int32_t M, void* y, int32_t y_dtype,
+                    const float* resid, float* part, size_t part_bytes, int32_t ksplit, void* stream);
 
 /* ---- fused decode ---------------------------------------------------------- */
 /* One cached decoder layer (batch 1): hidden_out = layer(hidden_in); appends

@@ -364,12 +364,294 @@ __global__ __launch_bounds__(256) void attn_kernel(const AttnArgs a) {
   if (t == 0) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);  // next launch
 }
 
+// Long-context variant of attn_kernel<64> with merge = 1 (batched decode,
+// q4d_cached_attention): a block covers `span` positions (a multiple of 64)
+// as consecutive 64-position sub-chunks, with the next sub-chunk's K/V loads
+// in flight while the current one is used, and an online softmax across the
+// sub-chunks (running maximum M and sum L per head; the output accumulators
+// are rescaled by 2^(M_old - M_new) when M grows).  `span` is chosen so a
+// head has at most eight splits, which the last block merges with one batch
+// of loads.  Same thread mapping, prologue and partial format as
+// attn_kernel<64>.
+__global__ __launch_bounds__(256) void attn_span_kernel(const AttnArgs a, int span) {
+  constexpr int D = 128, CH = 64, NPT = CH / 16;
+  const int s = blockIdx.x, j = blockIdx.y, b = blockIdx.z;
+  const int t = threadIdx.x, lane = t & 63;
+  const int wid = __builtin_amdgcn_readfirstlane(t >> 6);
+  const int pos = a.positions[b];
+  if (pos < 0 || pos >= a.max_ctx) {
+    if (s == 0 && j == 0 && t == 0) atomicOr(a.status, Q4D_STATUS_BAD_POSITION);
+    return;
+  }
+  const int T = pos + 1;
+  const int nsplit = (T + span - 1) / span;
+  if (s >= nsplit) return;
+  const int start = s * span;
+  const int end = min(T, start + span);
+  const int nsub = (end - start + CH - 1) / CH;
+  const int cached = a.fused ? pos : T;
+  const bool last = (s == nsplit - 1);  // block-uniform: holds pos
+
+  __shared__ float sq[2][D];
+  __shared__ uint16_t snew[2][D];
+  __shared__ float ssc[2][CH];
+  __shared__ float sscale[2];  // rescale of each head's running output for this sub-chunk
+  __shared__ float sml[2][2];
+  __shared__ float spv[16][2][D];
+  __shared__ int s_last;
+
+  const size_t plane_off = ((size_t)(b * a.kvh + j) * a.max_ctx) * D;
+  uint16_t* kb = a.kcache + plane_off;
+  uint16_t* vb = a.vcache + plane_off;
+
+  // ---- q / new k / new v rows first (as attn_kernel) ----------------------------
+  const float qscale = a.scaling * 1.4426950408889634f;
+  const int qkv_stride = (a.qh + 2 * a.kvh) * D;
+  const bool qk_wave = a.fused ? (wid < 2 || (last && wid == 2)) : (wid < 2);
+  const bool v_wave = a.fused && last && wid == 3;
+  const float* row;
+  const float* gam;
+  const float* ctab;
+  const float* stab;
+  if (a.fused) {
+    const float* src = a.qkv + (size_t)b * qkv_stride;
+    const int ridx = wid < 2 ? j * 2 + wid : (wid == 2 ? a.qh + j : a.qh + a.kvh + j);
+    row = src + (size_t)ridx * D;
+    gam = wid < 2 ? a.q_gamma : a.k_gamma;
+    ctab = a.rope_cos + (size_t)pos * (D / 2);
+    stab = a.rope_sin + (size_t)pos * (D / 2);
+  } else {
+    row = a.q + ((size_t)b * a.qh + j * 2 + (wid < 2 ? wid : 1)) * D;
+    gam = ctab = stab = row;
+  }
+  const float x0 = row[lane], x1 = row[lane + 64];
+  const float g0 = gam[lane], g1 = gam[lane + 64];
+  const float c = ctab[lane], sn = stab[lane];
+  __builtin_amdgcn_sched_barrier(0);
+
+  // ---- K/V of sub-chunk 0 (rows at or past `cached` read the last cached row:
+  // unconditional loads, zero softmax weight; position pos comes from LDS)
+  const int sub = t & 15, pr = t >> 4;
+  const int plast = cached > 0 ? cached - 1 : 0;
+  u32x4 kr[NPT], vr[NPT], kn[NPT], vn[NPT];
+#pragma unroll
+  for (int i = 0; i < NPT; ++i) {
+    int p = start + pr + 16 * i;
+    p = p < cached ? p : plast;
+    kr[i] = *reinterpret_cast<const u32x4*>(kb + (size_t)p * D + sub * 8);
+    vr[i] = *reinterpret_cast<const u32x4*>(vb + (size_t)p * D + sub * 8);
+  }
+
+  // ---- per-head RMSNorm (common.py:258-262) + rotate-half RoPE (264-268) -------
+  if (a.fused && qk_wave) {
+    const float ss = wave_sum_all(fmaf(x0, x0, x1 * x1));
+    const float inv = 1.0f / sqrtf(ss / (float)D + a.eps);
+    const float n0 = (x0 * inv) * g0, n1 = (x1 * inv) * g1;
+    const float r0 = n0 * c + (-n1) * sn;
+    const float r1 = n1 * c + n0 * sn;
+    if (wid < 2) {
+      sq[wid][lane] = r0 * qscale;
+      sq[wid][lane + 64] = r1 * qscale;
+    } else {
+      const uint16_t b0 = __builtin_bit_cast(uint16_t, (_Float16)r0);
+      const uint16_t b1 = __builtin_bit_cast(uint16_t, (_Float16)r1);
+      snew[0][lane] = b0;
+      snew[0][lane + 64] = b1;
+      kb[(size_t)pos * D + lane] = b0;
+      kb[(size_t)pos * D + lane + 64] = b1;
+    }
+  } else if (v_wave) {
+    const uint16_t b0 = __builtin_bit_cast(uint16_t, (_Float16)x0);
+    const uint16_t b1 = __builtin_bit_cast(uint16_t, (_Float16)x1);
+    snew[1][lane] = b0;
+    snew[1][lane + 64] = b1;
+    vb[(size_t)pos * D + lane] = b0;
+    vb[(size_t)pos * D + lane + 64] = b1;
+  } else if (qk_wave) {
+    sq[wid][lane] = x0 * qscale;
+    sq[wid][lane + 64] = x1 * qscale;
+  }
+  block_sync_lds();
+  float q0[8], q1[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    q0[e] = sq[0][sub * 8 + e];
+    q1[e] = sq[1][sub * 8 + e];
+  }
+
+  float o0[8], o1[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) o0[e] = o1[e] = 0.f;
+  float M = -INFINITY, L = 0.f;  // running max / sum of head `wid` (waves 0 and 1)
+  for (int sc = 0; sc < nsub; ++sc) {
+    const int base = start + sc * CH;
+    const int n = min(end - base, CH);
+    // the next sub-chunk's K/V go out now (the last iteration re-reads its
+    // own rows: unconditional loads keep the compiler from waiting on them)
+    const int nb = sc + 1 < nsub ? base + CH : base;
+#pragma unroll
+    for (int i = 0; i < NPT; ++i) {
+      int p = nb + pr + 16 * i;
+      p = p < cached ? p : plast;
+      kn[i] = *reinterpret_cast<const u32x4*>(kb + (size_t)p * D + sub * 8);
+      vn[i] = *reinterpret_cast<const u32x4*>(vb + (size_t)p * D + sub * 8);
+    }
+    if (a.fused && last) {
+      const int ip = pos - base - pr;
+      if (ip >= 0 && ip < CH && (ip & 15) == 0) {
+        const int i = ip >> 4;
+        const u32x4 kn4 = *reinterpret_cast<const u32x4*>(&snew[0][sub * 8]);
+        const u32x4 vn4 = *reinterpret_cast<const u32x4*>(&snew[1][sub * 8]);
+#pragma unroll
+        for (int ii = 0; ii < NPT; ++ii)
+          if (ii == i) {
+            kr[ii] = kn4;
+            vr[ii] = vn4;
+          }
+      }
+    }
+    // scores: 8-dim partial dots reduced over the 16 lanes of a position
+#pragma unroll
+    for (int i = 0; i < NPT; ++i) {
+      float kf[8];
+      unpack8(kr[i], kf);
+      float y0 = 0.f, y1 = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        y0 = fmaf(q0[e], kf[e], y0);
+        y1 = fmaf(q1[e], kf[e], y1);
+      }
+      y0 = row16_sum(y0);
+      y1 = row16_sum(y1);
+      const int p = pr + 16 * i;
+      if (sub == 0 && p < n) {
+        ssc[0][p] = y0;
+        ssc[1][p] = y1;
+      }
+    }
+    block_sync_lds();
+    // online softmax update, one wave per head, one position per lane
+    if (wid < 2) {
+      const float sv = lane < n ? ssc[wid][lane] : -INFINITY;
+      const float Mn = fmaxf(M, wave_max_all(sv));
+      const float e = lane < n ? exp2f(sv - Mn) : 0.f;
+      ssc[wid][lane] = e;
+      const float scale = M == -INFINITY ? 0.f : exp2f(M - Mn);
+      L = fmaf(L, scale, wave_sum_all(e));
+      M = Mn;
+      if (lane == 0) sscale[wid] = scale;
+    }
+    block_sync_lds();
+    const float sc0 = sscale[0], sc1 = sscale[1];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      o0[e] *= sc0;
+      o1[e] *= sc1;
+    }
+#pragma unroll
+    for (int i = 0; i < NPT; ++i) {
+      const int p = pr + 16 * i;
+      const float e0 = p < n ? ssc[0][p] : 0.f;
+      const float e1 = p < n ? ssc[1][p] : 0.f;
+      float vf[8];
+      unpack8(vr[i], vf);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        o0[e] = fmaf(e0, vf[e], o0[e]);
+        o1[e] = fmaf(e1, vf[e], o1[e]);
+      }
+    }
+    block_sync_lds();  // ssc / sscale are rewritten by the next sub-chunk
+#pragma unroll
+    for (int i = 0; i < NPT; ++i) {
+      kr[i] = kn[i];
+      vr[i] = vn[i];
+    }
+  }
+  if (wid < 2 && lane == 0) {
+    sml[wid][0] = M;
+    sml[wid][1] = L;
+  }
+#pragma unroll
+  for (int e = 0; e < 8; e += 4) {
+    *reinterpret_cast<f32x4*>(&spv[pr][0][sub * 8 + e]) = f32x4{o0[e], o0[e + 1], o0[e + 2], o0[e + 3]};
+    *reinterpret_cast<f32x4*>(&spv[pr][1][sub * 8 + e]) = f32x4{o1[e], o1[e + 1], o1[e + 2], o1[e + 3]};
+  }
+  block_sync_lds();
+  const int hh = t >> 7, d = t & (D - 1), h = j * 2 + hh;
+  float acc = 0.f;
+#pragma unroll
+  for (int g = 0; g < 16; ++g) acc += spv[g][hh][d];
+
+  // ---- publish the split partial, count in; the last block merges (as attn_kernel)
+  const size_t pbase = (size_t)(b * a.qh + h) * a.nsplit_max;
+  if (nsplit == 1) {
+    const float r = acc / sml[hh][1];
+    const size_t oi = ((size_t)b * a.qh + h) * D + d;
+    if (a.out_dtype == Q4D_F16)
+      static_cast<_Float16*>(a.out)[oi] = (_Float16)r;
+    else
+      static_cast<float*>(a.out)[oi] = r;
+    return;
+  }
+  store_dev(&a.part_acc[(pbase + s) * D + d], acc);
+  if (d == 0) {
+    store_dev(&a.part_ml[(pbase + s) * 2 + 0], sml[hh][0]);
+    store_dev(&a.part_ml[(pbase + s) * 2 + 1], sml[hh][1]);
+  }
+  __builtin_amdgcn_s_waitcnt(0);  // this thread's stores are performed
+  __syncthreads();                 // ... and every other thread's
+  int* counter = a.counters + b * a.kvh + j;
+  if (t == 0) s_last = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == nsplit - 1;
+  __syncthreads();
+  if (!s_last) return;
+  constexpr int kMergeBatch = 8;
+  float Mx = -INFINITY, Lx = 0.f, o = 0.f;
+  for (int i0 = 0; i0 < nsplit; i0 += kMergeBatch) {
+    float mi[kMergeBatch], li[kMergeBatch], ai[kMergeBatch];
+#pragma unroll
+    for (int k = 0; k < kMergeBatch; ++k) {
+      const int i = min(i0 + k, nsplit - 1);
+      mi[k] = load_dev(&a.part_ml[(pbase + i) * 2]);
+      li[k] = load_dev(&a.part_ml[(pbase + i) * 2 + 1]);
+      ai[k] = load_dev(&a.part_acc[(pbase + i) * D + d]);
+    }
+#pragma unroll
+    for (int k = 0; k < kMergeBatch; ++k) {
+      if (i0 + k >= nsplit) break;
+      const float Mn = fmaxf(Mx, mi[k]);
+      const float so = Mx == -INFINITY ? 0.f : exp2f(Mx - Mn);
+      const float si = exp2f(mi[k] - Mn);
+      Lx = Lx * so + li[k] * si;
+      o = o * so + ai[k] * si;
+      Mx = Mn;
+    }
+  }
+  const float r = o / Lx;
+  const size_t oi = ((size_t)b * a.qh + h) * D + d;
+  if (a.out_dtype == Q4D_F16)
+    static_cast<_Float16*>(a.out)[oi] = (_Float16)r;
+  else
+    static_cast<float*>(a.out)[oi] = r;
+  if (t == 0) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);  // next launch
+}
+
 }  // namespace
 
 int launch_attention(const AttnArgs& a, hipStream_t stream) {
   if (!a.part_ml || !a.part_acc || (a.merge && !a.counters)) return Q4D_ERR_NULL;
   if (a.merge) {
-    hipLaunchKernelGGL(attn_kernel<kAttnChunk>, dim3(a.nsplit_max, a.kvh, a.batch), dim3(256), 0, stream, a);
+    // contexts past kSpanSplits x 64 positions: spans of several 64-position
+    // sub-chunks, at most kSpanSplits per head
+    constexpr int kSpanSplits = 8;
+    const int nch = (a.max_ctx + kAttnChunk - 1) / kAttnChunk;
+    if (nch <= kSpanSplits) {
+      hipLaunchKernelGGL(attn_kernel<kAttnChunk>, dim3(a.nsplit_max, a.kvh, a.batch), dim3(256), 0, stream, a);
+    } else {
+      const int span = kAttnChunk * ((nch + kSpanSplits - 1) / kSpanSplits);
+      const int nsplit = (a.max_ctx + span - 1) / span;
+      hipLaunchKernelGGL(attn_span_kernel, dim3(nsplit, a.kvh, a.batch), dim3(256), 0, stream, a, span);
+    }
   } else {
     const int ns = (a.max_ctx + kAttnChunkLong - 1) / kAttnChunkLong;
     hipLaunchKernelGGL(attn_kernel<kAttnChunkLong>, dim3(ns, a.kvh, a.batch), dim3(256), 0, stream, a);

@@ -444,6 +444,34 @@ int q4d_gemm(const q4d_matrix_t* w, const uint16_t* x, int32_t M, void* y, int32
   return launch_gemm(a, resid ? EP_RESID : (y_dtype == Q4D_F16 ? EP_F16 : EP_F32), false, as_stream(stream));
 }
 
+int q4d_gemm_splitk(const q4d_matrix_t* w, const uint16_t* x, int32_t M, void* y, int32_t y_dtype,
+                    const float* resid, float* part, size_t part_bytes, int32_t ksplit, void* stream) {
+  if (!w || !part) return Q4D_ERR_NULL;
+  int rc = check_matrix(w, w->rows, w->cols);
+  if (rc) return rc;
+  if (y_dtype != Q4D_F16 && y_dtype != Q4D_F32) return Q4D_ERR_DTYPE;
+  if (resid && y_dtype != Q4D_F32) return Q4D_ERR_DTYPE;
+  if (ksplit < 0 || ksplit > kGemmMaxSplit || (ksplit > 0 && ksplit > w->cols / 64)) return Q4D_ERR_SHAPE;
+  if (!aligned(part, 16)) return Q4D_ERR_BAD_ADDR;
+  GemmArgs a;
+  memset(&a, 0, sizeof(a));
+  a.w[0] = w->w;
+  a.s[0] = w->s;
+  a.seg_end[0] = w->rows;
+  a.nseg = 1;
+  a.N = w->rows;
+  a.K = w->cols;
+  a.M = M;
+  a.x = x;
+  a.y = y;
+  a.ldy = w->rows;
+  a.resid = resid;
+  a.part = part;
+  a.part_cap = part_bytes / 4;
+  a.ksplit = ksplit;
+  return launch_gemm(a, resid ? EP_RESID : (y_dtype == Q4D_F16 ? EP_F16 : EP_F32), false, as_stream(stream));
+}
+
 // Final RMSNorm (to fp16) + LM head GEMM with per-row argmax partials over
 // 128-column blocks + one wave per row reducing them.
 static int run_lm_head_batch(const q4d_model_t* model, const float* hidden, int batch, int32_t* next_tokens,
@@ -489,6 +517,7 @@ int q4d_decode_batch(const q4d_model_t* model, const int32_t* tokens, const int3
   uint16_t* attn = ws_ptr<uint16_t>(ws, W.attn);
   uint16_t* act = ws_ptr<uint16_t>(ws, W.act);
   int32_t* status = ws_ptr<int32_t>(ws, W.status);
+  float* part = ws_ptr<float>(ws, W.gemm_part);  // split-K tiles of the M = batch GEMMs
   if ((rc = launch_embedding(&model->embed_tokens, tokens, batch, hidden, status, st))) return rc;
   for (int l = 0; l < model->num_layers; ++l) {
     const q4d_layer_t& L = model->layers[l];
@@ -509,6 +538,7 @@ int q4d_decode_batch(const q4d_model_t* model, const int32_t* tokens, const int3
     g.x = xh;
     g.y = qkv;
     g.ldy = g.N;
+    g.part = part; g.part_cap = W.gemm_part_floats;
     if ((rc = launch_gemm(g, EP_F32, false, st))) return rc;
 
     AttnArgs t;
@@ -544,6 +574,7 @@ int q4d_decode_batch(const q4d_model_t* model, const int32_t* tokens, const int3
     g.nseg = 1;
     g.N = H; g.K = qd; g.M = batch;
     g.x = attn; g.y = hidden; g.ldy = H; g.resid = hidden;
+    g.part = part; g.part_cap = W.gemm_part_floats;
     if ((rc = launch_gemm(g, EP_RESID, false, st))) return rc;
 
     if ((rc = launch_rms_norm(hidden, L.post_attention_layernorm, model->rms_norm_eps, batch, H, xh, Q4D_F16, st)))
@@ -555,6 +586,7 @@ int q4d_decode_batch(const q4d_model_t* model, const int32_t* tokens, const int3
     g.nseg = 2;
     g.N = I; g.K = H; g.M = batch;
     g.x = xh; g.y = act; g.ldy = I;
+    g.part = part; g.part_cap = W.gemm_part_floats;
     if ((rc = launch_gemm(g, EP_SWIGLU, true, st))) return rc;
 
     memset(&g, 0, sizeof(g));
@@ -563,6 +595,7 @@ int q4d_decode_batch(const q4d_model_t* model, const int32_t* tokens, const int3
     g.nseg = 1;
     g.N = H; g.K = I; g.M = batch;
     g.x = act; g.y = hidden; g.ldy = H; g.resid = hidden;
+    g.part = part; g.part_cap = W.gemm_part_floats;
     if ((rc = launch_gemm(g, EP_RESID, false, st))) return rc;
   }
   return run_lm_head_batch(model, hidden, batch, next_tokens, scores, logits, ws, W, st);

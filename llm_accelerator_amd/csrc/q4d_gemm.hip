@@ -21,6 +21,11 @@
 // gate/up row pair (common.py:293-295; the B tile then holds 64 gate rows and
 // the matching 64 up rows), and per-row argmax partials over the block's
 // columns for the batched LM head (lowest index wins ties).
+//
+// Split-K: when the output tiles alone cannot fill the device (batched
+// decode: M = 64 rows, N = 1024 gives 8 tiles), blockIdx.z takes a
+// contiguous range of the K steps and stores its raw fp32 tile; a second
+// kernel adds the splits in order (deterministic) and applies the epilogue.
 #include <math.h>
 
 #include "q4d_device.h"
@@ -153,7 +158,10 @@ __global__ __launch_bounds__(256) void q4_gemm_kernel(const GemmArgs a) {
   const int t = threadIdx.x, lane = t & 63, w = t >> 6;
   const int wm = (w >> 1) * WM, wn = (w & 1);
   const int nblk = blockIdx.x, m0 = blockIdx.y * BM;
-  const int nk = a.K / kGemmBK;
+  // K steps [k_begin, k_end) of this split
+  const int nk_all = a.K / kGemmBK, z = blockIdx.z, ksplit = gridDim.z;
+  const int k_begin = z * nk_all / ksplit;
+  const int nk = (z + 1) * nk_all / ksplit - k_begin;
 
   f32x4 acc[MI][NI];
 #pragma unroll
@@ -169,13 +177,13 @@ __global__ __launch_bounds__(256) void q4_gemm_kernel(const GemmArgs a) {
 
   const SegPtrs P = seg_ptrs(a);
   GemmTileLoad L;
-  gemm_load<BM, PAIR>(a, P, m0, nblk, 0, t, L);
+  gemm_load<BM, PAIR>(a, P, m0, nblk, k_begin * kGemmBK, t, L);
   gemm_store_lds<BM>(As[0], Bs[0], t, L);
   __syncthreads();
 
   for (int ks = 0; ks < nk; ++ks) {
     const int buf = ks & 1;
-    if (ks + 1 < nk) gemm_load<BM, PAIR>(a, P, m0, nblk, (ks + 1) * kGemmBK, t, L);
+    if (ks + 1 < nk) gemm_load<BM, PAIR>(a, P, m0, nblk, (k_begin + ks + 1) * kGemmBK, t, L);
 #pragma unroll
     for (int kk = 0; kk < 2; ++kk) {
       const int kc = kk * 32 + (lane >> 4) * 8;
@@ -195,6 +203,23 @@ __global__ __launch_bounds__(256) void q4_gemm_kernel(const GemmArgs a) {
 
   // ---- epilogue: lane holds rows (lane/16)*4 + r of each 16x16 tile, column lane%16
   const int cl = lane & 15, rq = (lane >> 4) * 4;
+  if (EP != EP_ARGMAX && ksplit > 1) {
+    // raw split tile: [z][m][n], PAIR: gate columns n, up columns N + n
+    const int wp = PAIR ? 2 * a.N : a.N;
+#pragma unroll
+    for (int i = 0; i < MI; ++i)
+#pragma unroll
+      for (int j = 0; j < NI; ++j) {
+        const int n = PAIR ? (j < 2 ? 0 : a.N) + nblk * 64 + 32 * wn + 16 * (j & 1) + cl
+                           : nblk * kGemmBN + 64 * wn + 16 * j + cl;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int m = m0 + wm + 16 * i + rq + r;
+          if (m < a.M) a.part[((size_t)z * a.M + m) * wp + n] = acc[i][j][r];
+        }
+      }
+    return;
+  }
   if constexpr (EP == EP_SWIGLU) {
 #pragma unroll
     for (int i = 0; i < MI; ++i)
@@ -283,6 +308,37 @@ __global__ __launch_bounds__(256) void q4_gemm_kernel(const GemmArgs a) {
   }
 }
 
+// Sum of the split-K tiles in split order, then the epilogue; one thread per
+// four consecutive outputs of the [M, N] result (N % 4 == 0).
+template <int EP, bool PAIR>
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(const GemmArgs a, int ksplit) {
+  const int q = blockIdx.x * 256 + threadIdx.x;
+  const int per_row = a.N / 4;
+  if (q >= a.M * per_row) return;
+  const int m = q / per_row, n = (q % per_row) * 4;
+  const int wp = PAIR ? 2 * a.N : a.N;
+  f32x4 v = f32x4{0.f, 0.f, 0.f, 0.f}, u = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int z = 0; z < ksplit; ++z) {
+    const float* row = a.part + ((size_t)z * a.M + m) * wp;
+    v += *reinterpret_cast<const f32x4*>(row + n);
+    if constexpr (PAIR) u += *reinterpret_cast<const f32x4*>(row + a.N + n);
+  }
+  const size_t o = (size_t)m * a.ldy + n;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    if constexpr (EP == EP_SWIGLU) {
+      const float g = v[e];
+      static_cast<_Float16*>(a.y)[o + e] = (_Float16)((g / (1.0f + expf(-g))) * u[e]);
+    } else if constexpr (EP == EP_F16) {
+      static_cast<_Float16*>(a.y)[o + e] = (_Float16)v[e];
+    } else if constexpr (EP == EP_RESID) {
+      static_cast<float*>(a.y)[o + e] = a.resid[o + e] + v[e];
+    } else {
+      static_cast<float*>(a.y)[o + e] = v[e];
+    }
+  }
+}
+
 // Row-wise reduction of the argmax partials: one wave per activation row.
 __global__ __launch_bounds__(64) void argmax_rows_kernel(const float* part_score, const int* part_idx, int nparts,
                                                          int M, int32_t* out_token, float* out_score) {
@@ -313,11 +369,35 @@ __global__ __launch_bounds__(64) void argmax_rows_kernel(const float* part_score
   }
 }
 
+// Splits of K for a grid of `tiles` output tiles: enough to reach ~256
+// blocks, each split keeping at least two K steps, within the partial buffer.
+static int choose_ksplit(const GemmArgs& a, int tiles, bool pair) {
+  if (a.ksplit > 0) return a.ksplit;
+  if (!a.part || tiles >= 128) return 1;
+  const int nk = a.K / kGemmBK;
+  int ks = (256 + tiles - 1) / tiles;
+  if (ks > nk / 2) ks = nk / 2;
+  if (ks > kGemmMaxSplit) ks = kGemmMaxSplit;
+  const size_t per_split = (size_t)a.M * (pair ? 2 * a.N : a.N);
+  while (ks > 1 && (size_t)ks * per_split > a.part_cap) --ks;
+  return ks < 1 ? 1 : ks;
+}
+
 template <int BM, int EP, bool PAIR>
 static int launch_gemm_inst(const GemmArgs& a, hipStream_t st) {
   const int nblk = PAIR ? a.N / 64 : a.N / kGemmBN;
-  dim3 grid(nblk, (a.M + BM - 1) / BM);
-  hipLaunchKernelGGL((q4_gemm_kernel<BM, EP, PAIR>), grid, dim3(256), 0, st, a);
+  const int mblk = (a.M + BM - 1) / BM;
+  const int ks = EP == EP_ARGMAX ? 1 : choose_ksplit(a, nblk * mblk, PAIR);
+  if (ks > 1 && (!a.part || (size_t)ks * a.M * (PAIR ? 2 * a.N : a.N) > a.part_cap || a.N % 4 ||
+                 ks > a.K / kGemmBK))
+    return Q4D_ERR_CAPACITY;
+  hipLaunchKernelGGL((q4_gemm_kernel<BM, EP, PAIR>), dim3(nblk, mblk, ks), dim3(256), 0, st, a);
+  int rc = check_launch();
+  if (rc || ks == 1) return rc;
+  if constexpr (EP != EP_ARGMAX) {
+    const int n4 = a.M * (a.N / 4);
+    hipLaunchKernelGGL((splitk_reduce_kernel<EP, PAIR>), dim3((n4 + 255) / 256), dim3(256), 0, st, a, ks);
+  }
   return check_launch();
 }
 
@@ -354,8 +434,11 @@ int launch_gemm(const GemmArgs& a, int ep, bool pair, hipStream_t st) {
     return Q4D_ERR_NULL;
   }
   if (ep == EP_RESID && !a.resid) return Q4D_ERR_NULL;
-  // small M (batched decode) uses 64-row tiles
-  return a.M <= 64 ? launch_gemm_bm<64>(a, ep, pair, st) : launch_gemm_bm<128>(a, ep, pair, st);
+  // small M (batched decode) uses 64-row tiles, and so does a large M whose
+  // 128-row tiles would leave CUs idle (prefill's N = 1024 projections)
+  const int nblk = pair ? a.N / 64 : a.N / kGemmBN;
+  const bool bm64 = a.M <= 64 || (size_t)nblk * ((a.M + 127) / 128) < 256;
+  return bm64 ? launch_gemm_bm<64>(a, ep, pair, st) : launch_gemm_bm<128>(a, ep, pair, st);
 }
 
 int launch_argmax_rows(const float* part_score, const int* part_idx, int nparts, int M, int32_t* out_token,

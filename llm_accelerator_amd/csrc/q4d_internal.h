@@ -56,6 +56,8 @@ struct WsLayout {
   size_t xh;         // f16 [batch, max(hidden, qh*d, intermediate)]  MFMA-path activations
   size_t row_score;  // f32 [batch, vocab/128]  batched LM-head argmax partials
   size_t row_idx;    // i32 [batch, vocab/128]
+  size_t gemm_part;  // f32 [8][batch][max(q|k|v rows, 2 x intermediate)] split-K partial tiles
+  size_t gemm_part_floats;
   size_t total;
   int nsplit_max;
   int lm_counter_index;  // index into counters
@@ -87,6 +89,11 @@ inline WsLayout ws_layout(const q4d_model_t* m, int batch) {
   L.xh = o;        o = align_up(o + (size_t)batch * wmax * 2, A);
   L.row_score = o; o = align_up(o + (size_t)batch * nparts * 4, A);
   L.row_idx = o;   o = align_up(o + (size_t)batch * nparts * 4, A);
+  {
+    const size_t w1 = (size_t)(qh + 2 * kvh) * d, w2 = 2 * (size_t)m->intermediate_size;
+    L.gemm_part_floats = 8 * (size_t)batch * (w1 > w2 ? w1 : w2);
+    L.gemm_part = o; o = align_up(o + L.gemm_part_floats * 4, A);
+  }
   L.total = o;
   return L;
 }
@@ -201,7 +208,17 @@ struct GemmArgs {
   float* logits;       // EP_ARGMAX: optional [M, N]
   float* part_score;   // EP_ARGMAX: [M, N/128]
   int* part_idx;
+  // Split-K (not for EP_ARGMAX): with `part` set, launch_gemm may split the K
+  // steps over ksplit blocks per output tile when the tiles alone would not
+  // fill the device; each writes its fp32 tile to part[z][M][N (PAIR: 2N)]
+  // and a reduction kernel sums the splits in order and applies the
+  // epilogue.  part_cap = floats available at `part`.  ksplit = 0 lets
+  // launch_gemm choose (ksplit = 1: no split).
+  float* part;
+  size_t part_cap;
+  int ksplit;
 };
+constexpr int kGemmMaxSplit = 16;
 int launch_gemm(const GemmArgs& a, int ep, bool pair, hipStream_t st);
 int launch_argmax_rows(const float* part_score, const int* part_idx, int nparts, int M, int32_t* out_token,
                        float* out_score, hipStream_t st);

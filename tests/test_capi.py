@@ -143,6 +143,22 @@ def test_batched_entry_validation_codes(lib):
     assert lib.q4d_gemm(ctypes.byref(w), FAKE + 2, 4, FAKE, 1, None, None) == -4
 
 
+def test_gemm_splitk_validation_codes(lib):
+    w = Q4dMatrix(FAKE, FAKE, 1024, 2048)
+    args = dict(x=FAKE, M=64, y=FAKE, dt=1, resid=None, part=FAKE, nbytes=64 * 1024 * 16 * 4, ks=16)
+
+    def call(**kw):
+        a = dict(args, **kw)
+        return lib.q4d_gemm_splitk(ctypes.byref(w), a["x"], a["M"], a["y"], a["dt"], a["resid"], a["part"],
+                                   a["nbytes"], a["ks"], None)
+    assert call(part=None) == -7
+    assert call(ks=17) == -11            # more than 16 splits
+    assert call(ks=-1) == -11
+    assert call(nbytes=64 * 1024 * 15 * 4) == -9   # 16 split tiles do not fit
+    assert call(part=FAKE + 4) == -4     # 16-byte aligned tiles
+    assert call(dt=0, resid=FAKE) == -13
+
+
 def test_prefill_validation_codes(lib):
     arr = _layers(2)
     m = _model(arr)

@@ -92,6 +92,60 @@ def test_gemm_epilogues_exact(dev):
     np.testing.assert_array_equal(r.cpu().numpy(), resid + ref.astype(np.float32))
 
 
+def gemm_splitk(w, x: torch.Tensor, ksplit: int, y_dtype=Q4D_F32, resid: torch.Tensor | None = None,
+                y: torch.Tensor | None = None) -> torch.Tensor:
+    rows, cols = w.shape
+    M = x.shape[0]
+    if y is None:
+        y = torch.empty((M, rows), dtype=torch.float16 if y_dtype == Q4D_F16 else torch.float32, device=x.device)
+    part = torch.full((max(ksplit, 16) * M * rows,), float("nan"), dtype=torch.float32, device=x.device)
+    desc = w.descriptor()
+    check(_lib.load().q4d_gemm_splitk(ctypes.byref(desc), x.data_ptr(), M, y.data_ptr(), y_dtype,
+                                      resid.data_ptr() if resid is not None else None, part.data_ptr(),
+                                      part.numel() * 4, ksplit, current_stream()), "q4d_gemm_splitk")
+    torch.cuda.synchronize()
+    return y
+
+
+@pytest.mark.parametrize("ksplit", [0, 2, 5, 16])
+@pytest.mark.parametrize("N,K,M", [(1024, 2048, 64), (1024, 3072, 37), (256, 1024, 1)])
+def test_gemm_splitk_integer_exact(dev, N, K, M, ksplit):
+    """Split-K on integer-exact inputs (every fp32 sum exact, whatever its
+    grouping) equals the float64 product bit for bit; ksplit = 0 lets the
+    library choose.  The partial buffer starts as NaN, so a split tile left
+    unwritten or read twice shows up."""
+    if ksplit > K // 64:
+        pytest.skip("more splits than K steps")
+    rng = np.random.default_rng(N + K + M + ksplit)
+    packed, scale, x, ref = exact_case(rng, N, K, M)
+    print(f"[gemm splitk] M={M} N={N} K={K} ksplit={ksplit}", flush=True)
+    w = q4(packed, scale)
+    xd = torch.from_numpy(x).to(dev)
+    y = gemm_splitk(w, xd, ksplit).cpu().numpy()
+    np.testing.assert_array_equal(y, ref.astype(np.float32))
+    y16 = gemm_splitk(w, xd, ksplit, Q4D_F16).cpu().numpy()
+    np.testing.assert_array_equal(y16, ref.astype(np.float32).astype(np.float16))
+    resid = rng.normal(size=ref.shape).astype(np.float32)
+    r = torch.from_numpy(resid).to(dev)
+    gemm_splitk(w, xd, ksplit, Q4D_F32, resid=r, y=r)  # in place, as the residual stream
+    np.testing.assert_array_equal(r.cpu().numpy(), resid + ref.astype(np.float32))
+
+
+def test_gemm_splitk_real_weights_match_unsplit(dev, golden):
+    f = golden("mlp_down_proj_real")
+    packed, scale = f["weight_packed"], f["scale_q2_14"]
+    N, K = packed.shape[0], packed.shape[1] * 2
+    x = np.random.default_rng(8).normal(size=(64, K)).astype(np.float16)
+    w = q4(packed, scale)
+    xd = torch.from_numpy(x).to(dev)
+    y1 = gemm(w, xd).cpu().numpy().astype(np.float64)
+    Wex = o.dequantize_q4(packed, scale, np.float64)
+    bound = np.abs(x.astype(np.float64)) @ np.abs(Wex).T
+    for ks in (3, 16):
+        y = gemm_splitk(w, xd, ks).cpu().numpy().astype(np.float64)
+        assert np.all(np.abs(y - y1) <= 2.0 ** -16 * bound + 1e-30), ks
+
+
 @pytest.mark.parametrize("name,M", [("mlp_gate_proj_real", 64), ("mlp_down_proj_real", 33)])
 def test_gemm_real_weights(dev, golden, name, M):
     f = golden(name)
