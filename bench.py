@@ -23,7 +23,10 @@ GB/s flushed and resident; the LM head alone; full 28-layer greedy decode
 tok/s (config 3: 64-token prompt, 256 generated); prefill of one 2048-token
 sequence (config 4: tok/s and TFLOP/s against the dense fp16 MFMA peak);
 batched decode of 64 sequences over 4096 cached positions (config 5: tok/s
-and GB/s of K/V + weights); and the oracle's CPU rate on the host cores.
+and GB/s of K/V + weights); a measured HBM rate (torch's device copy of
+512 MiB windows, read + written bytes) that ``roofline`` also quotes its
+rate against, beside the 8 TB/s vendor figure; and the oracle's CPU rate on
+the host cores.
 """
 
 from __future__ import annotations
@@ -336,6 +339,29 @@ def main():
         del fmodel
         torch.cuda.empty_cache()
 
+    if legs:
+        # measured HBM ceiling beside the 8 TB/s vendor figure: torch's device
+        # copy of 512 MiB windows rotating over 2 GiB (past the 256 MB cache),
+        # read + written bytes over the time
+        buf = torch.empty(2 << 30, dtype=torch.uint8, device=dev)
+        w = 512 << 20
+        for _ in range(2):
+            buf[w:2 * w].copy_(buf[:w])
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for i in range(8):
+            k = i % 2
+            buf[(2 * k + 1) * w:(2 * k + 2) * w].copy_(buf[2 * k * w:(2 * k + 1) * w])
+        e1.record()
+        torch.cuda.synchronize()
+        cms = e0.elapsed_time(e1) / 8
+        extras["hbm_copy"] = {"bytes_moved": 2 * w, "us": round(cms * 1e3, 1),
+                              "GBps": round(2 * w / (cms * 1e-3) / 1e9, 1)}
+        log(f"[bench] measured copy: {json.dumps(extras['hbm_copy'])}")
+        del buf
+        torch.cuda.empty_cache()
+
     if args.copy_calibration:
         # a plain copy of known size: its FETCH_SIZE / WRITE_SIZE per dispatch
         # converts the counters of the GEMV dispatches to bytes
@@ -352,6 +378,9 @@ def main():
         cpu = cpu_baseline(args.cpu_seconds, ctx, step_bytes)
         log(f"[bench] CPU baseline: {json.dumps(cpu)}")
 
+    if "hbm_copy" in extras:
+        roofline["measured_copy_GBps"] = extras["hbm_copy"]["GBps"]
+        roofline["frac_of_measured_copy"] = round(roofline["achieved"] / extras["hbm_copy"]["GBps"], 4)
     line = {"metric": METRIC, "value": round(value, 2), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
             "warmup": args.warmup, "ms_per_step": round(ms_per_step, 6), "higher_is_better": True,
             "scaling": "weak", "vs_baseline": None, "dtype": "q4xf32",
