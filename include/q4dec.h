@@ -214,6 +214,22 @@ int q4d_gemm(const q4d_matrix_t* w, const uint16_t* x, int32_t M, void* y, int32
 int q4d_gemm_splitk(const q4d_matrix_t* w, const uint16_t* x, int32_t M, void* y, int32_t y_dtype,
                     const float* resid, float* part, size_t part_bytes, int32_t ksplit, void* stream);
 
+/* Integer Q4 GEMV of the reference's fixed-point path, exact:
+ *   y_q26[n]    = sum_g scale[n,g] * sum_{j<64} x[64g+j] * q[n,64g+j]   (int64, Q26)
+ *   y_q12_12[n] = sat24(y_q26[n] >> 14)  (arithmetic shift, signed 24-bit saturation)
+ * x_int: Q12.12 (or Q4.12) activations as int32 in 24-bit signed range, [cols], 16-byte
+ * aligned; either output may be NULL; *saturated (may be NULL) is incremented once per
+ * saturated row.  cols % 64 == 0, cols <= 3072.
+ * Replaces compute_q4_gemv_q26 + q26_to_q12_12
+ * (Qwen3-0.6B-Base/python_each_module/28_export_mlp_gate_up_vectors.py:124-138) and
+ * q4_gemv_from_ints (13_export_q4_gemv_vectors.py:138-154). */
+int q4d_linear_q26(const q4d_matrix_t* w, const int32_t* x_int, int64_t* y_q26, int32_t* y_q12_12,
+                   int32_t* saturated, void* stream);
+
+/* Argmax over n int64 scores: the highest, and among equal scores the lowest index (the
+ * streamed LM-head scan, 56_export_persistent_multitoken_layer_golden.py:766-798,860). */
+int q4d_argmax_q26(const int64_t* scores, int32_t n, int32_t* out_token, int64_t* out_score, void* stream);
+
 /* ---- fused decode ---------------------------------------------------------- */
 /* One cached decoder layer (batch 1): hidden_out = layer(hidden_in); appends
  * K/V at positions[0] of the cache.  hidden_in and hidden_out may alias. */

@@ -86,6 +86,8 @@ SIGNATURES = {
     "q4d_lm_head_argmax_batch": ([POINTER(Q4dModel), _P, c_int32, _P, _P, _P, _P, c_size_t, _P], c_int32),
     "q4d_gemm": ([POINTER(Q4dMatrix), _P, c_int32, _P, c_int32, _P, _P], c_int32),
     "q4d_gemm_splitk": ([POINTER(Q4dMatrix), _P, c_int32, _P, c_int32, _P, _P, c_size_t, c_int32, _P], c_int32),
+    "q4d_linear_q26": ([POINTER(Q4dMatrix), _P, _P, _P, _P, _P], c_int32),
+    "q4d_argmax_q26": ([_P, c_int32, _P, _P, _P], c_int32),
     "q4d_decode_batch": ([POINTER(Q4dModel), _P, _P, c_int32, POINTER(Q4dKVCache), _P, _P, _P, _P, c_size_t, _P],
                          c_int32),
     "q4d_run_one_token": ([POINTER(Q4dModel), _P, _P, POINTER(Q4dKVCache), _P, _P, _P, _P, c_size_t, _P],

@@ -444,6 +444,23 @@ int q4d_gemm(const q4d_matrix_t* w, const uint16_t* x, int32_t M, void* y, int32
   return launch_gemm(a, resid ? EP_RESID : (y_dtype == Q4D_F16 ? EP_F16 : EP_F32), false, as_stream(stream));
 }
 
+int q4d_linear_q26(const q4d_matrix_t* w, const int32_t* x_int, int64_t* y_q26, int32_t* y_q12_12,
+                   int32_t* saturated, void* stream) {
+  if (!w || !x_int || (!y_q26 && !y_q12_12)) return Q4D_ERR_NULL;
+  if (!w->w || !w->s) return Q4D_ERR_NULL;
+  if (w->rows <= 0 || w->cols <= 0 || w->cols % 64 || w->cols > 3072) return Q4D_ERR_SHAPE;
+  if (!aligned(w->w, 16) || !aligned(w->s, 2) || !aligned(x_int, 16)) return Q4D_ERR_BAD_ADDR;
+  if ((y_q26 && !aligned(y_q26, 8)) || (y_q12_12 && !aligned(y_q12_12, 4))) return Q4D_ERR_BAD_ADDR;
+  return launch_gemv_q26(w, x_int, y_q26, y_q12_12, saturated, as_stream(stream));
+}
+
+int q4d_argmax_q26(const int64_t* scores, int32_t n, int32_t* out_token, int64_t* out_score, void* stream) {
+  if (!scores || !out_token || !out_score) return Q4D_ERR_NULL;
+  if (n <= 0) return Q4D_ERR_SHAPE;
+  if (!aligned(scores, 8) || !aligned(out_score, 8)) return Q4D_ERR_BAD_ADDR;
+  return launch_argmax_q26(scores, n, out_token, out_score, as_stream(stream));
+}
+
 int q4d_gemm_splitk(const q4d_matrix_t* w, const uint16_t* x, int32_t M, void* y, int32_t y_dtype,
                     const float* resid, float* part, size_t part_bytes, int32_t ksplit, void* stream) {
   if (!w || !part) return Q4D_ERR_NULL;

@@ -36,6 +36,9 @@ namespace q4d {
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 
 constexpr int kGemmBN = 128;
+// waves per block for 128- and 64-row tiles
+constexpr int kGemmWaves128 = 8;
+constexpr int kGemmWaves64 = 8;
 constexpr int kGemmBK = 64;
 constexpr int kGemmPad = 8;  // fp16 elements of padding per LDS row
 constexpr int kGemmLds = kGemmBK + kGemmPad;
@@ -83,13 +86,13 @@ __device__ __forceinline__ SegPtrs seg_ptrs(const GemmArgs& a) {
   return SegPtrs{a.w[0], a.w[1], a.w[2], a.s[0], a.s[1], a.s[2], a.seg_end[0], a.seg_end[1]};
 }
 
-template <int BM, bool PAIR>
+template <int BM, bool PAIR, int NT>
 __device__ __forceinline__ void gemm_load(const GemmArgs& a, const SegPtrs& P, int m0, int nblk, int k0, int t,
                                           GemmTileLoad& L) {
-  // X: BM x 64 fp16 = BM * 8 chunks of 16 B
+  // X: BM x 64 fp16 = BM * 8 chunks of 16 B, spread over the NT threads
 #pragma unroll
-  for (int i = 0; i < BM * 8 / 256; ++i) {
-    const int c = t + 256 * i;
+  for (int i = 0; i < BM * 8 / NT; ++i) {
+    const int c = t + NT * i;
     const int row = c >> 3, seg = c & 7;
     const int m = m0 + row;
     if (m < a.M)
@@ -97,7 +100,8 @@ __device__ __forceinline__ void gemm_load(const GemmArgs& a, const SegPtrs& P, i
     else
       L.x[i] = u32x4{0u, 0u, 0u, 0u};
   }
-  // W: 128 rows x 32 B; thread t -> row t/2, half t%2
+  // W: 128 rows x 32 B; thread t < 256 -> row t/2, half t%2 (the first four waves)
+  if (t >= 256) return;
   const int r = t >> 1, half = t & 1;
   const uint8_t* wb;
   const uint16_t* sb;
@@ -128,14 +132,15 @@ __device__ __forceinline__ void gemm_load(const GemmArgs& a, const SegPtrs& P, i
   L.s = sb[(size_t)grow * (a.K / 64) + k0 / 64];
 }
 
-template <int BM>
+template <int BM, int NT>
 __device__ __forceinline__ void gemm_store_lds(_Float16 (*As)[kGemmLds], _Float16 (*Bs)[kGemmLds], int t,
                                                const GemmTileLoad& L) {
 #pragma unroll
-  for (int i = 0; i < BM * 8 / 256; ++i) {
-    const int c = t + 256 * i;
+  for (int i = 0; i < BM * 8 / NT; ++i) {
+    const int c = t + NT * i;
     *reinterpret_cast<u32x4*>(&As[c >> 3][(c & 7) * 8]) = L.x[i];
   }
+  if (t >= 256) return;
   const int r = t >> 1, half = t & 1;
   const _Float16 sc = (_Float16)((float)L.s * (1.0f / 16384.0f));
   uint32_t out[16];
@@ -145,11 +150,15 @@ __device__ __forceinline__ void gemm_store_lds(_Float16 (*As)[kGemmLds], _Float1
   for (int q = 0; q < 4; ++q) dst[q] = u32x4{out[4 * q], out[4 * q + 1], out[4 * q + 2], out[4 * q + 3]};
 }
 
-template <int BM, int EP, bool PAIR>
-__global__ __launch_bounds__(256) void q4_gemm_kernel(const GemmArgs a) {
-  constexpr int WM = BM / 2;       // rows per wave
-  constexpr int MI = WM / 16;      // 16-row MFMA tiles per wave
-  constexpr int NI = 4;            // 16-col MFMA tiles per wave (64 columns)
+// NW waves per block: NW / 2 along M x 2 along N; each wave owns
+// (BM / (NW / 2)) x 64 of the output.
+template <int BM, int EP, bool PAIR, int NW>
+__global__ __launch_bounds__(NW * 64) void q4_gemm_kernel(const GemmArgs a) {
+  constexpr int NT = NW * 64;
+  constexpr int WM = BM / (NW / 2);  // rows per wave
+  constexpr int MI = WM / 16;        // 16-row MFMA tiles per wave
+  constexpr int NI = 4;              // 16-col MFMA tiles per wave (64 columns)
+  static_assert(MI >= 1 && BM * 8 % NT == 0, "tile / wave split");
   __shared__ _Float16 As[2][BM][kGemmLds];
   __shared__ _Float16 Bs[2][kGemmBN][kGemmLds];
   __shared__ float s_best[2][BM];
@@ -177,13 +186,13 @@ __global__ __launch_bounds__(256) void q4_gemm_kernel(const GemmArgs a) {
 
   const SegPtrs P = seg_ptrs(a);
   GemmTileLoad L;
-  gemm_load<BM, PAIR>(a, P, m0, nblk, k_begin * kGemmBK, t, L);
-  gemm_store_lds<BM>(As[0], Bs[0], t, L);
+  gemm_load<BM, PAIR, NT>(a, P, m0, nblk, k_begin * kGemmBK, t, L);
+  gemm_store_lds<BM, NT>(As[0], Bs[0], t, L);
   __syncthreads();
 
   for (int ks = 0; ks < nk; ++ks) {
     const int buf = ks & 1;
-    if (ks + 1 < nk) gemm_load<BM, PAIR>(a, P, m0, nblk, (k_begin + ks + 1) * kGemmBK, t, L);
+    if (ks + 1 < nk) gemm_load<BM, PAIR, NT>(a, P, m0, nblk, (k_begin + ks + 1) * kGemmBK, t, L);
 #pragma unroll
     for (int kk = 0; kk < 2; ++kk) {
       const int kc = kk * 32 + (lane >> 4) * 8;
@@ -197,7 +206,7 @@ __global__ __launch_bounds__(256) void q4_gemm_kernel(const GemmArgs a) {
         for (int j = 0; j < NI; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, bf[j], acc[i][j], 0, 0, 0);
       }
     }
-    if (ks + 1 < nk) gemm_store_lds<BM>(As[buf ^ 1], Bs[buf ^ 1], t, L);
+    if (ks + 1 < nk) gemm_store_lds<BM, NT>(As[buf ^ 1], Bs[buf ^ 1], t, L);
     __syncthreads();
   }
 
@@ -271,7 +280,7 @@ __global__ __launch_bounds__(256) void q4_gemm_kernel(const GemmArgs a) {
         }
       }
     __syncthreads();
-    for (int lr = t; lr < BM; lr += 256) {
+    for (int lr = t; lr < BM; lr += NT) {
       const int m = m0 + lr;
       if (m < a.M) {
         float bs = s_best[0][lr];
@@ -391,7 +400,8 @@ static int launch_gemm_inst(const GemmArgs& a, hipStream_t st) {
   if (ks > 1 && (!a.part || (size_t)ks * a.M * (PAIR ? 2 * a.N : a.N) > a.part_cap || a.N % 4 ||
                  ks > a.K / kGemmBK))
     return Q4D_ERR_CAPACITY;
-  hipLaunchKernelGGL((q4_gemm_kernel<BM, EP, PAIR>), dim3(nblk, mblk, ks), dim3(256), 0, st, a);
+  constexpr int NW = BM == 128 ? kGemmWaves128 : kGemmWaves64;
+  hipLaunchKernelGGL((q4_gemm_kernel<BM, EP, PAIR, NW>), dim3(nblk, mblk, ks), dim3(NW * 64), 0, st, a);
   int rc = check_launch();
   if (rc || ks == 1) return rc;
   if constexpr (EP != EP_ARGMAX) {

@@ -274,6 +274,11 @@ struct PersistArgs {
 bool persist_eligible(const q4d_model_t* m);
 int launch_persist(const PersistArgs& a, int xp, hipStream_t st);
 
+// ---- integer Q4 GEMV of the fixed-point path (q4d_int.hip) ------------------
+int launch_gemv_q26(const q4d_matrix_t* w, const int32_t* x, int64_t* y_q26, int32_t* y_q12, int32_t* saturated,
+                    hipStream_t st);
+int launch_argmax_q26(const int64_t* scores, int n, int32_t* tok, int64_t* score, hipStream_t st);
+
 int launch_prefill_rope(const PrefillArgs& a, hipStream_t st);
 int launch_prefill_attention(const PrefillArgs& a, hipStream_t st);
 

@@ -159,6 +159,19 @@ def test_gemm_splitk_validation_codes(lib):
     assert call(dt=0, resid=FAKE) == -13
 
 
+def test_integer_gemv_validation_codes(lib):
+    w = Q4dMatrix(FAKE, FAKE, 3072, 1024)
+    assert lib.q4d_linear_q26(ctypes.byref(w), FAKE, None, None, None, None) == -7   # no output
+    assert lib.q4d_linear_q26(ctypes.byref(w), None, FAKE, None, None, None) == -7
+    assert lib.q4d_linear_q26(ctypes.byref(Q4dMatrix(FAKE, FAKE, 8, 1000)), FAKE, FAKE, None, None, None) == -11
+    assert lib.q4d_linear_q26(ctypes.byref(Q4dMatrix(FAKE, FAKE, 8, 4096)), FAKE, FAKE, None, None, None) == -11
+    assert lib.q4d_linear_q26(ctypes.byref(w), FAKE + 4, FAKE, None, None, None) == -4  # 16-byte activations
+    assert lib.q4d_linear_q26(ctypes.byref(w), FAKE, FAKE + 4, None, None, None) == -4  # 8-byte int64 outputs
+    assert lib.q4d_argmax_q26(FAKE, 0, FAKE, FAKE, None) == -11
+    assert lib.q4d_argmax_q26(None, 5, FAKE, FAKE, None) == -7
+    assert lib.q4d_argmax_q26(FAKE + 4, 5, FAKE, FAKE, None) == -4
+
+
 def test_prefill_validation_codes(lib):
     arr = _layers(2)
     m = _model(arr)
