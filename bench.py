@@ -25,8 +25,10 @@ sequence (config 4: tok/s and TFLOP/s against the dense fp16 MFMA peak);
 batched decode of 64 sequences over 4096 cached positions (config 5: tok/s
 and GB/s of K/V + weights); a measured HBM rate (torch's device copy of
 512 MiB windows, read + written bytes) that ``roofline`` also quotes its
-rate against, beside the 8 TB/s vendor figure; and the oracle's CPU rate on
-the host cores.
+rate against, beside the 8 TB/s vendor figure; and the oracle's CPU rates on
+the host cores (``cpu_baseline``: the config-2 layer step on all cores;
+``extras.cpu_legs``: config 1 as an fp32 matvec and as the int64 Q26
+restatement, config 2 on one thread, config 3 per token).
 """
 
 from __future__ import annotations
@@ -377,6 +379,8 @@ def main():
     if not args.no_cpu and legs:
         cpu = cpu_baseline(args.cpu_seconds, ctx, step_bytes)
         log(f"[bench] CPU baseline: {json.dumps(cpu)}")
+        extras["cpu_legs"] = cpu_extra_legs(ctx, step_bytes)
+        log(f"[bench] CPU legs: {json.dumps(extras['cpu_legs'])}")
 
     if "hbm_copy" in extras:
         roofline["measured_copy_GBps"] = extras["hbm_copy"]["GBps"]
@@ -424,6 +428,76 @@ def cpu_baseline(seconds, ctx, step_bytes):
             "sample": f"{n} fp32 numpy layer steps at ctx {ctx} (oracle restatement of common.py:231-298), "
                       f"{dt * 1e3:.2f} ms/step; os.cpu_count()={os.cpu_count()}, "
                       f"affinity={len(os.sched_getaffinity(0))}"}
+
+
+def _median_time(fn, reps, budget_s):
+    fn()
+    ts = []
+    t_end = time.perf_counter() + budget_s
+    while len(ts) < reps or (time.perf_counter() < t_end and len(ts) < 10 * reps):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    ts.sort()
+    return ts[len(ts) // 2], len(ts)
+
+
+def cpu_extra_legs(ctx, step_bytes):
+    """The other CPU baselines: config 1 (fp32 matvec on pre-dequantised
+    weights as manual_linear_from_weight holds them, common.py:137-145, and the
+    int64 Q26 restatement of compute_q4_gemv_q26, 28_export_mlp_gate_up_vectors.py:124-133),
+    the config-2 layer step on one thread, and config 3 (run_manual_one_token,
+    10_validate_full_run_one_token.py:17-56, 8 serial steps of the 28-layer
+    model, per token).  Medians of >= 10 timed runs after a warm-up."""
+    import numpy as np
+
+    import oracle as o
+    from llm_accelerator_amd import model as M
+    try:
+        from threadpoolctl import threadpool_limits
+    except Exception:  # threadpoolctl missing: no one-thread leg
+        threadpool_limits = None
+    out = {"cores": os.cpu_count(), "affinity": len(os.sched_getaffinity(0))}
+    rng = np.random.default_rng(0)
+    packed, scale = M.random_q4(rng, 3072, 1024)
+    W = o.dequantize_q4(packed, scale, np.float32)
+    q = o.unpack_signed_int4(packed, 1024)
+    x = rng.normal(size=1024).astype(np.float32)
+    xi = rng.integers(-(1 << 20), 1 << 20, size=1024)
+    gb = M.gemv_bytes(3072, 1024)
+    t, n = _median_time(lambda: W @ x, 10, 2.0)
+    out["c1_fp32"] = {"us": round(t * 1e6, 1), "GBps": round(gb / t / 1e9, 2), "runs": n}
+    t, n = _median_time(lambda: o.q4_gemv_q26(xi, q, scale), 10, 2.0)
+    out["c1_int64_q26"] = {"us": round(t * 1e6, 1), "GBps": round(gb / t / 1e9, 3), "runs": n}
+    if threadpool_limits is not None:
+        cfg = M.Qwen3Config(num_hidden_layers=1, vocab_size=2048)
+        host = M.random_host_weights(cfg, seed=0, num_layers=1)
+        om = o.OracleModel.from_q4(o.OracleConfig(num_hidden_layers=1, vocab_size=2048), host["layers"],
+                                   *host["embed_tokens"], host["norm"])
+        k = rng.normal(size=(1, 8, ctx, 128)).astype(np.float32)
+        v = rng.normal(size=(1, 8, ctx, 128)).astype(np.float32)
+        h = rng.normal(size=(1, 1, 1024)).astype(np.float32)
+        pos = np.array([[ctx]])
+        with threadpool_limits(limits=1):
+            t, n = _median_time(lambda: o.manual_decoder_layer_cached(h, om.layers[0], om.config, om.inv_freq,
+                                                                      pos, k, v), 10, 3.0)
+        out["c2_one_thread"] = {"ms_per_step": round(t * 1e3, 3), "GBps": round(step_bytes / t / 1e9, 3),
+                                "runs": n}
+    fcfg = M.Qwen3Config()
+    fhost = M.random_host_weights(fcfg, seed=0)
+    om = o.OracleModel.from_q4(o.OracleConfig(), fhost["layers"], *fhost["embed_tokens"], fhost["norm"])
+    del fhost
+    kc, vc = [None] * fcfg.num_hidden_layers, [None] * fcfg.num_hidden_layers
+    toks = rng.integers(0, fcfg.vocab_size, 8)
+    ts = []
+    for p, tk in enumerate(toks):
+        t0 = time.perf_counter()
+        o.run_manual_one_token(np.array([[int(tk)]]), p, om, kc, vc)
+        ts.append(time.perf_counter() - t0)
+    tt = sorted(ts[1:])[len(ts[1:]) // 2]
+    out["c3_per_token"] = {"ms": round(tt * 1e3, 1), "tok_s": round(1.0 / tt, 2), "steps": len(ts),
+                           "note": "median of steps 1-7 at positions 1-7 (the first step is the warm-up)"}
+    return out
 
 
 if __name__ == "__main__":
