@@ -290,6 +290,123 @@ int q4d_advance(int32_t* tokens, int32_t* positions, const int32_t* next_token, 
                 int32_t* hist_tokens, float* hist_scores, int32_t* hist_count, int32_t hist_capacity,
                 void* stream);
 
+/* ---- fixed-point (RTL-exact) decode ------------------------------------------
+ * The integer arithmetic of the reference's FPGA datapath, bit for bit
+ * (Qwen3-0.6B-Base/python_each_module/56_export_persistent_multitoken_layer_golden.py:468-561
+ * and the stage exporters it loads, :862-875).  Formats (56_...:1087-1095):
+ *   hidden state / layer output   signed 24-bit Q14.10 in int32
+ *   norm, projection, RoPE, attention and MLP values   signed 24-bit Q12.12 in int32
+ *   gammas Q8.7 and RoPE cos/sin Q1.15 in int16; scores Q24.24 int64; probabilities
+ *   unsigned Q0.16; LM-head logits Q26 int64.
+ * Shifts are arithmetic (floor); every stage output saturates to signed 24 bits.
+ * The Q4 matrices are those of q4d_model_t (same layout); the KV cache holds int32 Q12.12
+ * words in the reference's physical order [layer][K/V][kv_head][position][dim]
+ * (23_export_kv_cache_append_vectors.py:64-84).  Batch 1, max_ctx <= 4096. */
+typedef struct q4d_fixed_layer {
+  const int16_t* input_gamma;  /* [hidden] Q8.7 */
+  const int16_t* post_gamma;   /* [hidden] Q8.7 */
+  const int16_t* q_gamma;      /* [head_dim] Q8.7 */
+  const int16_t* k_gamma;      /* [head_dim] Q8.7 */
+} q4d_fixed_layer_t;
+
+typedef struct q4d_fixed_model {
+  const q4d_model_t* base;          /* shapes, layers[l].*_proj and the tied embed_tokens (Q4);
+                                       its float norm/RoPE pointers are not read */
+  const q4d_fixed_layer_t* layers;  /* host array [base->num_layers] */
+  const int16_t* final_gamma;       /* [hidden] Q8.7 */
+  const int16_t* rope_cos;          /* [base->max_ctx, head_dim] Q1.15 (54_export_rope_runtime_table.py) */
+  const int16_t* rope_sin;          /* [base->max_ctx, head_dim] Q1.15 */
+  int32_t score_scale_q0_31;        /* round(head_dim**-0.5 * 2**31) (56_...:449-451) */
+} q4d_fixed_model_t;
+
+typedef struct q4d_fixed_kv {
+  int32_t* data;  /* [num_layers][2][num_kv_heads][max_ctx][head_dim] int32 Q12.12 */
+  int32_t num_layers;
+  int32_t num_kv_heads;
+  int32_t max_ctx;
+  int32_t head_dim;
+} q4d_fixed_kv_t;
+
+/* Saturation / status counters of the fixed-point workspace (q4d_fixed_read_counts),
+ * one per stage, as in the per-position "saturation" record of 56_...:634-650. */
+enum {
+  Q4D_FX_STATUS = 0,  /* device status bits (Q4D_STATUS_*) */
+  Q4D_FX_SAT_INPUT_NORM = 1, Q4D_FX_SAT_QKV = 2, Q4D_FX_SAT_QK_NORM = 3, Q4D_FX_SAT_ROPE = 4,
+  Q4D_FX_SAT_ATTENTION = 5, Q4D_FX_SAT_O_PROJ = 6, Q4D_FX_SAT_POST_RESIDUAL = 7,
+  Q4D_FX_SAT_POST_NORM = 8, Q4D_FX_SAT_GATE = 9, Q4D_FX_SAT_UP = 10, Q4D_FX_SAT_SILU = 11,
+  Q4D_FX_SAT_MLP_HIDDEN = 12, Q4D_FX_SAT_DOWN = 13, Q4D_FX_SAT_LAYER_RESIDUAL = 14,
+  Q4D_FX_SAT_FINAL_NORM = 15, Q4D_FX_COUNTS = 16
+};
+
+/* Host only (no device access): the exp LUT (n_exp = 257: round(exp(-i/16) * 2**20),
+ * 46_export_chained_attention_score_value_vectors.py:88-93) and the sigmoid LUT
+ * (n_sigmoid = 1025: round(sigmoid(-8 + i/64) * 2**16) clipped to 65535,
+ * 29_export_mlp_silu_mul_vectors.py:77-83). */
+int q4d_fixed_tables(int32_t* exp_lut, int32_t n_exp, int32_t* sigmoid_lut, int32_t n_sigmoid);
+/* Workspace of the fixed-point decode (256-byte aligned); init uploads the LUTs and clears
+ * the counters. */
+size_t q4d_fixed_workspace_bytes(const q4d_fixed_model_t* model);
+int q4d_fixed_workspace_init(void* ws, size_t ws_bytes, const q4d_fixed_model_t* model, void* stream);
+/* Copies the Q4D_FX_COUNTS counters to host memory (synchronises the stream). */
+int q4d_fixed_read_counts(const void* ws, size_t ws_bytes, int32_t* counts, int32_t n, void* stream);
+
+/* Stage entry points (device buffers; the fused calls below run the same device code). */
+/* Integer RMSNorm of `rows` vectors of `dim` elements.  kind 0 = hidden (Q14.10 in,
+ * mean >> 10, eps 1, 2**26 / rms, output >> 21; 17_export_rmsnorm_fixed_vectors.py:108-150,
+ * 27_...:110-149, 32_...:101-141), kind 1 = head (Q12.12 in, mean >> 7, eps 17, 2**28 / rms,
+ * output >> 23; 22_export_qk_norm_rope_fixed_vectors.py:127-166; dim must be 128).
+ * stats (may be NULL): int64 [rows][6] = sum_squares, mean_square, sqrt_radicand, rms,
+ * inv_rms, saturated elements. */
+int q4d_fixed_rms_norm(const int32_t* x, const int16_t* gamma, int32_t rows, int32_t dim, int32_t kind,
+                       int32_t* y, int64_t* stats, void* stream);
+/* Per-head q/k RMSNorm then RoPE of one position (22_...:169-212): q [q_heads,128],
+ * k [kv_heads,128] Q12.12; cos/sin: the position's Q1.15 table row [128].  q_norm / k_norm
+ * (may be NULL) receive the normalised heads.  With q_gamma and k_gamma both NULL the norm
+ * is skipped and the inputs are rotated as given (fixed_rope_reference alone, 18_...). */
+int q4d_fixed_qk_norm_rope(const int32_t* q, const int32_t* k, int32_t q_heads, int32_t kv_heads,
+                           const int16_t* q_gamma, const int16_t* k_gamma, const int16_t* cos_row,
+                           const int16_t* sin_row, int32_t* q_rope, int32_t* k_rope, int32_t* q_norm,
+                           int32_t* k_norm, void* stream);
+/* Attention of one token over cache positions 0 .. cache_length-1 of `layer`
+ * (attention_score_value, 56_...:347-381): raw[h,p] = q_h . k_p (int64), scaled =
+ * (raw * score_scale) >> 31, LUT softmax (46_...:96-121), out = sat24((sum_p prob * v) >> 16).
+ * q_rope [q_heads,128]; exp_lut: device int32 [257] (q4d_fixed_tables).  raw, scaled
+ * (int64), lut_index, prob (int32) [q_heads, cache_length] may be NULL. */
+int q4d_fixed_attention(const q4d_fixed_kv_t* kv, int32_t layer, int32_t q_heads, int32_t cache_length,
+                        const int32_t* q_rope, int32_t score_scale_q0_31, const int32_t* exp_lut,
+                        int32_t* out, int64_t* raw, int64_t* scaled, int32_t* lut_index, int32_t* prob,
+                        void* stream);
+/* Writes k [kv_heads,128] and v [kv_heads,128] at positions[0] of `layer` (23_...:64-84). */
+int q4d_fixed_kv_append(const q4d_fixed_kv_t* kv, int32_t layer, const int32_t* positions,
+                        const int32_t* k, const int32_t* v, void* stream);
+/* SwiGLU of the fixed path (29_export_mlp_silu_mul_vectors.py:86-93, 56_...:547-556):
+ * index = gate on the 1/64 grid of [-8, 8]; silu = sat24((gate * lut[index]) >> 16);
+ * hidden = sat24((silu * up) >> 12).  sigmoid_lut: device int32 [1025]; lut_index,
+ * sigmoid, silu_gate may be NULL. */
+int q4d_fixed_silu_mul(const int32_t* gate, const int32_t* up, int32_t n, const int32_t* sigmoid_lut,
+                       int32_t* hidden, int32_t* lut_index, int32_t* sigmoid, int32_t* silu_gate,
+                       void* stream);
+/* out = sat24(hidden + (x >> 2)): a Q12.12 branch output onto the Q14.10 residual stream
+ * (56_...:530-533, 558-561). */
+int q4d_fixed_residual_add(const int32_t* hidden, const int32_t* x, int32_t n, int32_t* out, void* stream);
+/* Q14.10 embedding rows of the tied Q4 table: (q * scale) >> 4 (56_...:214-221). */
+int q4d_fixed_embedding(const q4d_matrix_t* table, const int32_t* tokens, int32_t n, int32_t* hidden,
+                        void* stream);
+
+/* One fixed-point decoder layer at positions[0] (run_fixed_layer, 56_...:468-561): input
+ * norm + q|k|v, q/k norm + RoPE + KV append + attention, o_proj + residual, post norm +
+ * gate/up + SiLU*up, down + residual.  hidden_in / hidden_out: Q14.10 [hidden]; may alias. */
+int q4d_fixed_decoder_layer(const q4d_fixed_model_t* model, int32_t layer, const int32_t* hidden_in,
+                            int32_t* hidden_out, const q4d_fixed_kv_t* kv, const int32_t* positions,
+                            void* ws, size_t ws_bytes, void* stream);
+/* Embedding, every layer, final RMSNorm and the full-vocabulary tied-Q4 LM-head scan
+ * (56_...:684-798): next_token[0] = the highest Q26 logit, lowest row on ties;
+ * score[0] its Q26 value; logits (int64 [vocab]) optional; hidden_out (Q14.10 [hidden],
+ * the last layer's output) optional. */
+int q4d_fixed_run_one_token(const q4d_fixed_model_t* model, const int32_t* tokens, const int32_t* positions,
+                            const q4d_fixed_kv_t* kv, int32_t* next_token, int64_t* score, int64_t* logits,
+                            int32_t* hidden_out, void* ws, size_t ws_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -62,7 +62,27 @@ class Q4dKVCache(ctypes.Structure):
                 ("max_ctx", c_int32), ("head_dim", c_int32)]
 
 
+class Q4dFixedLayer(ctypes.Structure):
+    _fields_ = [("input_gamma", c_void_p), ("post_gamma", c_void_p), ("q_gamma", c_void_p), ("k_gamma", c_void_p)]
+
+
+class Q4dFixedModel(ctypes.Structure):
+    _fields_ = [("base", POINTER(Q4dModel)), ("layers", POINTER(Q4dFixedLayer)), ("final_gamma", c_void_p),
+                ("rope_cos", c_void_p), ("rope_sin", c_void_p), ("score_scale_q0_31", c_int32)]
+
+
+class Q4dFixedKV(ctypes.Structure):
+    _fields_ = [("data", c_void_p), ("num_layers", c_int32), ("num_kv_heads", c_int32), ("max_ctx", c_int32),
+                ("head_dim", c_int32)]
+
+
+# Fixed-point workspace counters (Q4D_FX_* in include/q4dec.h).
+FX_COUNT_NAMES = ["status", "input_norm", "qkv", "qk_norm", "rope", "attention", "o_proj", "post_residual",
+                  "post_norm", "gate", "up", "silu", "mlp_hidden", "down", "layer_residual", "final_norm"]
+
 _P = c_void_p
+_FM = POINTER(Q4dFixedModel)
+_FKV = POINTER(Q4dFixedKV)
 SIGNATURES = {
     "q4d_version": ([], c_int32),
     "q4d_status_string": ([c_int32], ctypes.c_char_p),
@@ -97,6 +117,19 @@ SIGNATURES = {
     "q4d_prefill_workspace_bytes": ([POINTER(Q4dModel), c_int32], c_size_t),
     "q4d_prefill": ([POINTER(Q4dModel), _P, c_int32, c_int32, c_int32, POINTER(Q4dKVCache), _P, _P, _P, _P,
                      c_size_t, _P], c_int32),
+    "q4d_fixed_tables": ([_P, c_int32, _P, c_int32], c_int32),
+    "q4d_fixed_workspace_bytes": ([_FM], c_size_t),
+    "q4d_fixed_workspace_init": ([_P, c_size_t, _FM, _P], c_int32),
+    "q4d_fixed_read_counts": ([_P, c_size_t, _P, c_int32, _P], c_int32),
+    "q4d_fixed_rms_norm": ([_P, _P, c_int32, c_int32, c_int32, _P, _P, _P], c_int32),
+    "q4d_fixed_qk_norm_rope": ([_P, _P, c_int32, c_int32, _P, _P, _P, _P, _P, _P, _P, _P, _P], c_int32),
+    "q4d_fixed_attention": ([_FKV, c_int32, c_int32, c_int32, _P, c_int32, _P, _P, _P, _P, _P, _P, _P], c_int32),
+    "q4d_fixed_kv_append": ([_FKV, c_int32, _P, _P, _P, _P], c_int32),
+    "q4d_fixed_silu_mul": ([_P, _P, c_int32, _P, _P, _P, _P, _P, _P], c_int32),
+    "q4d_fixed_residual_add": ([_P, _P, c_int32, _P, _P], c_int32),
+    "q4d_fixed_embedding": ([POINTER(Q4dMatrix), _P, c_int32, _P, _P], c_int32),
+    "q4d_fixed_decoder_layer": ([_FM, c_int32, _P, _P, _FKV, _P, _P, c_size_t, _P], c_int32),
+    "q4d_fixed_run_one_token": ([_FM, _P, _P, _FKV, _P, _P, _P, _P, _P, c_size_t, _P], c_int32),
 }
 
 _lib = None
