@@ -64,9 +64,9 @@ def parse():
     ap.add_argument("--copies", type=int, default=40)
     ap.add_argument("--precision", type=int, default=2, choices=(1, 2))
     ap.add_argument("--no-extras", action="store_true", help="skip every leg beside the layer step")
-    ap.add_argument("--extras", default="c1,c3,c4,c5",
+    ap.add_argument("--extras", default="c1,c3,c4,c5,fx",
                     help="comma list of the legs to run beside the layer step: c1 GEMV, c3 decode + LM head, "
-                         "c4 prefill, c5 batched decode")
+                         "c4 prefill, c5 batched decode, fx fixed-point (RTL-exact) layer and token")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--decode-gen", type=int, default=256)
@@ -202,8 +202,8 @@ def main():
     torch.cuda.empty_cache()
 
     legs = set() if args.no_extras else {x.strip() for x in args.extras.split(",") if x.strip()}
-    if legs - {"c1", "c3", "c4", "c5"}:
-        sys.exit(f"unknown legs {sorted(legs - {'c1', 'c3', 'c4', 'c5'})}")
+    if legs - {"c1", "c3", "c4", "c5", "fx"}:
+        sys.exit(f"unknown legs {sorted(legs - {'c1', 'c3', 'c4', 'c5', 'fx'})}")
     if "c1" in legs:
         # -------------------------------------------------------- C1 GEMV
         from llm_accelerator_amd.model import Q4Tensor, gemv_bytes, random_q4
@@ -231,11 +231,13 @@ def main():
         del P, S, g1, g2
         torch.cuda.empty_cache()
 
-    if legs & {"c3", "c4", "c5"}:
+    if legs & {"c3", "c4", "c5", "fx"}:
         fcfg = M.Qwen3Config()
         t = time.time()
         fhost = M.random_host_weights(fcfg, seed=0)
         fmodel = M.build_model(fcfg, fhost, max_ctx=max(64 + args.decode_gen + 16, C5_CTX + 1), device=dev)
+        norm_keys = ("input_layernorm", "post_attention_layernorm", "q_norm", "k_norm")
+        fnorms = {"layers": [{k: L[k] for k in norm_keys} for L in fhost["layers"]], "norm": fhost["norm"]}
         del fhost
         log(f"[bench] 28-layer model setup {time.time() - t:.1f}s")
     if "c3" in legs:
@@ -337,7 +339,51 @@ def main():
                                        "status": bd.status()}
         log(f"[bench] C5 batched decode: {json.dumps(extras['c5_batched_decode'])}")
         del bkv, bd
-    if legs & {"c3", "c4", "c5"}:
+    if "fx" in legs:
+        # -------------------------------------------------------- fixed-point (RTL-exact) decode
+        from llm_accelerator_amd.fixed import FixedQ4Model
+        fxm = FixedQ4Model(M.with_context(fmodel, ctx + 1), fnorms)
+        fkv = fxm.new_cache()
+        fkv.data.copy_(torch.randint(-8192, 8192, fkv.data.shape, generator=gen, device=dev, dtype=torch.int32))
+        fdesc, fkvd = fxm.descriptor(), fkv.descriptor()
+        fpos = torch.tensor([ctx], dtype=torch.int32, device=dev)
+        fh = torch.randint(-4096, 4096, (1024,), generator=gen, device=dev, dtype=torch.int32)
+        fo = torch.empty_like(fh)
+
+        def fx_layer(i):
+            check(lib.q4d_fixed_decoder_layer(ctypes.byref(fdesc), i, fh.data_ptr(), fo.data_ptr(),
+                                              ctypes.byref(fkvd), fpos.data_ptr(), fxm.ws.data_ptr(), fxm.ws_bytes,
+                                              st()), "q4d_fixed_decoder_layer")
+        L = fcfg.num_hidden_layers
+        g_fx = graph_of(fx_layer, L, torch)
+        g_fx.replay()
+        fx_us = time_graph(g_fx, 10, torch) / L * 1e3
+        fx_bytes = M.fixed_layer_bytes(fcfg, ctx)
+        # one-token steps: serial prompt of 64 tokens, then graphs of 16 steps feeding the argmax back
+        ftok = torch.tensor([1], dtype=torch.int32, device=dev)
+        fnxt = torch.zeros(1, dtype=torch.int32, device=dev)
+        fscore = torch.zeros(1, dtype=torch.int64, device=dev)
+        fpos.zero_()
+
+        def fx_token(i):
+            check(lib.q4d_fixed_run_one_token(ctypes.byref(fdesc), ftok.data_ptr(), fpos.data_ptr(),
+                                              ctypes.byref(fkvd), fnxt.data_ptr(), fscore.data_ptr(), None, None,
+                                              fxm.ws.data_ptr(), fxm.ws_bytes, st()), "q4d_fixed_run_one_token")
+            ftok.copy_(fnxt)
+            fpos.add_(1)
+        for i in range(64):
+            fx_token(i)
+        g_tok = graph_of(fx_token, 16, torch)
+        g_tok.replay()
+        tok_ms = time_graph(g_tok, (args.decode_gen - 16) // 16, torch) / 16
+        counts = fxm.counts()
+        extras["fx_fixed_point"] = {
+            "layer_us": round(fx_us, 3), "layer_bytes": fx_bytes, "layer_GBps": round(fx_bytes / fx_us / 1e3, 1),
+            "token_ms": round(tok_ms, 4), "tok_s": round(1e3 / tok_ms, 1), "positions": [64, int(fpos.item())],
+            "status": counts["status"]}
+        log(f"[bench] fixed-point decode: {json.dumps(extras['fx_fixed_point'])}")
+        del fxm, fkv, g_fx, g_tok
+    if legs & {"c3", "c4", "c5", "fx"}:
         del fmodel
         torch.cuda.empty_cache()
 

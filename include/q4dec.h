@@ -347,7 +347,8 @@ int q4d_fixed_tables(int32_t* exp_lut, int32_t n_exp, int32_t* sigmoid_lut, int3
  * the counters. */
 size_t q4d_fixed_workspace_bytes(const q4d_fixed_model_t* model);
 int q4d_fixed_workspace_init(void* ws, size_t ws_bytes, const q4d_fixed_model_t* model, void* stream);
-/* Copies the Q4D_FX_COUNTS counters to host memory (synchronises the stream). */
+/* Copies the first n (<= Q4D_FX_COUNTS) counters to host memory, each summed over the
+ * workspace's 64 stripes of counter words (synchronises the stream). */
 int q4d_fixed_read_counts(const void* ws, size_t ws_bytes, int32_t* counts, int32_t n, void* stream);
 
 /* Stage entry points (device buffers; the fused calls below run the same device code). */
@@ -371,11 +372,14 @@ int q4d_fixed_qk_norm_rope(const int32_t* q, const int32_t* k, int32_t q_heads, 
  * (attention_score_value, 56_...:347-381): raw[h,p] = q_h . k_p (int64), scaled =
  * (raw * score_scale) >> 31, LUT softmax (46_...:96-121), out = sat24((sum_p prob * v) >> 16).
  * q_rope [q_heads,128]; exp_lut: device int32 [257] (q4d_fixed_tables).  raw, scaled
- * (int64), lut_index, prob (int32) [q_heads, cache_length] may be NULL. */
+ * (int64), lut_index, prob (int32) [q_heads, cache_length] may be NULL.  ws: 256-byte
+ * aligned scratch of q4d_fixed_attention_workspace_bytes(q_heads, kv->max_ctx) bytes (scores
+ * and chunk maxima between the two launches). */
+size_t q4d_fixed_attention_workspace_bytes(int32_t q_heads, int32_t max_ctx);
 int q4d_fixed_attention(const q4d_fixed_kv_t* kv, int32_t layer, int32_t q_heads, int32_t cache_length,
                         const int32_t* q_rope, int32_t score_scale_q0_31, const int32_t* exp_lut,
                         int32_t* out, int64_t* raw, int64_t* scaled, int32_t* lut_index, int32_t* prob,
-                        void* stream);
+                        void* ws, size_t ws_bytes, void* stream);
 /* Writes k [kv_heads,128] and v [kv_heads,128] at positions[0] of `layer` (23_...:64-84). */
 int q4d_fixed_kv_append(const q4d_fixed_kv_t* kv, int32_t layer, const int32_t* positions,
                         const int32_t* k, const int32_t* v, void* stream);

@@ -123,7 +123,9 @@ SIGNATURES = {
     "q4d_fixed_read_counts": ([_P, c_size_t, _P, c_int32, _P], c_int32),
     "q4d_fixed_rms_norm": ([_P, _P, c_int32, c_int32, c_int32, _P, _P, _P], c_int32),
     "q4d_fixed_qk_norm_rope": ([_P, _P, c_int32, c_int32, _P, _P, _P, _P, _P, _P, _P, _P, _P], c_int32),
-    "q4d_fixed_attention": ([_FKV, c_int32, c_int32, c_int32, _P, c_int32, _P, _P, _P, _P, _P, _P, _P], c_int32),
+    "q4d_fixed_attention_workspace_bytes": ([c_int32, c_int32], c_size_t),
+    "q4d_fixed_attention": ([_FKV, c_int32, c_int32, c_int32, _P, c_int32, _P, _P, _P, _P, _P, _P, _P, c_size_t, _P],
+                            c_int32),
     "q4d_fixed_kv_append": ([_FKV, c_int32, _P, _P, _P, _P], c_int32),
     "q4d_fixed_silu_mul": ([_P, _P, c_int32, _P, _P, _P, _P, _P, _P], c_int32),
     "q4d_fixed_residual_add": ([_P, _P, c_int32, _P, _P], c_int32),

@@ -36,7 +36,7 @@ namespace {
 constexpr int kFxMaxCtx = 4096;  // positions one attention block keeps in LDS
 constexpr int kFxExpLut = 257;
 constexpr int kFxSigLut = 1025;
-constexpr int kFxRowsLm = 4;     // rows per wave of the LM-head scan (16 per block)
+constexpr int kFxRowsLm = 8;     // rows per wave of the LM-head scan (32 per block)
 constexpr int kFxLmRowsPerBlock = 4 * kFxRowsLm;
 
 typedef int i32x4 __attribute__((ext_vector_type(4)));
@@ -127,18 +127,31 @@ __device__ __forceinline__ unsigned long long udiv_small(unsigned long long a, u
   return q;
 }
 
+// Saturation counters: kFxStripes copies of the Q4D_FX_COUNTS words, 256 bytes apart, so
+// that the waves of a saturating launch spread their atomics over many L2 channels
+// instead of queueing on one word (the host sums the stripes).
+constexpr int kFxStripes = 64;
+constexpr int kFxStripeWords = 64;
+
+// Adds the wave's saturation count to its stripe of counter `slot`: one atomic per wave,
+// none when no lane saturated.  Called by every lane of a wave (wave-uniform control flow).
 __device__ __forceinline__ void count(int32_t* counts, int slot, int n) {
-  if (counts && n) atomicAdd(counts + slot, n);
+  if (!counts || __ballot(n != 0) == 0) return;
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) n += __shfl_xor(n, m, kWave);
+  const int stripe = (int)((blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6)) & (kFxStripes - 1));
+  if ((threadIdx.x & 63) == 0) atomicAdd(counts + stripe * kFxStripeWords + slot, n);
 }
 
 // sum_{i<16} x_i * q_i for the 16 columns of an 8-byte weight word pair (column i in
 // bits 4i..4i+3, signed).  |x| <= 2^23: the sum fits int32.
+// x is a saturated 24-bit value and q a 4-bit code, so the 24-bit multiply is exact.
 __device__ __forceinline__ int dot16(uint32_t w0, uint32_t w1, const int (&x)[16]) {
   int s = 0;
 #pragma unroll
-  for (int i = 0; i < 8; ++i) s += x[i] * (((int)(w0 << (28 - 4 * i))) >> 28);
+  for (int i = 0; i < 8; ++i) s += __mul24(x[i], ((int)(w0 << (28 - 4 * i))) >> 28);
 #pragma unroll
-  for (int i = 0; i < 8; ++i) s += x[8 + i] * (((int)(w1 << (28 - 4 * i))) >> 28);
+  for (int i = 0; i < 8; ++i) s += __mul24(x[8 + i], ((int)(w1 << (28 - 4 * i))) >> 28);
   return s;
 }
 
@@ -175,30 +188,13 @@ __global__ __launch_bounds__(256) void fx_gemv_kernel(const FxGemv a) {
   __shared__ __align__(16) int xs[KC * 1280];
   __shared__ long long red[4];
   const int t = threadIdx.x, lane = t & 63, wid = t >> 6;
-  if constexpr (PRO == FX_PRO_NORM) {
-    static_assert(KC == 1, "the norm prologue covers the 1024-wide hidden state");
-    int xv[4];
-    long long ss = 0;
+  // 1. activation loads first, then every weight / scale load of this wave: the weights
+  //    stream in while the prologue runs (its barriers wait on LDS only)
+  constexpr int NX = PRO == FX_PRO_NORM ? 4 : KC * 4;
+  int xv[NX];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      xv[i] = a.x[t + 256 * i];
-      ss += (long long)xv[i] * xv[i];
-    }
-    ss = wave_sum_ll(ss);
-    if (lane == 0) red[wid] = ss;
-    __syncthreads();
-    const NormParams p = norm_params(red[0] + red[1] + red[2] + red[3], 0);
-    int nsat = 0;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int c = t + 256 * i;
-      xs[c + (c >> 4) * 4] = norm_apply(xv[i], a.gamma[c], p.inv, 0, nsat);
-    }
-    if (blockIdx.x == 0) count(a.counts, a.slot_norm, nsat);
-  } else {
-    for (int c = t; c < KC * 1024; c += 256) xs[c + (c >> 4) * 4] = a.x[c];
-  }
-  __syncthreads();
+  for (int i = 0; i < NX; ++i) xv[i] = a.x[t + 256 * i];
+  __builtin_amdgcn_sched_barrier(0);
 
   constexpr int ND = EPI == FX_EPI_SILU ? 2 * R : R;
   const int row0 = (blockIdx.x * 4 + wid) * R;
@@ -231,6 +227,34 @@ __global__ __launch_bounds__(256) void fx_gemv_kernel(const FxGemv a) {
       sv[r][j] = sr[16 * j];
     }
   }
+  __builtin_amdgcn_sched_barrier(0);
+
+  // 2. prologue: the activations (normalised for NORM) into LDS
+  if constexpr (PRO == FX_PRO_NORM) {
+    static_assert(KC == 1, "the norm prologue covers the 1024-wide hidden state");
+    long long ss = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) ss += (long long)xv[i] * xv[i];
+    ss = wave_sum_ll(ss);
+    if (lane == 0) red[wid] = ss;
+    block_sync_lds();
+    const NormParams p = norm_params(red[0] + red[1] + red[2] + red[3], 0);
+    int nsat = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int c = t + 256 * i;
+      xs[c + (c >> 4) * 4] = norm_apply(xv[i], a.gamma[c], p.inv, 0, nsat);
+    }
+    if (blockIdx.x == 0) count(a.counts, a.slot_norm, nsat);
+  } else {
+#pragma unroll
+    for (int i = 0; i < NX; ++i) {
+      const int c = t + 256 * i;
+      xs[c + (c >> 4) * 4] = xv[i];
+    }
+  }
+  block_sync_lds();
+
   long long acc[ND];
 #pragma unroll
   for (int r = 0; r < ND; ++r) acc[r] = 0;
@@ -315,6 +339,18 @@ __global__ __launch_bounds__(256) void fx_gemv_kernel(const FxGemv a) {
 }
 
 // ---------------------------------------------------------------- attention
+// Two launches per layer:
+//   fx_attn_scores, (chunk, head) blocks of 256 threads, CH positions per chunk: q/k norm +
+//     RoPE (the chunk holding the new position of the first q head of a kv group appends the
+//     K/V row), the chunk's scaled scores and their maximum to the workspace.
+//   fx_attn_value, (32 dims, head) blocks of 256 threads: the head's integer softmax over
+//     all T positions (global maximum of the chunk maxima, LUT exp values, their sum,
+//     floor((e << 16) / sum)) into LDS, then sum_p prob_p * v_p for the block's 32 dims,
+//     exact in int64, and sat24(sum >> 16).  Every block of a head recomputes the same
+//     softmax (T scores and at most 16 maxima), which costs less than handing it over.
+// The kernel boundary orders the workspace traffic; no counters or device-scope atomics.
+constexpr int kFxMaxChunks = 16;
+
 struct FxAttn {
   const int32_t* qkv;       // FULL: q|k|v projections of this token
   const int32_t* q_in;      // !FULL: q after norm and RoPE [qh, 128]
@@ -326,10 +362,12 @@ struct FxAttn {
   int cache_length;         // !FULL
   int32_t* kc;              // K plane of the layer [kvh][max_ctx][128]
   int32_t* vc;              // V plane
-  int max_ctx, qh, kvh;
+  int max_ctx, qh, kvh, ch;
   int score_scale;
   const int32_t* exp_lut;
   int32_t* out;             // [qh, 128]
+  int64_t* sc;              // workspace: scaled scores [qh][max_ctx]
+  int64_t* cmax;            // workspace: chunk maxima [qh][kFxMaxChunks]
   int64_t* raw;             // debug outputs [qh, T] (may be null)
   int64_t* scaled;
   int32_t* lut_index;
@@ -338,162 +376,297 @@ struct FxAttn {
   int32_t* status;
 };
 
+// Position of this step; false (nothing to do) for an out-of-range device position.
 template <bool FULL>
-__global__ __launch_bounds__(1024) void fx_attn_kernel(const FxAttn a) {
-  __shared__ long long sc[kFxMaxCtx];  // scaled score, then exp value, then probability
-  __shared__ long long vred[8][128];
-  __shared__ long long wred[16];
-  __shared__ int lut[kFxExpLut];
-  __shared__ int qn[128], kn[128], qr[128], kr[128], vv[128];
-  const int t = threadIdx.x, lane = t & 63, wid = t >> 6;
-  const int h = blockIdx.x, rep = a.qh / a.kvh, g = h / rep;
-  int pos;
+__device__ __forceinline__ bool fx_attn_pos(const FxAttn& a, int& pos) {
   if constexpr (FULL) {
     pos = *a.position;
     if (pos < 0 || pos >= a.max_ctx) {  // uniform over the grid: nothing is written
-      if (t == 0 && h == 0 && a.status) atomicOr(a.status, Q4D_STATUS_BAD_POSITION);
-      return;
+      if (threadIdx.x == 0 && blockIdx.x == 0 && blockIdx.y == 0 && a.status)
+        atomicOr(a.status, Q4D_STATUS_BAD_POSITION);
+      return false;
     }
   } else {
     pos = a.cache_length - 1;
   }
-  const int T = pos + 1;
-  for (int i = t; i < kFxExpLut; i += 1024) lut[i] = a.exp_lut[i];
+  return true;
+}
+
+template <bool FULL>
+__global__ __launch_bounds__(256) void fx_attn_scores_kernel(const FxAttn a) {
+  __shared__ int qn[128], kn[128], qr[128], kr[128];
+  __shared__ long long wred[4];
+  const int t = threadIdx.x, lane = t & 63, wid = t >> 6;
+  const int c = blockIdx.x, h = blockIdx.y, rep = a.qh / a.kvh, g = h / rep;
+  int pos;
+  if (!fx_attn_pos<FULL>(a, pos)) return;
+  const int T = pos + 1, p_begin = c * a.ch;
+  if (p_begin >= T) return;  // chunk past the context
+  const int p_end = min(T, p_begin + a.ch);
+
+  // loads in the order they are consumed (completion is counted in issue order): this
+  // token's q / k / v rows and RoPE row, then the chunk's first two passes of K rows
+  const int qd = a.qh * 128, kd = a.kvh * 128, d = t & 127;
+  const bool app = FULL && c == pos / a.ch && h % rep == 0;  // one block per kv head appends
+  int v = 0, vrow = 0, cs = 0, sn = 0;
+  if constexpr (FULL) {
+    cs = a.cos[(size_t)pos * 128 + d];
+    sn = a.sin[(size_t)pos * 128 + d];
+    v = t < 128 ? a.qkv[h * 128 + d] : a.qkv[qd + g * 128 + d];
+    vrow = app && t < 128 ? a.qkv[qd + kd + g * 128 + d] : 0;
+  } else {
+    v = t < 128 ? a.q_in[h * 128 + t] : 0;
+  }
+  const int sub = lane & 7, grp = (wid << 3) | (lane >> 3);
+  const int32_t* kbase = a.kc + (size_t)g * a.max_ctx * 128 + 16 * sub;
+  i32x4 k4[2][4];
+  auto load_k = [&](int pp) {
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int p = pp + 32 * u + grp;
+      const int pc = p < p_end ? p : p_end - 1;  // clamped: in bounds, result unused
+      const i32x4* kp = reinterpret_cast<const i32x4*>(kbase + (size_t)pc * 128);
+#pragma unroll
+      for (int v4 = 0; v4 < 4; ++v4) k4[u][v4] = kp[v4];
+    }
+  };
+  __builtin_amdgcn_sched_barrier(0);
+  load_k(p_begin);
+  __builtin_amdgcn_sched_barrier(0);
 
   if constexpr (FULL) {
     // q/k RMSNorm per head (22_...:127-182), RoPE (22_...:185-212), K/V append
-    const int qd = a.qh * 128, kd = a.kvh * 128;
-    int v = 0;
-    if (t < 128) v = a.qkv[h * 128 + t];
-    else if (t < 256) v = a.qkv[qd + g * 128 + (t - 128)];
-    else if (t < 384) vv[t - 256] = a.qkv[qd + kd + g * 128 + (t - 256)];
-    long long ss = t < 256 ? (long long)v * v : 0;
-    ss = wave_sum_ll(ss);
+    long long ss = wave_sum_ll((long long)v * v);
     if (lane == 0) wred[wid] = ss;
-    __syncthreads();
+    block_sync_lds();
+    const NormParams p = norm_params(t < 128 ? wred[0] + wred[1] : wred[2] + wred[3], 1);
     int nsat = 0;
-    if (t < 256) {
-      const NormParams p = norm_params(t < 128 ? wred[0] + wred[1] : wred[2] + wred[3], 1);
-      const int d = t & 127;
-      if (t < 128) qn[d] = norm_apply(v, a.q_gamma[d], p.inv, 1, nsat);
-      else kn[d] = norm_apply(v, a.k_gamma[d], p.inv, 1, nsat);
-    }
-    if (t < 128 || h % rep == 0) count(a.counts, Q4D_FX_SAT_QK_NORM, nsat);  // each k head once per group
-    __syncthreads();
+    const int y = norm_apply(v, (t < 128 ? a.q_gamma : a.k_gamma)[d], p.inv, 1, nsat);
+    if (t < 128) qn[d] = y;
+    else kn[d] = y;
+    const bool counter_block = c == 0 && (t < 128 || h % rep == 0);  // each head counted once
+    if (counter_block) count(a.counts, Q4D_FX_SAT_QK_NORM, nsat);
+    block_sync_lds();
     nsat = 0;
-    if (t < 256) {
-      const int d = t & 127;
-      const int* src = t < 128 ? qn : kn;
-      const int x = src[d];
-      const int rot = d < 64 ? -src[d + 64] : src[d - 64];
-      const long long s = (long long)x * a.cos[(size_t)pos * 128 + d] + (long long)rot * a.sin[(size_t)pos * 128 + d];
-      const int y = sat24(s >> 15, nsat);
-      if (t < 128) {
-        qr[d] = y;
-      } else {
-        kr[d] = y;
-        if (h % rep == 0) a.kc[((size_t)g * a.max_ctx + pos) * 128 + d] = y;
-      }
-    } else if (t < 384 && h % rep == 0) {
-      a.vc[((size_t)g * a.max_ctx + pos) * 128 + (t - 256)] = vv[t - 256];
+    const int* src = t < 128 ? qn : kn;
+    const int rot = d < 64 ? -src[d + 64] : src[d - 64];
+    const int r = sat24(((long long)src[d] * cs + (long long)rot * sn) >> 15, nsat);
+    if (t < 128) {
+      qr[d] = r;
+      if (app) a.vc[((size_t)g * a.max_ctx + pos) * 128 + d] = vrow;
+    } else {
+      kr[d] = r;
+      if (app) a.kc[((size_t)g * a.max_ctx + pos) * 128 + d] = r;
     }
-    if (t < 128 || h % rep == 0) count(a.counts, Q4D_FX_SAT_ROPE, nsat);
+    if (counter_block) count(a.counts, Q4D_FX_SAT_ROPE, nsat);
   } else {
-    if (t < 128) qr[t] = a.q_in[h * 128 + t];
+    if (t < 128) qr[t] = v;
   }
-  __syncthreads();
+  block_sync_lds();
 
-  // scores: 8 lanes per position (16 dims each), 128 positions per pass
-  const int sub = lane & 7, grp = (wid << 3) | (lane >> 3);
+  // scores of this chunk: 8 lanes per position (16 dims each), 32 positions per pass
   int qreg[16];
 #pragma unroll
   for (int i = 0; i < 16; ++i) qreg[i] = qr[16 * sub + i];
-  const int32_t* kbase = a.kc + (size_t)g * a.max_ctx * 128;
-  for (int p0 = 0; p0 < T; p0 += 128) {
-    const int p = p0 + grp;
-    long long dot = 0;
-    if (p < T) {
-      if (FULL && p == pos) {
+  long long cm = LLONG_MIN;
+  auto score_round = [&](int pp) {
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int p = pp + 32 * u + grp;
+      long long dot = 0;
+      if (FULL && p == pos) {  // this token's K from LDS: the cache row may not be written yet
 #pragma unroll
         for (int i = 0; i < 16; ++i) dot += (long long)qreg[i] * kr[16 * sub + i];
       } else {
-        const i32x4* kp = reinterpret_cast<const i32x4*>(kbase + (size_t)p * 128 + 16 * sub);
 #pragma unroll
         for (int v4 = 0; v4 < 4; ++v4) {
-          const i32x4 k4 = kp[v4];
-          dot += (long long)qreg[4 * v4 + 0] * k4.x + (long long)qreg[4 * v4 + 1] * k4.y +
-                 (long long)qreg[4 * v4 + 2] * k4.z + (long long)qreg[4 * v4 + 3] * k4.w;
+          const i32x4 kk = k4[u][v4];
+          dot += (long long)qreg[4 * v4 + 0] * kk.x + (long long)qreg[4 * v4 + 1] * kk.y +
+                 (long long)qreg[4 * v4 + 2] * kk.z + (long long)qreg[4 * v4 + 3] * kk.w;
         }
       }
+      dot += shfl_xor_ll(dot, 1);
+      dot += shfl_xor_ll(dot, 2);
+      dot += shfl_xor_ll(dot, 4);
+      if (p < p_end && sub == 0) {
+        const long long hi = dot >> 31, lo = dot & 0x7FFFFFFFLL;
+        const long long sv = hi * (long long)a.score_scale + ((lo * (long long)a.score_scale) >> 31);
+        a.sc[(size_t)h * a.max_ctx + p] = sv;
+        cm = sv > cm ? sv : cm;
+        if (a.raw) a.raw[(size_t)h * T + p] = dot;
+        if (a.scaled) a.scaled[(size_t)h * T + p] = sv;
+      }
     }
-    dot += shfl_xor_ll(dot, 1);
-    dot += shfl_xor_ll(dot, 2);
-    dot += shfl_xor_ll(dot, 4);
-    if (p < T && sub == 0) {
-      const long long hi = dot >> 31, lo = dot & 0x7FFFFFFFLL;
-      const long long s = hi * (long long)a.score_scale + ((lo * (long long)a.score_scale) >> 31);
-      sc[p] = s;
-      if (a.raw) a.raw[(size_t)h * T + p] = dot;
-      if (a.scaled) a.scaled[(size_t)h * T + p] = s;
-    }
+  };
+  score_round(p_begin);
+  for (int pp = p_begin + 64; pp < p_end; pp += 64) {
+    load_k(pp);
+    score_round(pp);
   }
-  __syncthreads();
-
-  // softmax (46_...:96-121): max, LUT index, sum, probability
-  long long m = LLONG_MIN;
-  for (int p = t; p < T; p += 1024) m = sc[p] > m ? sc[p] : m;
-  m = wave_max_ll(m);
-  if (lane == 0) wred[wid] = m;
-  __syncthreads();
-  m = wred[0];
+  cm = wave_max_ll(cm);
+  if (lane == 0) wred[wid] = cm;
+  block_sync_lds();
+  if (t == 0) {
+    long long m = wred[0];
 #pragma unroll
-  for (int k = 1; k < 16; ++k) m = wred[k] > m ? wred[k] : m;
-  __syncthreads();
+    for (int k = 1; k < 4; ++k) m = wred[k] > m ? wred[k] : m;
+    a.cmax[h * kFxMaxChunks + c] = m;
+  }
+}
+
+template <bool FULL>
+__global__ __launch_bounds__(256) void fx_attn_value_kernel(const FxAttn a) {
+  __shared__ int prs[kFxMaxCtx];  // probabilities of the head
+  __shared__ int lut[kFxExpLut];
+  __shared__ long long wred[4];
+  __shared__ long long vred[4][32];
+  const int t = threadIdx.x, lane = t & 63, wid = t >> 6;
+  const int db = blockIdx.x, h = blockIdx.y, rep = a.qh / a.kvh, g = h / rep;
+  int pos;
+  if (!fx_attn_pos<FULL>(a, pos)) return;
+  const int T = pos + 1, nct = (T + a.ch - 1) / a.ch;
+
+  // loads in the order they are consumed: chunk maxima, scores, LUT, then the first round
+  // of V rows (thread = 4 dims x position residue mod 32)
+  long long cmv[kFxMaxChunks];
+#pragma unroll
+  for (int i = 0; i < kFxMaxChunks; ++i) cmv[i] = a.cmax[h * kFxMaxChunks + (i < nct ? i : nct - 1)];
+  constexpr int NP = kFxMaxCtx / 256;  // score positions per thread
+  long long sv[NP];
+#pragma unroll
+  for (int k = 0; k < NP; ++k) {  // clamped: slots past the context re-read the last score
+    const int p = t + 256 * k;
+    sv[k] = a.sc[(size_t)h * a.max_ctx + (p < T ? p : T - 1)];
+  }
+  for (int i = t; i < kFxExpLut; i += 256) lut[i] = a.exp_lut[i];
+  const int dq = t & 7, j = t >> 3;
+  const int32_t* vbase = a.vc + (size_t)g * a.max_ctx * 128 + 32 * db + 4 * dq;
+  i32x4 v4[8];
+  auto load_v = [&](int p0) {
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int p = p0 + 32 * u;
+      v4[u] = *reinterpret_cast<const i32x4*>(vbase + (size_t)(p < T ? p : T - 1) * 128);
+    }
+  };
+  __builtin_amdgcn_sched_barrier(0);
+  load_v(j);
+  __builtin_amdgcn_sched_barrier(0);
+
+  // softmax (46_...:96-121)
+  long long m = cmv[0];
+#pragma unroll
+  for (int i = 1; i < kFxMaxChunks; ++i) m = cmv[i] > m ? cmv[i] : m;
+  block_sync_lds();  // LUT in LDS
+  int e[NP];
   long long se = 0;
-  for (int p = t; p < T; p += 1024) {
-    const long long neg = m - sc[p];
+  const bool dbg = db == 0;
+#pragma unroll
+  for (int k = 0; k < NP; ++k) {
+    e[k] = 0;
+    if (256 * k >= T) continue;  // block-uniform: slots past the context are skipped whole
+    const int p = t + 256 * k;
+    const long long neg = m - sv[k];
     int idx = 0;
     if (neg > 0) {
       const long long r = (neg + (1LL << 19)) >> 20;
       idx = r > kFxExpLut - 1 ? kFxExpLut - 1 : (int)r;
     }
-    const int e = lut[idx];
-    sc[p] = e;
-    se += e;
-    if (a.lut_index) a.lut_index[(size_t)h * T + p] = idx;
+    e[k] = p < T ? lut[idx] : 0;
+    se += e[k];
+    if (dbg && a.lut_index && p < T) a.lut_index[(size_t)h * T + p] = idx;
   }
   se = wave_sum_ll(se);
   if (lane == 0) wred[wid] = se;
-  __syncthreads();
-  se = 0;
+  block_sync_lds();
+  se = wred[0] + wred[1] + wred[2] + wred[3];
 #pragma unroll
-  for (int k = 0; k < 16; ++k) se += wred[k];
-  for (int p = t; p < T; p += 1024) {
-    const long long pr = (long long)udiv_small((unsigned long long)sc[p] << 16, (unsigned long long)se);
-    sc[p] = pr;
-    if (a.prob) a.prob[(size_t)h * T + p] = (int32_t)pr;
+  for (int k = 0; k < NP; ++k) {
+    if (256 * k >= T) break;
+    const int p = t + 256 * k;
+    if (p < T) {
+      const int pv = (int)udiv_small((unsigned long long)e[k] << 16, (unsigned long long)se);
+      prs[p] = pv;
+      if (dbg && a.prob) a.prob[(size_t)h * T + p] = pv;
+    }
   }
-  __syncthreads();
+  block_sync_lds();
 
-  // value sums (46_...:124-137): thread = (dim, position residue mod 8)
-  const int d = t & 127, j = t >> 7;
-  const int32_t* vbase = a.vc + (size_t)g * a.max_ctx * 128 + d;
-  long long acc = 0;
-#pragma unroll 4
-  for (int p = j; p < T; p += 8) {
-    const int v = (FULL && p == pos) ? vv[d] : vbase[(size_t)p * 128];
-    acc += sc[p] * (long long)v;
-  }
-  vred[j][d] = acc;
-  __syncthreads();
-  if (t < 128) {
-    long long s = 0;
+  // value sums (46_...:124-137) for dims 32 db + 4 dq .. + 3
+  long long acc0 = 0, acc1 = 0, acc2 = 0, acc3 = 0;
+  auto value_round = [&](int p0) {
 #pragma unroll
-    for (int k = 0; k < 8; ++k) s += vred[k][t];
+    for (int u = 0; u < 8; ++u) {
+      const int p = p0 + 32 * u;
+      const long long pr = p < T ? prs[p] : 0;
+      acc0 += pr * v4[u].x;
+      acc1 += pr * v4[u].y;
+      acc2 += pr * v4[u].z;
+      acc3 += pr * v4[u].w;
+    }
+  };
+  value_round(j);
+  for (int p0 = j + 256; p0 < T; p0 += 256) {
+    load_v(p0);
+    value_round(p0);
+  }
+  // the 8 residues of a wave sit in lanes dq + 8 r: reduce over r, then over the 4 waves
+#pragma unroll
+  for (int m2 = 8; m2 <= 32; m2 <<= 1) {
+    acc0 += shfl_xor_ll(acc0, m2);
+    acc1 += shfl_xor_ll(acc1, m2);
+    acc2 += shfl_xor_ll(acc2, m2);
+    acc3 += shfl_xor_ll(acc3, m2);
+  }
+  if (lane < 8) {
+    vred[wid][4 * dq + 0] = acc0;
+    vred[wid][4 * dq + 1] = acc1;
+    vred[wid][4 * dq + 2] = acc2;
+    vred[wid][4 * dq + 3] = acc3;
+  }
+  block_sync_lds();
+  if (t < 64) {  // one full wave: the saturation count below is wave-uniform
     int nsat = 0;
-    a.out[h * 128 + t] = sat24(s >> 16, nsat);
+    if (t < 32) {
+      const long long sum = vred[0][t] + vred[1][t] + vred[2][t] + vred[3][t];
+      a.out[h * 128 + 32 * db + t] = sat24(sum >> 16, nsat);
+    }
     count(a.counts, Q4D_FX_SAT_ATTENTION, nsat);
   }
+}
+
+struct FxAttnLayout {
+  size_t sc, cmax, total;
+  int ch, nch;
+};
+
+// Chunk length: 64 positions, longer (by 32) until at most kFxMaxChunks chunks cover max_ctx.
+FxAttnLayout fx_attn_layout(int qh, int max_ctx) {
+  FxAttnLayout L{};
+  L.ch = 64;
+  while ((max_ctx + L.ch - 1) / L.ch > kFxMaxChunks) L.ch += 32;
+  L.nch = (max_ctx + L.ch - 1) / L.ch;
+  const size_t A = 256;
+  size_t o = 0;
+  L.sc = o;   o = align_up(o + (size_t)qh * max_ctx * 8, A);
+  L.cmax = o; o = align_up(o + (size_t)qh * kFxMaxChunks * 8, A);
+  L.total = o;
+  return L;
+}
+
+void fx_attn_bind(FxAttn& a, void* ws, const FxAttnLayout& L) {
+  a.sc = ws_ptr<int64_t>(ws, L.sc);
+  a.cmax = ws_ptr<int64_t>(ws, L.cmax);
+  a.ch = L.ch;
+}
+
+template <bool FULL>
+int fx_launch_attention(const FxAttn& a, int nch, hipStream_t st) {
+  hipLaunchKernelGGL(fx_attn_scores_kernel<FULL>, dim3(nch, a.qh), dim3(256), 0, st, a);
+  int rc = check_launch();
+  if (rc) return rc;
+  hipLaunchKernelGGL(fx_attn_value_kernel<FULL>, dim3(4, a.qh), dim3(256), 0, st, a);
+  return check_launch();
 }
 
 // ---------------------------------------------------------------- small stage kernels
@@ -611,13 +784,22 @@ __global__ __launch_bounds__(1024) void fx_argmax_kernel(const int64_t* ps, cons
   const int t = threadIdx.x, lane = t & 63, wid = t >> 6;
   long long bs = LLONG_MIN;
   int bi = INT_MAX;
-  for (int i = t; i < n; i += 1024) {
-    const long long v = ps[i];
-    const int ix = pi[i];
-    if (ix != INT_MAX && (v > bs || (v == bs && ix < bi) || bi == INT_MAX)) {
-      bs = v;
-      bi = ix;
+  for (int base = 0; base < n; base += 8 * 1024) {  // eight loads in flight per thread
+    long long v[8];
+    int ix[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const int i = base + t + 1024 * k;
+      const int ic = i < n ? i : n - 1;
+      v[k] = ps[ic];
+      ix[k] = i < n ? pi[ic] : INT_MAX;
     }
+#pragma unroll
+    for (int k = 0; k < 8; ++k)
+      if (ix[k] != INT_MAX && (v[k] > bs || (v[k] == bs && ix[k] < bi) || bi == INT_MAX)) {
+        bs = v[k];
+        bi = ix[k];
+      }
   }
 #pragma unroll
   for (int m = 32; m >= 1; m >>= 1) {
@@ -646,8 +828,9 @@ __global__ __launch_bounds__(1024) void fx_argmax_kernel(const int64_t* ps, cons
 
 // ---------------------------------------------------------------- host side
 struct FxLayout {
-  size_t counts, exp_lut, sig_lut, hidden, qkv, attn, post, mlp, part_score, part_idx, total;
+  size_t counts, exp_lut, sig_lut, hidden, qkv, attn, post, mlp, part_score, part_idx, attn_ws, total;
   int nparts;
+  FxAttnLayout al;  // attention scratch, at attn_ws
 };
 
 FxLayout fx_layout(const q4d_model_t* m) {
@@ -656,7 +839,7 @@ FxLayout fx_layout(const q4d_model_t* m) {
   const int qd = m->num_q_heads * m->head_dim, kd = m->num_kv_heads * m->head_dim;
   L.nparts = (m->vocab_size + kFxLmRowsPerBlock - 1) / kFxLmRowsPerBlock;
   size_t o = 0;
-  L.counts = o;     o = align_up(o + 64 * 4, A);
+  L.counts = o;     o = align_up(o + kFxStripes * kFxStripeWords * 4, A);
   L.exp_lut = o;    o = align_up(o + kFxExpLut * 4, A);
   L.sig_lut = o;    o = align_up(o + kFxSigLut * 4, A);
   L.hidden = o;     o = align_up(o + (size_t)m->hidden_size * 4, A);
@@ -666,6 +849,8 @@ FxLayout fx_layout(const q4d_model_t* m) {
   L.mlp = o;        o = align_up(o + (size_t)m->intermediate_size * 4, A);
   L.part_score = o; o = align_up(o + (size_t)L.nparts * 8, A);
   L.part_idx = o;   o = align_up(o + (size_t)L.nparts * 4, A);
+  L.al = fx_attn_layout(m->num_q_heads, m->max_ctx);
+  L.attn_ws = o;    o = align_up(o + L.al.total, A);
   L.total = o;
   return L;
 }
@@ -734,7 +919,7 @@ int fx_launch_gemv_t(const FxGemv& g, hipStream_t st) {
 // Row sums of one GEMV per output row (R rows per wave); K = 1024 KC.
 template <int PRO, int EPI>
 int fx_launch_gemv(const FxGemv& g, hipStream_t st) {
-  constexpr int R = EPI == FX_EPI_LOGITS ? kFxRowsLm : (EPI == FX_EPI_SILU ? 1 : 2);
+  constexpr int R = EPI == FX_EPI_LOGITS ? kFxRowsLm : (EPI == FX_EPI_Q12 ? 2 : 1);
   switch (g.K) {
     case 1024: return fx_launch_gemv_t<1, R, PRO, EPI>(g, st);
     case 2048:
@@ -784,8 +969,8 @@ int fx_run_layer(const q4d_fixed_model_t* fm, int l, const int32_t* hin, int32_t
   a.score_scale = fm->score_scale_q0_31;
   a.exp_lut = ws_ptr<int32_t>(ws, W.exp_lut);
   a.out = attn; a.counts = counts; a.status = counts + Q4D_FX_STATUS;
-  hipLaunchKernelGGL(fx_attn_kernel<true>, dim3(m->num_q_heads), dim3(1024), 0, st, a);
-  if ((rc = check_launch())) return rc;
+  fx_attn_bind(a, ws_ptr<char>(ws, W.attn_ws), W.al);
+  if ((rc = fx_launch_attention<true>(a, W.al.nch, st))) return rc;
 
   g = fx_gemv_base();  // 3. o_proj + residual
   g.w0 = L.o_proj.w; g.s0 = L.o_proj.s; g.e0 = g.e1 = g.rows = 1024; g.K = qd;
@@ -852,10 +1037,19 @@ int q4d_fixed_workspace_init(void* ws, size_t ws_bytes, const q4d_fixed_model_t*
 int q4d_fixed_read_counts(const void* ws, size_t ws_bytes, int32_t* counts, int32_t n, void* stream) {
   if (!ws || !counts) return Q4D_ERR_NULL;
   if (n <= 0 || n > Q4D_FX_COUNTS) return Q4D_ERR_SHAPE;
-  if (ws_bytes < (size_t)n * 4) return Q4D_ERR_CAPACITY;
+  static_assert(Q4D_FX_COUNTS <= kFxStripeWords, "counter stripe too small");
+  const size_t bytes = (size_t)kFxStripes * kFxStripeWords * 4;
+  if (ws_bytes < bytes) return Q4D_ERR_CAPACITY;
+  int32_t stripes[kFxStripes * kFxStripeWords];
   hipStream_t st = fx_stream(stream);
-  if (hipMemcpyAsync(counts, ws, (size_t)n * 4, hipMemcpyDeviceToHost, st) != hipSuccess) return Q4D_ERR_LAUNCH;
-  return hipStreamSynchronize(st) == hipSuccess ? Q4D_OK : Q4D_ERR_LAUNCH;
+  if (hipMemcpyAsync(stripes, ws, bytes, hipMemcpyDeviceToHost, st) != hipSuccess) return Q4D_ERR_LAUNCH;
+  if (hipStreamSynchronize(st) != hipSuccess) return Q4D_ERR_LAUNCH;
+  for (int i = 0; i < n; ++i) {
+    int64_t v = 0;
+    for (int k = 0; k < kFxStripes; ++k) v += stripes[k * kFxStripeWords + i];
+    counts[i] = i == Q4D_FX_STATUS ? stripes[i] : (int32_t)(v > INT32_MAX ? INT32_MAX : v);
+  }
+  return Q4D_OK;
 }
 
 int q4d_fixed_rms_norm(const int32_t* x, const int16_t* gamma, int32_t rows, int32_t dim, int32_t kind, int32_t* y,
@@ -880,16 +1074,26 @@ int q4d_fixed_qk_norm_rope(const int32_t* q, const int32_t* k, int32_t q_heads, 
   return check_launch();
 }
 
+size_t q4d_fixed_attention_workspace_bytes(int32_t q_heads, int32_t max_ctx) {
+  if (q_heads <= 0 || q_heads > 64 || max_ctx <= 0 || max_ctx > kFxMaxCtx) return 0;
+  return fx_attn_layout(q_heads, max_ctx).total;
+}
+
 int q4d_fixed_attention(const q4d_fixed_kv_t* kv, int32_t layer, int32_t q_heads, int32_t cache_length,
                         const int32_t* q_rope, int32_t score_scale_q0_31, const int32_t* exp_lut, int32_t* out,
-                        int64_t* raw, int64_t* scaled, int32_t* lut_index, int32_t* prob, void* stream) {
-  if (!kv || !kv->data || !q_rope || !exp_lut || !out) return Q4D_ERR_NULL;
+                        int64_t* raw, int64_t* scaled, int32_t* lut_index, int32_t* prob, void* ws,
+                        size_t ws_bytes, void* stream) {
+  if (!kv || !kv->data || !q_rope || !exp_lut || !out || !ws) return Q4D_ERR_NULL;
   if (kv->head_dim != 128 || kv->num_kv_heads <= 0 || kv->max_ctx <= 0 || kv->max_ctx > kFxMaxCtx) return Q4D_ERR_SHAPE;
   if (layer < 0 || layer >= kv->num_layers) return Q4D_ERR_BAD_LAYER;
   if (q_heads <= 0 || q_heads % kv->num_kv_heads) return Q4D_ERR_SHAPE;
   if (cache_length <= 0 || cache_length > kv->max_ctx) return Q4D_ERR_CONTEXT;
   if (score_scale_q0_31 <= 0) return Q4D_ERR_SHAPE;
-  if (!aligned(kv->data, 16) || (raw && !aligned(raw, 8)) || (scaled && !aligned(scaled, 8))) return Q4D_ERR_BAD_ADDR;
+  if (!aligned(kv->data, 16) || (raw && !aligned(raw, 8)) || (scaled && !aligned(scaled, 8)) || !aligned(ws, 256))
+    return Q4D_ERR_BAD_ADDR;
+  const FxAttnLayout AL = fx_attn_layout(q_heads, kv->max_ctx);
+  if (q_heads > 64) return Q4D_ERR_SHAPE;
+  if (ws_bytes < AL.total) return Q4D_ERR_CAPACITY;
   FxAttn a;
   memset(&a, 0, sizeof(a));
   a.q_in = q_rope;
@@ -905,8 +1109,8 @@ int q4d_fixed_attention(const q4d_fixed_kv_t* kv, int32_t layer, int32_t q_heads
   a.scaled = scaled;
   a.lut_index = lut_index;
   a.prob = prob;
-  hipLaunchKernelGGL(fx_attn_kernel<false>, dim3(q_heads), dim3(1024), 0, fx_stream(stream), a);
-  return check_launch();
+  fx_attn_bind(a, ws, AL);
+  return fx_launch_attention<false>(a, AL.nch, fx_stream(stream));
 }
 
 int q4d_fixed_kv_append(const q4d_fixed_kv_t* kv, int32_t layer, const int32_t* positions, const int32_t* k,

@@ -150,9 +150,11 @@ def attention_score_value(q_current, k_cache, v_cache, score_scale: int, exp_lut
     idx = torch.empty(qh, t, dtype=torch.int32, device=q.device)
     prob = torch.empty_like(idx)
     desc = kv.descriptor()
+    nbytes = int(lib.q4d_fixed_attention_workspace_bytes(qh, t))
+    ws = torch.zeros(nbytes, dtype=torch.uint8, device=q.device)
     check(lib.q4d_fixed_attention(ctypes.byref(desc), 0, qh, t, q.data_ptr(), int(score_scale), lut.data_ptr(),
                                   out.data_ptr(), raw.data_ptr(), scaled.data_ptr(), idx.data_ptr(), prob.data_ptr(),
-                                  current_stream()), "q4d_fixed_attention")
+                                  ws.data_ptr(), nbytes, current_stream()), "q4d_fixed_attention")
     return {"raw": raw, "scaled": scaled, "probs": prob, "lut_indices": idx, "output": out.view(qh, d)}
 
 

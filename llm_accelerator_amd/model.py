@@ -211,6 +211,19 @@ class Q4ForCausalLM:
                 "total": per_layer * len(self.model.layers) + self.lm_head.weight.nbytes}
 
 
+def with_context(model: Q4ForCausalLM, max_ctx: int) -> Q4ForCausalLM:
+    """The same device weights under another context capacity (its own RoPE tables
+    and descriptor); the layers keep pointing at ``model`` for the fused layer call."""
+    bb = model.model
+    view = Q4ForCausalLM.__new__(Q4ForCausalLM)
+    view.config = model.config
+    view.model = Q4Backbone(bb.layers, bb.embed_tokens, bb.norm, RotaryEmbedding(model.config, max_ctx, model.device))
+    view.lm_head = view.model.embed_tokens
+    view.max_ctx = max_ctx
+    view._desc = None
+    return view
+
+
 # ---------------------------------------------------------------- synthetic init
 def random_q4(rng: np.random.Generator, rows: int, cols: int) -> tuple[np.ndarray, np.ndarray]:
     packed = rng.integers(0, 256, size=(rows, cols // 2), dtype=np.uint8)
@@ -324,6 +337,17 @@ def algorithmic_bytes_layer(cfg: Qwen3Config, ctx: int) -> int:
     return weights + kv_read + kv_write + 2 * h * 2
 
 
+def fixed_layer_bytes(cfg: Qwen3Config, ctx: int) -> int:
+    """HBM bytes of one fixed-point decode layer at context ``ctx``: the same Q4
+    weights + scales, the int32 K/V of ``ctx`` positions read and one row of each
+    written, the int32 hidden state in and out, int16 gammas."""
+    h, i = cfg.hidden_size, cfg.intermediate_size
+    qd, kd = cfg.num_attention_heads * cfg.head_dim, cfg.num_key_value_heads * cfg.head_dim
+    elems = qd * h + 2 * kd * h + h * qd + 2 * i * h + h * i
+    weights = elems // 2 + 2 * (elems // GROUP_SIZE)
+    return weights + 2 * kd * ctx * 4 + 2 * kd * 4 + 2 * h * 4 + 2 * (2 * h + 2 * cfg.head_dim)
+
+
 def stage_bytes_layer(cfg: Qwen3Config, ctx: int) -> dict:
     """Algorithmic bytes per launch of each decode-layer stage at context
     ``ctx``, in the dtypes the kernels read and write: Q4 codes + Q2.14
@@ -376,5 +400,5 @@ def ceil_div(a: int, b: int) -> int:
 
 __all__ = ["Qwen3Config", "Q4Tensor", "Q4ForCausalLM", "Q4DecoderLayer", "Q4Backbone", "RotaryEmbedding",
            "KVCache", "Workspace", "random_q4", "random_gamma", "random_host_weights", "build_model",
-           "algorithmic_bytes_layer", "stage_bytes_layer", "prefill_flops", "batched_step_bytes", "gemv_bytes",
+           "algorithmic_bytes_layer", "fixed_layer_bytes", "with_context", "stage_bytes_layer", "prefill_flops", "batched_step_bytes", "gemv_bytes",
            "current_stream", "ceil_div"]

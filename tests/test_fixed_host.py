@@ -75,7 +75,7 @@ def test_fixed_model_validation(lib):
     fm, keep = _fixed_model()
     need = lib.q4d_fixed_workspace_bytes(ctypes.byref(fm))
     # counters, LUTs, hidden, q|k|v, attention, post, SwiGLU, per-block LM-head results
-    assert need >= 256 + 1280 + 4352 + 4096 + 16384 + 8192 + 4096 + 12288 + 9496 * 12
+    assert need >= 16384 + 1280 + 4352 + 4096 + 16384 + 8192 + 4096 + 12288 + 4748 * 12
     kv = Q4dFixedKV(FAKE, 2, 8, 256, 128)
 
     def layer(model=fm, cache=kv, l=0, ws=FAKE, nbytes=need, hin=FAKE, pos=FAKE):
@@ -127,9 +127,15 @@ def test_stage_entry_validation(lib):
     assert lib.q4d_fixed_qk_norm_rope(FAKE, FAKE, 16, 8, FAKE, None, FAKE, FAKE, FAKE, FAKE, None, None, None) == -7
     assert lib.q4d_fixed_qk_norm_rope(FAKE, FAKE, 0, 8, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, None, None, None) == -11
 
-    def att(cache=kv, layer=0, qh=16, t=5, scale=189812531, lut=FAKE, raw=None):
+    need = lib.q4d_fixed_attention_workspace_bytes(16, 256)
+    assert need >= 16 * 256 * 8 + 16 * 16 * 8 and lib.q4d_fixed_attention_workspace_bytes(16, 8192) == 0
+
+    def att(cache=kv, layer=0, qh=16, t=5, scale=189812531, lut=FAKE, raw=None, ws=FAKE, nbytes=need):
         return lib.q4d_fixed_attention(ctypes.byref(cache), layer, qh, t, FAKE, scale, lut, FAKE, raw, None, None,
-                                       None, None)
+                                       None, ws, nbytes, None)
+    assert att(ws=None) == -7
+    assert att(ws=FAKE + 64) == -4
+    assert att(nbytes=need - 1) == -9
     assert att(t=257) == -10
     assert att(t=0) == -10
     assert att(layer=2) == -2
