@@ -411,6 +411,114 @@ int q4d_fixed_run_one_token(const q4d_fixed_model_t* model, const int32_t* token
                             const q4d_fixed_kv_t* kv, int32_t* next_token, int64_t* score, int64_t* logits,
                             int32_t* hidden_out, void* ws, size_t ws_bytes, void* stream);
 
+/* ---- decode session (host state machine) ------------------------------------
+ * Serial prompt prefill, greedy feedback, stop reasons and the context cap, one
+ * model invocation per q4d_session_step: the state machine and event stream of the
+ * board session loop qot_session (FPGA_Project/software/qmap_prompt_demo/qot_session.h,
+ * qot_session.c:101-276), with the context cap and vocabulary size as parameters
+ * (the board fixes QOT_MAX_CONTEXT = 256, QOT_VOCAB_SIZE = 151936) and the runner
+ * being one GPU decode step.  Host memory only; the runners synchronise their stream. */
+#define Q4D_SESSION_DEFAULT_EOS_TOKEN_ID 151643u    /* QOT_SESSION_DEFAULT_EOS_TOKEN_ID */
+#define Q4D_SESSION_DEFAULT_IM_END_TOKEN_ID 151645u /* QOT_SESSION_DEFAULT_IM_END_TOKEN_ID */
+enum { Q4D_SESSION_ERR_STATE = -100 };              /* QOT_SESSION_ERR_STATE */
+enum {
+  Q4D_SESSION_STATE_UNINITIALIZED = 0, Q4D_SESSION_STATE_IDLE, Q4D_SESSION_STATE_PREFILL,
+  Q4D_SESSION_STATE_DECODE, Q4D_SESSION_STATE_STOPPING, Q4D_SESSION_STATE_DONE, Q4D_SESSION_STATE_ERROR
+};
+enum {
+  Q4D_SESSION_STOP_NONE = 0, Q4D_SESSION_STOP_EOS, Q4D_SESSION_STOP_IM_END, Q4D_SESSION_STOP_MAX_NEW,
+  Q4D_SESSION_STOP_CONTEXT, Q4D_SESSION_STOP_HW_ERROR
+};
+enum {
+  Q4D_SESSION_EVENT_NONE = 0, Q4D_SESSION_EVENT_PREFILL, Q4D_SESSION_EVENT_TOKEN, Q4D_SESSION_EVENT_DONE,
+  Q4D_SESSION_EVENT_ERROR
+};
+
+/* Result of one model invocation (qot_result_t's status / token_id / score_q26). */
+typedef struct q4d_token_result {
+  uint32_t status;    /* device status word (0 = ok) */
+  uint32_t token_id;  /* argmax of the logits */
+  float score;        /* its logit (float path) */
+  int32_t reserved;
+  int64_t score_q26;  /* its Q26 score (fixed-point path) */
+} q4d_token_result_t;
+
+/* One full-model token invocation (qot_session_runner_fn without the board handles). */
+typedef int (*q4d_session_runner_fn)(void* runner_context, uint32_t input_token_id, uint32_t position,
+                                     q4d_token_result_t* result);
+
+typedef struct q4d_session_options {
+  uint32_t max_new_tokens;
+  uint32_t eos_token_id;
+  uint32_t im_end_token_id;
+  uint32_t stop_on_eos;
+  uint32_t stop_on_im_end;
+} q4d_session_options_t;
+
+typedef struct q4d_session_event {
+  int32_t kind;         /* Q4D_SESSION_EVENT_* */
+  int32_t stop_reason;  /* Q4D_SESSION_STOP_* */
+  uint32_t input_token_id;
+  uint32_t input_position;
+  uint32_t prompt_tokens_consumed;
+  uint32_t generated_index;
+  int32_t error_code;
+  q4d_token_result_t result;
+} q4d_session_event_t;
+
+typedef struct q4d_session {
+  uint32_t start_position, max_context, vocab_size;
+  q4d_session_runner_fn runner;
+  void* runner_context;
+  const uint32_t* prompt;  /* caller's, valid until DONE or ERROR */
+  uint32_t prompt_count, prompt_index, next_position, pending_token, generated_count;
+  q4d_session_options_t options;
+  q4d_token_result_t last_result;
+  int32_t last_error;
+  int32_t state;        /* Q4D_SESSION_STATE_* */
+  int32_t stop_reason;  /* Q4D_SESSION_STOP_* */
+} q4d_session_t;
+
+/* Runner contexts.  io: caller's device int32[8], 16-byte aligned (token, position, next
+ * token, -, score).  The float runner also reads the workspace status word. */
+typedef struct q4d_gpu_runner {
+  const q4d_model_t* model;
+  const q4d_kv_cache_t* kv;
+  void* ws;
+  size_t ws_bytes;
+  void* stream;
+  int32_t* io;
+} q4d_gpu_runner_t;
+typedef struct q4d_fixed_runner {
+  const q4d_fixed_model_t* model;
+  const q4d_fixed_kv_t* kv;
+  void* ws;
+  size_t ws_bytes;
+  void* stream;
+  int32_t* io;
+} q4d_fixed_runner_t;
+
+/* qot_session_default_options: max_new 1, stop on EOS 151643 and <|im_end|> 151645. */
+void q4d_session_default_options(q4d_session_options_t* options);
+/* qot_session_init (qot_session.c:101-123); Q4D_ERR_CONTEXT if start_position >= max_context. */
+int q4d_session_init(q4d_session_t* session, uint32_t start_position, uint32_t max_context, uint32_t vocab_size,
+                     q4d_session_runner_fn runner, void* runner_context);
+/* qot_session_begin (qot_session.c:125-172). */
+int q4d_session_begin(q4d_session_t* session, const uint32_t* prompt_token_ids, uint32_t prompt_token_count,
+                      const q4d_session_options_t* options);
+/* qot_session_step (qot_session.c:174-245): at most one runner call, one event. */
+int q4d_session_step(q4d_session_t* session, q4d_session_event_t* event);
+void q4d_session_reset(q4d_session_t* session);
+int q4d_session_is_terminal(const q4d_session_t* session);
+const char* q4d_session_state_name(int32_t state);
+const char* q4d_session_stop_reason_name(int32_t reason);
+/* Runners to pass to q4d_session_init with a q4d_gpu_runner_t / q4d_fixed_runner_t context:
+ * one q4d_run_one_token / q4d_fixed_run_one_token step (the board's qot_run_token). */
+int q4d_session_gpu_runner(void* runner_context, uint32_t input_token_id, uint32_t position,
+                           q4d_token_result_t* result);
+int q4d_session_fixed_runner(void* runner_context, uint32_t input_token_id, uint32_t position,
+                             q4d_token_result_t* result);
+
 #ifdef __cplusplus
 }
 #endif

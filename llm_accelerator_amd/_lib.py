@@ -76,6 +76,41 @@ class Q4dFixedKV(ctypes.Structure):
                 ("head_dim", c_int32)]
 
 
+class Q4dTokenResult(ctypes.Structure):
+    _fields_ = [("status", ctypes.c_uint32), ("token_id", ctypes.c_uint32), ("score", c_float),
+                ("reserved", c_int32), ("score_q26", ctypes.c_int64)]
+
+
+SESSION_RUNNER = ctypes.CFUNCTYPE(c_int32, c_void_p, ctypes.c_uint32, ctypes.c_uint32, POINTER(Q4dTokenResult))
+
+
+class Q4dSessionOptions(ctypes.Structure):
+    _fields_ = [("max_new_tokens", ctypes.c_uint32), ("eos_token_id", ctypes.c_uint32),
+                ("im_end_token_id", ctypes.c_uint32), ("stop_on_eos", ctypes.c_uint32),
+                ("stop_on_im_end", ctypes.c_uint32)]
+
+
+class Q4dSessionEvent(ctypes.Structure):
+    _fields_ = [("kind", c_int32), ("stop_reason", c_int32), ("input_token_id", ctypes.c_uint32),
+                ("input_position", ctypes.c_uint32), ("prompt_tokens_consumed", ctypes.c_uint32),
+                ("generated_index", ctypes.c_uint32), ("error_code", c_int32), ("result", Q4dTokenResult)]
+
+
+class Q4dSession(ctypes.Structure):
+    _fields_ = [("start_position", ctypes.c_uint32), ("max_context", ctypes.c_uint32),
+                ("vocab_size", ctypes.c_uint32), ("runner", c_void_p), ("runner_context", c_void_p),
+                ("prompt", c_void_p), ("prompt_count", ctypes.c_uint32), ("prompt_index", ctypes.c_uint32),
+                ("next_position", ctypes.c_uint32), ("pending_token", ctypes.c_uint32),
+                ("generated_count", ctypes.c_uint32), ("options", Q4dSessionOptions),
+                ("last_result", Q4dTokenResult), ("last_error", c_int32), ("state", c_int32),
+                ("stop_reason", c_int32)]
+
+
+class Q4dGpuRunner(ctypes.Structure):
+    _fields_ = [("model", c_void_p), ("kv", c_void_p), ("ws", c_void_p), ("ws_bytes", c_size_t),
+                ("stream", c_void_p), ("io", c_void_p)]
+
+
 # Fixed-point workspace counters (Q4D_FX_* in include/q4dec.h).
 FX_COUNT_NAMES = ["status", "input_norm", "qkv", "qk_norm", "rope", "attention", "o_proj", "post_residual",
                   "post_norm", "gate", "up", "silu", "mlp_hidden", "down", "layer_residual", "final_norm"]
@@ -132,6 +167,16 @@ SIGNATURES = {
     "q4d_fixed_embedding": ([POINTER(Q4dMatrix), _P, c_int32, _P, _P], c_int32),
     "q4d_fixed_decoder_layer": ([_FM, c_int32, _P, _P, _FKV, _P, _P, c_size_t, _P], c_int32),
     "q4d_fixed_run_one_token": ([_FM, _P, _P, _FKV, _P, _P, _P, _P, _P, c_size_t, _P], c_int32),
+    "q4d_session_default_options": ([POINTER(Q4dSessionOptions)], None),
+    "q4d_session_init": ([POINTER(Q4dSession), ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32, _P, _P], c_int32),
+    "q4d_session_begin": ([POINTER(Q4dSession), _P, ctypes.c_uint32, POINTER(Q4dSessionOptions)], c_int32),
+    "q4d_session_step": ([POINTER(Q4dSession), POINTER(Q4dSessionEvent)], c_int32),
+    "q4d_session_reset": ([POINTER(Q4dSession)], None),
+    "q4d_session_is_terminal": ([POINTER(Q4dSession)], c_int32),
+    "q4d_session_state_name": ([c_int32], ctypes.c_char_p),
+    "q4d_session_stop_reason_name": ([c_int32], ctypes.c_char_p),
+    "q4d_session_gpu_runner": ([_P, ctypes.c_uint32, ctypes.c_uint32, POINTER(Q4dTokenResult)], c_int32),
+    "q4d_session_fixed_runner": ([_P, ctypes.c_uint32, ctypes.c_uint32, POINTER(Q4dTokenResult)], c_int32),
 }
 
 _lib = None
