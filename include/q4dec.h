@@ -289,6 +289,15 @@ int q4d_prefill(const q4d_model_t* model, const int32_t* tokens, int32_t n_token
 int q4d_advance(int32_t* tokens, int32_t* positions, const int32_t* next_token, const float* score,
                 int32_t* hist_tokens, float* hist_scores, int32_t* hist_count, int32_t hist_capacity,
                 void* stream);
+/* q4d_advance with the decode session's stop rules on the device (qot_session.c:41-60, in
+ * this order after each generated token: end-of-text, end-of-turn, new-token budget, context
+ * cap).  stop_state: device int32[8] = {done, stop reason (Q4D_SESSION_STOP_*), generated
+ * count, max new tokens, end-of-text id or -1, end-of-turn id or -1, max context, 0}; the
+ * caller sets it before the first generated token.  Once done nothing advances, so further
+ * replayed steps recompute the last step unchanged; the host reads `done` between replays. */
+int q4d_advance_session(int32_t* tokens, int32_t* positions, const int32_t* next_token, const float* score,
+                        int32_t* hist_tokens, float* hist_scores, int32_t* hist_count, int32_t hist_capacity,
+                        int32_t* stop_state, void* stream);
 
 /* ---- fixed-point (RTL-exact) decode ------------------------------------------
  * The integer arithmetic of the reference's FPGA datapath, bit for bit

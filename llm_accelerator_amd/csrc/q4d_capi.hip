@@ -772,6 +772,16 @@ int q4d_advance(int32_t* tokens, int32_t* positions, const int32_t* next_token, 
                         hist_capacity, as_stream(stream));
 }
 
+int q4d_advance_session(int32_t* tokens, int32_t* positions, const int32_t* next_token, const float* score,
+                        int32_t* hist_tokens, float* hist_scores, int32_t* hist_count, int32_t hist_capacity,
+                        int32_t* stop_state, void* stream) {
+  if (!tokens || !positions || !next_token || !stop_state) return Q4D_ERR_NULL;
+  if (hist_tokens && (!hist_count || !score || hist_capacity < 0)) return Q4D_ERR_NULL;
+  if (!aligned(stop_state, 4)) return Q4D_ERR_BAD_ADDR;
+  return launch_advance_session(tokens, positions, next_token, score, hist_tokens, hist_scores, hist_count,
+                                hist_capacity, stop_state, as_stream(stream));
+}
+
 int q4d_apply_rope(const float* x, float* y, const float* cos, const float* sin, int32_t batch, int32_t heads,
                    int32_t head_dim, void* stream) {
   if (!x || !y || !cos || !sin) return Q4D_ERR_NULL;

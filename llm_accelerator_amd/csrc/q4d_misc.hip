@@ -160,6 +160,49 @@ __global__ void advance_kernel(int32_t* tokens, int32_t* positions, const int32_
   }
 }
 
+// The advance step with the decode session's stop rules applied on the device
+// (qot_session.c:41-60 checks them in this order after every generated token):
+// end-of-text, end-of-turn, the new-token budget, the context cap.  stop: int32[8] =
+// done, stop reason, generated count, max new tokens, end-of-text id (-1: off),
+// end-of-turn id (-1: off), max context, unused.  Once done, nothing moves: a
+// replayed step recomputes the last row with the same token and position.
+__global__ void advance_session_kernel(int32_t* tokens, int32_t* positions, const int32_t* next_token,
+                                       const float* score, int32_t* hist_tokens, float* hist_scores,
+                                       int32_t* hist_count, int32_t hist_capacity, int32_t* stop) {
+  if (threadIdx.x != 0 || stop[0]) return;
+  const int32_t nt = next_token[0];
+  if (hist_tokens) {
+    const int32_t c = hist_count[0];
+    if (c < hist_capacity) {
+      hist_tokens[c] = nt;
+      if (hist_scores) hist_scores[c] = score[0];
+      hist_count[0] = c + 1;
+    }
+  }
+  const int32_t gen = stop[2] + 1;
+  stop[2] = gen;
+  int32_t why = Q4D_SESSION_STOP_NONE;
+  if (stop[4] >= 0 && nt == stop[4]) why = Q4D_SESSION_STOP_EOS;
+  else if (stop[5] >= 0 && nt == stop[5]) why = Q4D_SESSION_STOP_IM_END;
+  else if (gen >= stop[3]) why = Q4D_SESSION_STOP_MAX_NEW;
+  else if (positions[0] + 1 >= stop[6]) why = Q4D_SESSION_STOP_CONTEXT;
+  if (why != Q4D_SESSION_STOP_NONE) {
+    stop[1] = why;
+    stop[0] = 1;
+    return;
+  }
+  tokens[0] = nt;
+  positions[0] += 1;
+}
+
+int launch_advance_session(int32_t* tokens, int32_t* positions, const int32_t* next_token, const float* score,
+                           int32_t* hist_tokens, float* hist_scores, int32_t* hist_count, int32_t hist_capacity,
+                           int32_t* stop, hipStream_t stream) {
+  hipLaunchKernelGGL(advance_session_kernel, dim3(1), dim3(64), 0, stream, tokens, positions, next_token, score,
+                     hist_tokens, hist_scores, hist_count, hist_capacity, stop);
+  return check_launch();
+}
+
 int launch_advance(int32_t* tokens, int32_t* positions, const int32_t* next_token, const float* score,
                    int32_t* hist_tokens, float* hist_scores, int32_t* hist_count, int32_t hist_capacity,
                    hipStream_t stream) {

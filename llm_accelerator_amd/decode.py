@@ -44,6 +44,11 @@ class GreedyDecoder:
         self._lib = _lib.load()
         self._prefill = None
         self.position = 0
+        # device stop state of the session mode (q4d_advance_session): done, reason, generated,
+        # max new, end-of-text id, end-of-turn id, max context, unused; None = plain feedback
+        self._stop = None
+        self._stop_buf = torch.zeros(8, dtype=torch.int32, device=dev)  # captured graphs keep its address
+        self._graph_session = None
 
     # -- one step, launched on the current stream ---------------------------------
     def _launch_step(self, logits: torch.Tensor | None = None, record: bool = True) -> None:
@@ -52,6 +57,12 @@ class GreedyDecoder:
                                           ctypes.byref(self._kvd), self.next_tok.data_ptr(),
                                           self.score.data_ptr(), logits.data_ptr() if logits is not None else None,
                                           self.ws.ptr, self.ws.nbytes, st), "q4d_run_one_token")
+        if self._stop is not None and record:
+            check(self._lib.q4d_advance_session(self.tok.data_ptr(), self.pos.data_ptr(), self.next_tok.data_ptr(),
+                                                self.score.data_ptr(), self.hist_tok.data_ptr(),
+                                                self.hist_score.data_ptr(), self.hist_count.data_ptr(), self.hist_cap,
+                                                self._stop.data_ptr(), st), "q4d_advance_session")
+            return
         check(self._lib.q4d_advance(self.tok.data_ptr(), self.pos.data_ptr(), self.next_tok.data_ptr(),
                                     self.score.data_ptr(), self.hist_tok.data_ptr() if record else None,
                                     self.hist_score.data_ptr() if record else None, self.hist_count.data_ptr(),
@@ -127,6 +138,52 @@ class GreedyDecoder:
             self.position += full * k
         for _ in range(rest):
             self.step()
+
+    def run_session(self, prompt: list[int], max_new_tokens: int, eos_token_id: int | None = 151643,
+                    im_end_token_id: int | None = 151645) -> tuple[list[int], list[float], str]:
+        """The decode session (qot_session semantics: serial prefill, stop on end-of-text /
+        end-of-turn / the new-token budget / the context cap) with the stop rules applied on
+        the device: graphs of ``steps_per_graph`` steps replay until the device says done, one
+        host read per replay.  ``None`` disables a stop token.  Returns (generated ids, their
+        logits, stop reason)."""
+        if max_new_tokens <= 0:
+            raise _lib.Q4DecError(-9, "GreedyDecoder.run_session")
+        vocab = self.model.config.vocab_size
+        for t in (eos_token_id, im_end_token_id):
+            if t is not None and not 0 <= t < vocab:
+                raise _lib.Q4DecError(-8, "GreedyDecoder.run_session")
+        if not prompt or len(prompt) > self.model.max_ctx:
+            raise _lib.Q4DecError(-10, "GreedyDecoder.run_session")
+        self._stop_buf.copy_(torch.tensor([0, 0, 0, max_new_tokens, -1 if eos_token_id is None else eos_token_id,
+                                           -1 if im_end_token_id is None else im_end_token_id, self.model.max_ctx,
+                                           0], dtype=torch.int32))
+        self._stop = self._stop_buf
+        try:
+            self.prefill(prompt)
+            while not int(self._stop[0].item()):
+                if self.use_graph:
+                    if self._graph_session is None:
+                        self._graph_session = self._capture_steps()
+                    self._graph_session.replay()
+                else:
+                    self._launch_step()
+            self.position = int(self.pos.item()) + 1
+            toks, scores = self.history()
+            reasons = ["NONE", "EOS", "IM_END", "MAX_NEW", "CONTEXT", "HW_ERROR"]
+            return toks, scores, reasons[int(self._stop[1].item())]
+        finally:
+            self._stop = None
+
+    def _capture_steps(self):
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.stream(s):
+            with torch.cuda.graph(g, stream=s):
+                for _ in range(self.steps_per_graph):
+                    self._launch_step()
+        torch.cuda.current_stream().wait_stream(s)
+        return g
 
     def history(self) -> tuple[list[int], list[float]]:
         c = int(self.hist_count.item())

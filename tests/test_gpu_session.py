@@ -9,6 +9,9 @@
   capacity ends two tokens after the prompt).
 - Fixed-point runner (q4d_session_fixed_runner): tokens and Q26 scores equal the
   oracle's fixed_run_one_token loop exactly.
+- Stop rules on the device (q4d_advance_session via GreedyDecoder.run_session, eager
+  and HIP-graph replays): the same tokens and stop reason as the host session for the
+  budget, end-of-text, end-of-turn and context-cap cases.
 """
 
 import numpy as np
@@ -101,3 +104,25 @@ def test_fixed_runner_matches_oracle(dev, small):
     print(f"[session] fixed-point tokens {toks} oracle {ref_toks}", flush=True)
     assert toks == ref_toks and why == "MAX_NEW"
     assert [e["score_q26"] for e in events if e["kind"] == "TOKEN"] == ref_scores
+
+
+@pytest.mark.parametrize("graph", [False, True])
+def test_device_stops_match_host_session(dev, small, graph):
+    """GreedyDecoder.run_session (stop rules on the device, graph replays) = the host session."""
+    cfg, host = small
+    model = build_model(cfg, host, max_ctx=24, device=dev)
+    ref_tokens, _ = greedy(model, PROMPT, 8)
+    dec = GreedyDecoder(model, steps_per_graph=4, use_graph=graph)
+    cases = [dict(max_new_tokens=7, eos_token_id=4095, im_end_token_id=4094),          # budget
+             dict(max_new_tokens=20, eos_token_id=int(ref_tokens[2]), im_end_token_id=4094),  # end-of-text
+             dict(max_new_tokens=20, eos_token_id=4095, im_end_token_id=int(ref_tokens[4])),  # end-of-turn
+             dict(max_new_tokens=40, eos_token_id=None, im_end_token_id=None)]            # context cap
+    for kw in cases:
+        toks, scores, why = dec.run_session(PROMPT, **kw)
+        hk = {k: (v if v is not None else 0) for k, v in kw.items()}
+        hk.update(stop_on_eos=int(kw["eos_token_id"] is not None), stop_on_im_end=int(kw["im_end_token_id"] is not None))
+        sess = DecodeSession.on_gpu(build_model(cfg, host, max_ctx=24, device=dev))
+        _, htoks, hwhy = sess.run(PROMPT, **hk)
+        print(f"[session] device stop {why} {toks} host {hwhy} {htoks}", flush=True)
+        assert (toks, why) == (htoks, hwhy)
+    assert dec.status() == 0
