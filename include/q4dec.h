@@ -405,6 +405,15 @@ int q4d_fixed_residual_add(const int32_t* hidden, const int32_t* x, int32_t n, i
 /* Q14.10 embedding rows of the tied Q4 table: (q * scale) >> 4 (56_...:214-221). */
 int q4d_fixed_embedding(const q4d_matrix_t* table, const int32_t* tokens, int32_t n, int32_t* hidden,
                         void* stream);
+/* Integer Q4 projection of one activation vector (compute_matrix_outputs,
+ * 21_export_qmap_qkv_projection_image.py:163-191; projection, 56_...:300-317):
+ * y[r] = sat24((sum_g s[r,g] * sum_{k in g} q[r,k] * x[k]) >> 14), Q12.12 in and out.
+ * x: device int32 [w->cols], w->cols in {1024, 2048, 3072}.  With input_gamma (device
+ * int16 Q8.7 [1024]) non-NULL, x is the Q14.10 hidden state and passes through the hidden
+ * RMSNorm first, as in the fused input-norm + q|k|v projection.  y: device int32
+ * [w->rows], not overlapping x.  Saturations are not counted. */
+int q4d_fixed_q4_gemv(const q4d_matrix_t* w, const int32_t* x, const int16_t* input_gamma, int32_t* y,
+                      void* stream);
 
 /* One fixed-point decoder layer at positions[0] (run_fixed_layer, 56_...:468-561): input
  * norm + q|k|v, q/k norm + RoPE + KV append + attention, o_proj + residual, post norm +

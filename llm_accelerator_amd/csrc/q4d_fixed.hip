@@ -1150,6 +1150,23 @@ int q4d_fixed_embedding(const q4d_matrix_t* table, const int32_t* tokens, int32_
   return check_launch();
 }
 
+int q4d_fixed_q4_gemv(const q4d_matrix_t* w, const int32_t* x, const int16_t* input_gamma, int32_t* y,
+                      void* stream) {
+  if (!w || !w->w || !w->s || !x || !y) return Q4D_ERR_NULL;
+  if (w->rows <= 0 || !fx_k_ok(w->cols) || (input_gamma && w->cols != 1024)) return Q4D_ERR_SHAPE;
+  if (!aligned(w->w, 16) || !aligned(w->s, 4) || !aligned(x, 16)) return Q4D_ERR_BAD_ADDR;
+  FxGemv g = fx_gemv_base();
+  g.w0 = g.w1 = g.w2 = w->w;
+  g.s0 = g.s1 = g.s2 = w->s;
+  g.e0 = g.e1 = g.rows = w->rows;
+  g.K = w->cols;
+  g.x = x;
+  g.gamma = input_gamma;
+  g.y = y;
+  hipStream_t st = fx_stream(stream);
+  return input_gamma ? fx_launch_gemv<FX_PRO_NORM, FX_EPI_Q12>(g, st) : fx_launch_gemv<FX_PRO_LOAD, FX_EPI_Q12>(g, st);
+}
+
 int q4d_fixed_decoder_layer(const q4d_fixed_model_t* model, int32_t layer, const int32_t* hidden_in,
                             int32_t* hidden_out, const q4d_fixed_kv_t* kv, const int32_t* positions, void* ws,
                             size_t ws_bytes, void* stream) {

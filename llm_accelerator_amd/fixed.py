@@ -170,6 +170,23 @@ def silu_mul(gate_q12_12, up_q12_12) -> dict:
     return {"lut_index": idx, "sigmoid": sig, "silu_gate": silu, "hidden": hidden}
 
 
+def projection(activation, weight, input_gamma=None) -> torch.Tensor:
+    """Integer Q4 projection of one vector (``projection``, 56_...:300-317, over
+    ``compute_matrix_outputs``, 21_export_qmap_qkv_projection_image.py:163-191): Q12.12
+    activations (or, with ``input_gamma``, the Q14.10 hidden state through the hidden
+    RMSNorm) times the Q4 matrix ``weight`` (a Q4Tensor or its (packed, scale) pair) ->
+    Q12.12 rows, int32 on the GPU."""
+    from .model import Q4Tensor
+    w = weight if isinstance(weight, Q4Tensor) else Q4Tensor.from_numpy(*weight, device="cuda")
+    x = _i32(activation, w.device).reshape(-1)
+    g = _i16(input_gamma, w.device) if input_gamma is not None else None
+    y = torch.empty(w.shape[0], dtype=torch.int32, device=w.device)
+    d = w.descriptor()
+    check(_lib.load().q4d_fixed_q4_gemv(ctypes.byref(d), x.data_ptr(), g.data_ptr() if g is not None else None,
+                                        y.data_ptr(), current_stream()), "q4d_fixed_q4_gemv")
+    return y
+
+
 def residual_add(hidden_q14_10, x_q12_12) -> torch.Tensor:
     """sat24(hidden + (x >> 2)) (56_...:530-533, 558-561)."""
     lib = _lib.load()
@@ -199,15 +216,44 @@ class FixedQ4Model:
     56_...:238-291), the Q1.15 RoPE table and the Q0.31 score scale."""
 
     def __init__(self, model: Q4ForCausalLM, host: dict):
+        q = lambda v: quantize_signed(v, GAMMA_WIDTH, GAMMA_FRAC)[0]  # noqa: E731
+        gammas = [{"input": q(L["input_layernorm"]), "post": q(L["post_attention_layernorm"]),
+                   "q": q(L["q_norm"]), "k": q(L["k_norm"])} for L in host["layers"]]
+        cos, sin = rope_table_q1_15(model.config, model.max_ctx)
+        self._setup(model, gammas, q(host["norm"]), cos, sin, score_scale_q0_31(model.config.head_dim ** -0.5))
+
+    @classmethod
+    def from_parts(cls, model: Q4ForCausalLM, gammas: list, final_gamma, rope_cos, rope_sin,
+                   score_scale: int) -> "FixedQ4Model":
+        """A model from integer parameters already in device format (a board runtime's):
+        per layer ``{"input", "post", "q", "k"}`` Q8.7 gammas, the final Q8.7 gamma,
+        Q1.15 cos/sin rows for positions ``0 .. model.max_ctx - 1`` and the Q0.31 score scale."""
+        cfg = model.config
+        if len(gammas) != cfg.num_hidden_layers:
+            raise ValueError(f"{len(gammas)} layers of gammas for a {cfg.num_hidden_layers}-layer model")
+        for L in gammas:
+            for k, n in (("input", cfg.hidden_size), ("post", cfg.hidden_size), ("q", cfg.head_dim),
+                         ("k", cfg.head_dim)):
+                if np.asarray(L[k]).shape != (n,):
+                    raise ValueError(f"gamma {k} has shape {np.asarray(L[k]).shape}, expected ({n},)")
+        if np.asarray(final_gamma).shape != (cfg.hidden_size,):
+            raise ValueError("final gamma shape")
+        for t in (rope_cos, rope_sin):
+            if np.asarray(t).shape != (model.max_ctx, cfg.head_dim):
+                raise ValueError(f"RoPE table shape {np.asarray(t).shape}, expected ({model.max_ctx}, {cfg.head_dim})")
+        if not 0 < int(score_scale) < 2 ** 31:
+            raise ValueError("score scale must be a positive Q0.31 value")
+        self = cls.__new__(cls)
+        self._setup(model, gammas, final_gamma, rope_cos, rope_sin, int(score_scale))
+        return self
+
+    def _setup(self, model, gammas, final_gamma, cos, sin, score_scale):
         cfg, dev = model.config, model.device
         self.model, self.config = model, cfg
-        q = lambda v: _i16(quantize_signed(v, GAMMA_WIDTH, GAMMA_FRAC)[0], dev)  # noqa: E731
-        self.gammas = [{"input": q(L["input_layernorm"]), "post": q(L["post_attention_layernorm"]),
-                        "q": q(L["q_norm"]), "k": q(L["k_norm"])} for L in host["layers"]]
-        self.final_gamma = q(host["norm"])
-        cos, sin = rope_table_q1_15(cfg, model.max_ctx)
+        self.gammas = [{k: _i16(L[k], dev) for k in ("input", "post", "q", "k")} for L in gammas]
+        self.final_gamma = _i16(final_gamma, dev)
         self.rope_cos, self.rope_sin = _i16(cos, dev), _i16(sin, dev)
-        self.score_scale = score_scale_q0_31(cfg.head_dim ** -0.5)
+        self.score_scale = score_scale
         self._base = model.descriptor()
         self._layers = (Q4dFixedLayer * len(self.gammas))(*[
             Q4dFixedLayer(g["input"].data_ptr(), g["post"].data_ptr(), g["q"].data_ptr(), g["k"].data_ptr())

@@ -218,9 +218,36 @@ def main() -> None:
     record("fixed_kv_append_l0", srcs + [vec / "kv_cache_append_real_meta.json"],
            "layer 0, position 4, base 0x414100000, max context 256, word32 elements", **arr)
 
+    # 7. QMAP v1 images (Source/QMAP_FORMAT.md:134-296) as raw little-endian bytes, and the
+    #    PL-DDR segment manifest of the board-validated runtime (a data file, copied as is).
+    def image(name: str) -> tuple[Path, np.ndarray]:
+        src = vec / f"{name}_words32.hex"
+        return src, read_hex(src, 32, False).astype("<u4").view(np.uint8)
+
+    small = {}
+    srcs = []
+    for name in ("qmap_dot64_image", "qmap_row1024_image", "qmap_input_rmsnorm_image", "qmap_attention_frontend_image",
+                 "qmap_attention_score_value_image", "qmap_o_proj_image", "qmap_post_attention_residual_norm_image",
+                 "qmap_mlp_silu_mul_image", "qmap_mlp_down_image", "qmap_final_token_tail_compact_image"):
+        src, b = image(name)
+        srcs.append(src)
+        small[name] = b
+    record("qmap_stage_images", srcs, "layer-0 QMAP packets / smoke images, raw bytes (little-endian words)", **small)
+    src, b = image("qmap_qkv_projection_from_input_rmsnorm_image")
+    e_src = vec / "qmap_qkv_projection_expected_from_input_rmsnorm_words32.hex"
+    record("qmap_qkv_layer0_image", [src, e_src],
+           "layer-0 q|k|v packet with the full Q4 q/k/v weights in the image; expected q|k|v Q12.12 for the "
+           "input-RMSNorm output of qmap_input_rmsnorm_image", image=b,
+           expected_q12_12=read_hex(e_src, 32, True))
+    seg = ref / "lmdeploy" / "qwen3-0p6b-q4-qweb-demo" / "model" / "pl_ddr_binary_segments.json"
+    (HERE / "pl_ddr_binary_segments.json").write_bytes(seg.read_bytes())
+    manifest["pl_ddr_binary_segments"] = {"file": "pl_ddr_binary_segments.json",
+                                          "note": "61-segment PL-DDR runtime manifest (data file, copied verbatim)",
+                                          "sources": {str(seg.relative_to(ref)): sha256(seg)}}
+
     (HERE / "MANIFEST.json").write_text(json.dumps(manifest, indent=2) + "\n")
     for k, v in manifest.items():
-        print(k, v["arrays"])
+        print(k, v.get("arrays", v["file"]))
 
 
 if __name__ == "__main__":

@@ -150,3 +150,11 @@ def test_stage_entry_validation(lib):
     assert lib.q4d_fixed_silu_mul(FAKE, FAKE, 8, None, FAKE, None, None, None, None) == -7
     assert lib.q4d_fixed_residual_add(FAKE, FAKE, 0, FAKE, None) == -11
     assert lib.q4d_fixed_embedding(ctypes.byref(Q4dMatrix(FAKE, FAKE, 10, 100)), FAKE, 1, FAKE, None) == -11
+    m = lambda rows, cols, w=FAKE: ctypes.byref(Q4dMatrix(w, FAKE, rows, cols))  # noqa: E731
+    assert lib.q4d_fixed_q4_gemv(m(16, 512), FAKE, None, FAKE, None) == -11       # K not 1024 / 2048 / 3072
+    assert lib.q4d_fixed_q4_gemv(m(16, 2048), FAKE, FAKE, FAKE, None) == -11      # norm prologue needs K = 1024
+    assert lib.q4d_fixed_q4_gemv(m(0, 1024), FAKE, None, FAKE, None) == -11
+    assert lib.q4d_fixed_q4_gemv(m(16, 1024, None), FAKE, None, FAKE, None) == -7
+    assert lib.q4d_fixed_q4_gemv(m(16, 1024), None, None, FAKE, None) == -7
+    assert lib.q4d_fixed_q4_gemv(m(16, 1024, FAKE + 8), FAKE, None, FAKE, None) == -4
+    assert lib.q4d_fixed_q4_gemv(m(16, 1024), FAKE + 4, None, FAKE, None) == -4
