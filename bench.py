@@ -23,12 +23,15 @@ GB/s flushed and resident; the LM head alone; full 28-layer greedy decode
 tok/s (config 3: 64-token prompt, 256 generated); prefill of one 2048-token
 sequence (config 4: tok/s and TFLOP/s against the dense fp16 MFMA peak);
 batched decode of 64 sequences over 4096 cached positions (config 5: tok/s
-and GB/s of K/V + weights); a measured HBM rate (torch's device copy of
+and GB/s of K/V + weights); the fixed-point (RTL-exact) layer and token;
+bf16 -> Q4 conversion of every matrix of the model (GB/s of bf16 read plus
+codes and scales written); a measured HBM rate (torch's device copy of
 512 MiB windows, read + written bytes) that ``roofline`` also quotes its
 rate against, beside the 8 TB/s vendor figure; and the oracle's CPU rates on
 the host cores (``cpu_baseline``: the config-2 layer step on all cores;
 ``extras.cpu_legs``: config 1 as an fp32 matvec and as the int64 Q26
-restatement, config 2 on one thread, config 3 per token).
+restatement, config 2 on one thread, config 3 per token, the oracle's
+quantizer on a 3072x1024 fp32 matrix).
 """
 
 from __future__ import annotations
@@ -64,9 +67,10 @@ def parse():
     ap.add_argument("--copies", type=int, default=40)
     ap.add_argument("--precision", type=int, default=2, choices=(1, 2))
     ap.add_argument("--no-extras", action="store_true", help="skip every leg beside the layer step")
-    ap.add_argument("--extras", default="c1,c3,c4,c5,fx",
+    ap.add_argument("--extras", default="c1,c3,c4,c5,fx,q4c",
                     help="comma list of the legs to run beside the layer step: c1 GEMV, c3 decode + LM head, "
-                         "c4 prefill, c5 batched decode, fx fixed-point (RTL-exact) layer and token")
+                         "c4 prefill, c5 batched decode, fx fixed-point (RTL-exact) layer and token, "
+                         "q4c float -> Q4 conversion of the whole model")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--decode-gen", type=int, default=256)
@@ -202,8 +206,8 @@ def main():
     torch.cuda.empty_cache()
 
     legs = set() if args.no_extras else {x.strip() for x in args.extras.split(",") if x.strip()}
-    if legs - {"c1", "c3", "c4", "c5", "fx"}:
-        sys.exit(f"unknown legs {sorted(legs - {'c1', 'c3', 'c4', 'c5', 'fx'})}")
+    if legs - {"c1", "c3", "c4", "c5", "fx", "q4c"}:
+        sys.exit(f"unknown legs {sorted(legs - {'c1', 'c3', 'c4', 'c5', 'fx', 'q4c'})}")
     if "c1" in legs:
         # -------------------------------------------------------- C1 GEMV
         from llm_accelerator_amd.model import Q4Tensor, gemv_bytes, random_q4
@@ -386,6 +390,43 @@ def main():
     if legs & {"c3", "c4", "c5", "fx"}:
         del fmodel
         torch.cuda.empty_cache()
+    if "q4c" in legs:
+        # -------------------------------------------------------- float -> Q4 conversion of the whole model
+        qcfg = M.Qwen3Config()
+        h, I = qcfg.hidden_size, qcfg.intermediate_size
+        shapes = [(2048, h), (1024, h), (1024, h), (h, 2048), (I, h), (I, h), (h, I)] * qcfg.num_hidden_layers
+        shapes.append((qcfg.vocab_size, h))
+        mats = [(torch.randn(r, c, generator=gen, device=dev) * 0.03).to(torch.bfloat16) for r, c in shapes]
+        outs = [(torch.empty(r, c // 2, dtype=torch.uint8, device=dev),
+                 torch.empty(r, c // 64, dtype=torch.uint16, device=dev)) for r, c in shapes]
+        qstatus = torch.zeros(2, dtype=torch.int32, device=dev)
+
+        def quant(i):
+            w, (pk, sc) = mats[i], outs[i]
+            check(lib.q4d_quantize_q4(w.data_ptr(), 2, w.shape[1], w.shape[0], w.shape[1], pk.data_ptr(),
+                                      sc.data_ptr(), qstatus.data_ptr(), st()), "q4d_quantize_q4")
+        for i in range(len(shapes)):
+            quant(i)
+        torch.cuda.synchronize()
+        # HIP graphs: one of the 197 conversions, one of the table alone
+        g_all = graph_of(quant, len(shapes), torch)
+        g_tab = graph_of(lambda i: quant(len(shapes) - 1), 1, torch)
+        g_all.replay()
+        g_tab.replay()
+        all_ms = time_graph(g_all, 10, torch)
+        emb_us = time_graph(g_tab, 20, torch) * 1e3
+        params = sum(r * c for r, c in shapes)
+        qbytes = params * 2 + params // 2 + params // 64 * 2   # bf16 in, codes + Q2.14 scales out
+        er, ec = shapes[-1]
+        ebytes = er * ec * 2 + er * ec // 2 + er * ec // 64 * 2
+        extras["q4c_quantize"] = {
+            "workload": "bf16 -> Q4 of every Qwen3-0.6B projection and the tied table (197 matrices)",
+            "params": params, "bytes": qbytes, "ms": round(all_ms, 4), "GBps": round(qbytes / all_ms / 1e6, 1),
+            "hbm_frac": round(qbytes / all_ms / 1e6 / HBM_PEAK_GBPS, 4), "table_us": round(emb_us, 2),
+            "table_GBps": round(ebytes / emb_us / 1e3, 1), "status": qstatus.tolist()}
+        log(f"[bench] Q4 conversion: {json.dumps(extras['q4c_quantize'])}")
+        del mats, outs, g_all, g_tab
+        torch.cuda.empty_cache()
 
     if legs:
         # measured HBM ceiling beside the 8 TB/s vendor figure: torch's device
@@ -543,6 +584,11 @@ def cpu_extra_legs(ctx, step_bytes):
     tt = sorted(ts[1:])[len(ts[1:]) // 2]
     out["c3_per_token"] = {"ms": round(tt * 1e3, 1), "tok_s": round(1.0 / tt, 2), "steps": len(ts),
                            "note": "median of steps 1-7 at positions 1-7 (the first step is the warm-up)"}
+    wq = (rng.standard_normal((3072, 1024)) * 0.03).astype(np.float32)
+    t, n = _median_time(lambda: o.quantize_weight_q4(wq), 5, 2.0)
+    qb = 3072 * 1024 * 4 + 3072 * 512 + 3072 * 16 * 2
+    out["q4c_oracle"] = {"shape": "3072x1024 fp32 -> Q4", "ms": round(t * 1e3, 2), "GBps": round(qb / t / 1e9, 3),
+                         "runs": n}
     return out
 
 

@@ -86,7 +86,7 @@ enum {
   Q4D_STATUS_SYNC_TIMEOUT = 4  /* a persistent decode kernel gave up waiting for another block */
 };
 
-enum { Q4D_F16 = 0, Q4D_F32 = 1 };
+enum { Q4D_F16 = 0, Q4D_F32 = 1, Q4D_BF16 = 2 };
 
 typedef struct q4d_matrix {
   const uint8_t* w;   /* [rows, cols/2] packed int4 */
@@ -536,6 +536,21 @@ int q4d_session_gpu_runner(void* runner_context, uint32_t input_token_id, uint32
                            q4d_token_result_t* result);
 int q4d_session_fixed_runner(void* runner_context, uint32_t input_token_id, uint32_t position,
                              q4d_token_result_t* result);
+
+/* ---- float -> Q4 weight conversion ------------------------------------------
+ * The reference's quantizer (quantize_weight_q4, 13_export_q4_gemv_vectors.py:101-135;
+ * the same rule in 26_...:126-145, 28_...:103-121, 30_...:103-121, 33_...:95-113) for a
+ * device matrix: per 64-column group absmax, code = rint(fp32(absmax / 7) * 2^14)
+ * round-half-even, 1 for a nonzero group that rounds to 0; q = clip(rint(w / (code /
+ * 2^14)), -8, 7), packed two per byte with the even column in the low nibble.
+ * weight: device fp32 (Q4D_F32) or bf16 (Q4D_BF16) [rows, ld], row-major, cols a
+ * multiple of 64, ld >= cols; packed: device uint8 [rows, cols/2]; scale: device uint16
+ * [rows, cols/64].  status: device int32 [2] that the caller zeroes first; the kernel
+ * adds the number of groups whose code exceeds 65535 (the reference raises "Q4 scale does
+ * not fit unsigned 16-bit Q2.14") to status[0] and of groups holding a non-finite value to
+ * status[1]; those groups' outputs are not meaningful. */
+int q4d_quantize_q4(const void* weight, int32_t dtype, int64_t ld, int32_t rows, int32_t cols, uint8_t* packed,
+                    uint16_t* scale, int32_t* status, void* stream);
 
 #ifdef __cplusplus
 }

@@ -15,6 +15,7 @@ LIB_PATH = Path(__file__).resolve().with_name("libq4dec.so")
 
 Q4D_F16 = 0
 Q4D_F32 = 1
+Q4D_BF16 = 2
 STATUS_BAD_TOKEN = 1
 STATUS_BAD_POSITION = 2
 
@@ -167,6 +168,7 @@ SIGNATURES = {
     "q4d_fixed_residual_add": ([_P, _P, c_int32, _P, _P], c_int32),
     "q4d_fixed_embedding": ([POINTER(Q4dMatrix), _P, c_int32, _P, _P], c_int32),
     "q4d_fixed_q4_gemv": ([POINTER(Q4dMatrix), _P, _P, _P, _P], c_int32),
+    "q4d_quantize_q4": ([_P, c_int32, ctypes.c_int64, c_int32, c_int32, _P, _P, _P, _P], c_int32),
     "q4d_fixed_decoder_layer": ([_FM, c_int32, _P, _P, _FKV, _P, _P, c_size_t, _P], c_int32),
     "q4d_fixed_run_one_token": ([_FM, _P, _P, _FKV, _P, _P, _P, _P, _P, c_size_t, _P], c_int32),
     "q4d_session_default_options": ([POINTER(Q4dSessionOptions)], None),

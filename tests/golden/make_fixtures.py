@@ -245,6 +245,13 @@ def main() -> None:
                                           "note": "61-segment PL-DDR runtime manifest (data file, copied verbatim)",
                                           "sources": {str(seg.relative_to(ref)): sha256(seg)}}
 
+    # 8. The model's config.json (hyperparameters the checkpoint converter reads; data file).
+    cfg = ref / "Qwen3-0.6B-Base" / "config.json"
+    (HERE / "qwen3_0p6b_config.json").write_bytes(cfg.read_bytes())
+    manifest["qwen3_0p6b_config"] = {"file": "qwen3_0p6b_config.json",
+                                     "note": "Qwen3-0.6B-Base config.json (data file, copied verbatim)",
+                                     "sources": {str(cfg.relative_to(ref)): sha256(cfg)}}
+
     (HERE / "MANIFEST.json").write_text(json.dumps(manifest, indent=2) + "\n")
     for k, v in manifest.items():
         print(k, v.get("arrays", v["file"]))
