@@ -18,19 +18,19 @@ with the largest time, HIP events around graph replays of that stage alone):
 its algorithmic bytes per launch (model.stage_bytes_layer) over its average
 launch time; every stage's rate is listed beside it.
 
-Also reported (same run, under "extras"): the 3072x1024 Q4 GEMV (config 1)
+Also reported (same run, under "extras"): the 3072x1024 Q4 GEMV
 GB/s flushed and resident; the LM head alone; full 28-layer greedy decode
-tok/s (config 3: 64-token prompt, 256 generated); prefill of one 2048-token
-sequence (config 4: tok/s and TFLOP/s against the dense fp16 MFMA peak);
-batched decode of 64 sequences over 4096 cached positions (config 5: tok/s
+tok/s (64-token prompt, 256 generated); prefill of one 2048-token
+sequence (tok/s and TFLOP/s against the dense fp16 MFMA peak);
+batched decode of 64 sequences over 4096 cached positions (tok/s
 and GB/s of K/V + weights); the fixed-point (RTL-exact) layer and token;
 bf16 -> Q4 conversion of every matrix of the model (GB/s of bf16 read plus
 codes and scales written); a measured HBM rate (torch's device copy of
 512 MiB windows, read + written bytes) that ``roofline`` also quotes its
 rate against, beside the 8 TB/s vendor figure; and the oracle's CPU rates on
-the host cores (``cpu_baseline``: the config-2 layer step on all cores;
-``extras.cpu_legs``: config 1 as an fp32 matvec and as the int64 Q26
-restatement, config 2 on one thread, config 3 per token, the oracle's
+the host cores (``cpu_baseline``: the layer step on all cores;
+``extras.cpu_legs``: the 3072x1024 GEMV as an fp32 matvec and as the int64 Q26
+restatement, the layer step on one thread, the 28-layer decode per token, the oracle's
 quantizer on a 3072x1024 fp32 matrix).
 """
 
@@ -50,8 +50,8 @@ STAGE_KERNELS = {"qkv": "input RMSNorm + q|k|v Q4 GEMV", "attention": "q/k norm 
                  "o_proj": "o_proj Q4 GEMV + residual", "gate_up": "post-norm + gate/up Q4 GEMV + SwiGLU",
                  "down": "down Q4 GEMV + residual"}
 HBM_PEAK_GBPS = 8000.0
-C4_TOKENS = 2048             # prefill of one 2048-token sequence
-C5_BATCH, C5_CTX = 64, 4096  # batched decode: 64 sequences over 4096 cached positions
+PREFILL_TOKENS = 2048              # prefill of one 2048-token sequence
+BATCH_SEQS, BATCH_CTX = 64, 4096  # batched decode: 64 sequences over 4096 cached positions
 
 
 def log(*a):
@@ -67,9 +67,10 @@ def parse():
     ap.add_argument("--copies", type=int, default=40)
     ap.add_argument("--precision", type=int, default=2, choices=(1, 2))
     ap.add_argument("--no-extras", action="store_true", help="skip every leg beside the layer step")
-    ap.add_argument("--extras", default="c1,c3,c4,c5,fx,q4c",
-                    help="comma list of the legs to run beside the layer step: c1 GEMV, c3 decode + LM head, "
-                         "c4 prefill, c5 batched decode, fx fixed-point (RTL-exact) layer and token, "
+    ap.add_argument("--extras", default="gemv,decode,prefill,batch,fx,q4c",
+                    help="comma list of the legs to run beside the layer step: gemv (3072x1024 GEMV), "
+                         "decode (28-layer decode + LM head), prefill, batch (batched decode), "
+                         "fx fixed-point (RTL-exact) layer and token, "
                          "q4c float -> Q4 conversion of the whole model")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
@@ -119,7 +120,7 @@ def main():
     dev = torch.device("cuda:0")
     st = lambda: torch.cuda.current_stream().cuda_stream  # noqa: E731
 
-    # ------------------------------------------------------------ C2 layer step
+    # ------------------------------------------------------------ layer step
     ctx, copies = args.ctx, args.copies
     cfg = M.Qwen3Config(num_hidden_layers=copies, vocab_size=2048)
     t = time.time()
@@ -134,7 +135,7 @@ def main():
     h_in = torch.randn(1, 1024, generator=gen, device=dev, dtype=torch.float32)
     h_out = torch.empty_like(h_in)
     desc, kvd = model.descriptor(), kv.descriptor()
-    log(f"[bench] C2 setup {time.time() - t:.1f}s: {copies} layers, ctx {ctx}")
+    log(f"[bench] layer-step setup {time.time() - t:.1f}s: {copies} layers, ctx {ctx}")
 
     def layer_step(i):
         check(lib.q4d_decoder_layer(ctypes.byref(desc), i % copies, h_in.data_ptr(), h_out.data_ptr(),
@@ -159,12 +160,12 @@ def main():
     ms_per_step = (t1 - t0) * 1e3 / args.steps
     step_bytes = M.algorithmic_bytes_layer(M.Qwen3Config(), ctx)
     value = step_bytes / (ms_per_step * 1e-3) / 1e9
-    log(f"[bench] C2 flushed: {ms_per_step * 1e3:.2f} us/step, {value:.1f} GB/s")
+    log(f"[bench] layer step flushed: {ms_per_step * 1e3:.2f} us/step, {value:.1f} GB/s")
 
     g_res = graph_of(lambda i: layer_step(0), copies, torch)
     res_ms = time_graph(g_res, max(1, args.steps // copies), torch) / copies
     resident = step_bytes / (res_ms * 1e-3) / 1e9
-    log(f"[bench] C2 resident: {res_ms * 1e3:.2f} us/step, {resident:.1f} GB/s")
+    log(f"[bench] layer step resident: {res_ms * 1e3:.2f} us/step, {resident:.1f} GB/s")
 
     # per-stage durations (graphs of `copies` launches of one stage, HIP events)
     stage_names = ["qkv", "attention", "o_proj", "gate_up", "down"]
@@ -200,16 +201,17 @@ def main():
                 "bytes_per_launch": stage_bytes[dom], "avg_launch_us": round(stage_us[dom], 3),
                 "per_stage_GBps": {k: round(v, 1) for k, v in stage_rate.items()}}
 
-    extras = {"c2_resident_GBps": round(resident, 1), "c2_resident_us_per_step": round(res_ms * 1e3, 3),
-              "c2_flushed_us_per_step": round(ms_per_step * 1e3, 3), "stage_us_flushed": stage_us}
+    extras = {"layer_resident_GBps": round(resident, 1), "layer_resident_us_per_step": round(res_ms * 1e3, 3),
+              "layer_flushed_us_per_step": round(ms_per_step * 1e3, 3), "stage_us_flushed": stage_us}
     del model, kv, ws, g_flush, g_res
     torch.cuda.empty_cache()
 
     legs = set() if args.no_extras else {x.strip() for x in args.extras.split(",") if x.strip()}
-    if legs - {"c1", "c3", "c4", "c5", "fx", "q4c"}:
-        sys.exit(f"unknown legs {sorted(legs - {'c1', 'c3', 'c4', 'c5', 'fx', 'q4c'})}")
-    if "c1" in legs:
-        # -------------------------------------------------------- C1 GEMV
+    known = {"gemv", "decode", "prefill", "batch", "fx", "q4c"}
+    if legs - known:
+        sys.exit(f"unknown legs {sorted(legs - known)}")
+    if "gemv" in legs:
+        # -------------------------------------------------------- 3072x1024 GEMV
         from llm_accelerator_amd.model import Q4Tensor, gemv_bytes, random_q4
         rng = np.random.default_rng(0)
         packed, scale = random_q4(rng, 3072, 1024)
@@ -228,24 +230,24 @@ def main():
         us_fl = time_graph(g1, 20, torch) / ncop * 1e3
         g2 = graph_of(lambda i: gemv(i, True), ncop, torch)
         us_res = time_graph(g2, 20, torch) / ncop * 1e3
-        extras["c1_gemv"] = {"shape": "3072x1024 q4, fp16 x/y", "bytes": gb,
+        extras["gemv_3072x1024"] = {"shape": "3072x1024 q4, fp16 x/y", "bytes": gb,
                              "flushed_us": round(us_fl, 3), "flushed_GBps": round(gb / us_fl / 1e3, 1),
                              "resident_us": round(us_res, 3), "resident_GBps": round(gb / us_res / 1e3, 1)}
-        log(f"[bench] C1 GEMV: {json.dumps(extras['c1_gemv'])}")
+        log(f"[bench] GEMV 3072x1024: {json.dumps(extras['gemv_3072x1024'])}")
         del P, S, g1, g2
         torch.cuda.empty_cache()
 
-    if legs & {"c3", "c4", "c5", "fx"}:
+    if legs & {"decode", "prefill", "batch", "fx"}:
         fcfg = M.Qwen3Config()
         t = time.time()
         fhost = M.random_host_weights(fcfg, seed=0)
-        fmodel = M.build_model(fcfg, fhost, max_ctx=max(64 + args.decode_gen + 16, C5_CTX + 1), device=dev)
+        fmodel = M.build_model(fcfg, fhost, max_ctx=max(64 + args.decode_gen + 16, BATCH_CTX + 1), device=dev)
         norm_keys = ("input_layernorm", "post_attention_layernorm", "q_norm", "k_norm")
         fnorms = {"layers": [{k: L[k] for k in norm_keys} for L in fhost["layers"]], "norm": fhost["norm"]}
         del fhost
         log(f"[bench] 28-layer model setup {time.time() - t:.1f}s")
-    if "c3" in legs:
-        # -------------------------------------------------------- C3 decode tok/s
+    if "decode" in legs:
+        # -------------------------------------------------------- 28-layer decode tok/s
         from llm_accelerator_amd.decode import GreedyDecoder
         prompt = np.random.default_rng(1).integers(0, fcfg.vocab_size, 64).tolist()
         dec = GreedyDecoder(fmodel, steps_per_graph=16, use_graph=True)
@@ -283,20 +285,20 @@ def main():
         avg_ctx = 64 + args.decode_gen / 2
         tok_bytes = wb["total"] + 2 * 2 * 1024 * avg_ctx * 28
         tok_s = (args.decode_gen - 1) / t_gen
-        extras["c3_decode"] = {"prompt": 64, "generated": len(toks), "tok_s": round(tok_s, 1),
+        extras["decode_28_layers"] = {"prompt": 64, "generated": len(toks), "tok_s": round(tok_s, 1),
                                "us_per_token": round(1e6 / tok_s, 2),
                                "serial_prefill_tok_s": round(64 / t_pre, 1),
                                "GBps_equiv": round(tok_bytes * tok_s / 1e9, 1),
                                "hbm_frac": round(tok_bytes * tok_s / 1e9 / HBM_PEAK_GBPS, 4),
                                "status": dec.status()}
-        log(f"[bench] C3 decode: {json.dumps(extras['c3_decode'])}")
+        log(f"[bench] 28-layer decode: {json.dumps(extras['decode_28_layers'])}")
         del dec, lws
         torch.cuda.empty_cache()
 
-    if "c4" in legs:
-        # -------------------------------------------------------- C4 prefill
+    if "prefill" in legs:
+        # -------------------------------------------------------- prefill of 2048 tokens
         from llm_accelerator_amd.decode import Prefill
-        T = C4_TOKENS
+        T = PREFILL_TOKENS
         pkv = M.KVCache(fcfg, fcfg.num_hidden_layers, 1, fmodel.max_ctx, dev)
         pf = Prefill(fmodel, pkv, T)
         ptok = torch.from_numpy(np.random.default_rng(4).integers(0, fcfg.vocab_size, T).astype(np.int32)).to(dev)
@@ -310,22 +312,22 @@ def main():
         torch.cuda.synchronize()
         pms = e0.elapsed_time(e1) / 5
         pflops = M.prefill_flops(fcfg, T)
-        extras["c4_prefill"] = {"tokens": T, "ms": round(pms, 3), "tok_s": round(T / pms * 1e3, 1),
+        extras["prefill_2048"] = {"tokens": T, "ms": round(pms, 3), "tok_s": round(T / pms * 1e3, 1),
                                 "TFLOPs": round(pflops / pms / 1e9, 1), "flops": pflops,
                                 "mfma_frac": round(pflops / pms / 1e9 / MFMA_PEAK_TFLOPS, 4)}
-        log(f"[bench] C4 prefill: {json.dumps(extras['c4_prefill'])}")
+        log(f"[bench] prefill 2048: {json.dumps(extras['prefill_2048'])}")
         del pkv, pf
         torch.cuda.empty_cache()
 
-    if "c5" in legs:
-        # -------------------------------------------------------- C5 batched decode
+    if "batch" in legs:
+        # -------------------------------------------------------- batched decode 64 x 4096
         from llm_accelerator_amd.decode import BatchedDecoder
-        B = C5_BATCH
-        bkv = M.KVCache(fcfg, fcfg.num_hidden_layers, B, C5_CTX + 1, dev)
-        bkv.data[..., :C5_CTX, :].normal_(generator=gen)
+        B = BATCH_SEQS
+        bkv = M.KVCache(fcfg, fcfg.num_hidden_layers, B, BATCH_CTX + 1, dev)
+        bkv.data[..., :BATCH_CTX, :].normal_(generator=gen)
         bd = BatchedDecoder(fmodel, B, bkv)
         btok = torch.from_numpy(np.random.default_rng(3).integers(0, fcfg.vocab_size, B).astype(np.int32)).to(dev)
-        bpos = torch.full((B,), C5_CTX, dtype=torch.int32, device=dev)
+        bpos = torch.full((B,), BATCH_CTX, dtype=torch.int32, device=dev)
         bd.step(btok, bpos)
         torch.cuda.synchronize()
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -335,13 +337,13 @@ def main():
         e1.record()
         torch.cuda.synchronize()
         bms = e0.elapsed_time(e1) / 5
-        bbytes = M.batched_step_bytes(fcfg, B, C5_CTX)
-        extras["c5_batched_decode"] = {"batch": B, "ctx": C5_CTX, "ms_per_step": round(bms, 3),
+        bbytes = M.batched_step_bytes(fcfg, B, BATCH_CTX)
+        extras["batched_decode_64x4096"] = {"batch": B, "ctx": BATCH_CTX, "ms_per_step": round(bms, 3),
                                        "tok_s": round(B / bms * 1e3, 1), "bytes_per_step": bbytes,
                                        "GBps": round(bbytes / bms / 1e6, 1),
                                        "hbm_frac": round(bbytes / bms / 1e6 / HBM_PEAK_GBPS, 4),
                                        "status": bd.status()}
-        log(f"[bench] C5 batched decode: {json.dumps(extras['c5_batched_decode'])}")
+        log(f"[bench] batched decode 64x4096: {json.dumps(extras['batched_decode_64x4096'])}")
         del bkv, bd
     if "fx" in legs:
         # -------------------------------------------------------- fixed-point (RTL-exact) decode
@@ -387,7 +389,7 @@ def main():
             "status": counts["status"]}
         log(f"[bench] fixed-point decode: {json.dumps(extras['fx_fixed_point'])}")
         del fxm, fkv, g_fx, g_tok
-    if legs & {"c3", "c4", "c5", "fx"}:
+    if legs & {"decode", "prefill", "batch", "fx"}:
         del fmodel
         torch.cuda.empty_cache()
     if "q4c" in legs:
@@ -476,7 +478,7 @@ def main():
             "warmup": args.warmup, "ms_per_step": round(ms_per_step, 6), "higher_is_better": True,
             "scaling": "weak", "vs_baseline": None, "dtype": "q4xf32",
             "data": "synthetic (seeded random-init Q4 weights, N(0,1) fp16 KV, N(0,1) hidden)",
-            "config": {"workload": "config 2: one Qwen3-0.6B decoder layer, one decode step at ctx 512, "
+            "config": {"workload": "one Qwen3-0.6B decoder layer, one decode step at ctx 512, "
                                    f"weights rotated over {copies} distinct layers (cache-flushed)",
                        "hidden": 1024, "q_heads": 16, "kv_heads": 8, "head_dim": 128, "intermediate": 3072,
                        "ctx": ctx, "batch": 1, "bytes_per_step": step_bytes, "activation_precision": args.precision},
@@ -530,10 +532,10 @@ def _median_time(fn, reps, budget_s):
 
 
 def cpu_extra_legs(ctx, step_bytes):
-    """The other CPU baselines: config 1 (fp32 matvec on pre-dequantised
+    """The other CPU baselines: the 3072x1024 GEMV (fp32 matvec on pre-dequantised
     weights as manual_linear_from_weight holds them, common.py:137-145, and the
     int64 Q26 restatement of compute_q4_gemv_q26, 28_export_mlp_gate_up_vectors.py:124-133),
-    the config-2 layer step on one thread, and config 3 (run_manual_one_token,
+    the layer step on one thread, and the 28-layer decode (run_manual_one_token,
     10_validate_full_run_one_token.py:17-56, 8 serial steps of the 28-layer
     model, per token).  Medians of >= 10 timed runs after a warm-up."""
     import numpy as np
@@ -553,9 +555,9 @@ def cpu_extra_legs(ctx, step_bytes):
     xi = rng.integers(-(1 << 20), 1 << 20, size=1024)
     gb = M.gemv_bytes(3072, 1024)
     t, n = _median_time(lambda: W @ x, 10, 2.0)
-    out["c1_fp32"] = {"us": round(t * 1e6, 1), "GBps": round(gb / t / 1e9, 2), "runs": n}
+    out["gemv_fp32"] = {"us": round(t * 1e6, 1), "GBps": round(gb / t / 1e9, 2), "runs": n}
     t, n = _median_time(lambda: o.q4_gemv_q26(xi, q, scale), 10, 2.0)
-    out["c1_int64_q26"] = {"us": round(t * 1e6, 1), "GBps": round(gb / t / 1e9, 3), "runs": n}
+    out["gemv_int64_q26"] = {"us": round(t * 1e6, 1), "GBps": round(gb / t / 1e9, 3), "runs": n}
     if threadpool_limits is not None:
         cfg = M.Qwen3Config(num_hidden_layers=1, vocab_size=2048)
         host = M.random_host_weights(cfg, seed=0, num_layers=1)
@@ -568,7 +570,7 @@ def cpu_extra_legs(ctx, step_bytes):
         with threadpool_limits(limits=1):
             t, n = _median_time(lambda: o.manual_decoder_layer_cached(h, om.layers[0], om.config, om.inv_freq,
                                                                       pos, k, v), 10, 3.0)
-        out["c2_one_thread"] = {"ms_per_step": round(t * 1e3, 3), "GBps": round(step_bytes / t / 1e9, 3),
+        out["layer_one_thread"] = {"ms_per_step": round(t * 1e3, 3), "GBps": round(step_bytes / t / 1e9, 3),
                                 "runs": n}
     fcfg = M.Qwen3Config()
     fhost = M.random_host_weights(fcfg, seed=0)
@@ -582,7 +584,7 @@ def cpu_extra_legs(ctx, step_bytes):
         o.run_manual_one_token(np.array([[int(tk)]]), p, om, kc, vc)
         ts.append(time.perf_counter() - t0)
     tt = sorted(ts[1:])[len(ts[1:]) // 2]
-    out["c3_per_token"] = {"ms": round(tt * 1e3, 1), "tok_s": round(1.0 / tt, 2), "steps": len(ts),
+    out["decode_per_token"] = {"ms": round(tt * 1e3, 1), "tok_s": round(1.0 / tt, 2), "steps": len(ts),
                            "note": "median of steps 1-7 at positions 1-7 (the first step is the warm-up)"}
     wq = (rng.standard_normal((3072, 1024)) * 0.03).astype(np.float32)
     t, n = _median_time(lambda: o.quantize_weight_q4(wq), 5, 2.0)

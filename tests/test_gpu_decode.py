@@ -1,4 +1,4 @@
-"""Full 28-layer Qwen3-0.6B-Q4 greedy decode (shortened)
+"""Full 28-layer Qwen3-0.6B-Q4 greedy decode (64-token prompt and 256 generated, shortened here)
 on the GPU vs the oracle restatement of run_manual_one_token
 (10_validate_full_run_one_token.py:17-56, feedback loop :81-172).
 
@@ -75,7 +75,7 @@ def test_teacher_forced_argmax_and_logits(full):
             assert gap <= explained, (gen_step, gap, explained)
             near_ties.append((gen_step, a_ref, a_gpu, float(gap)))
     hist, _ = dec.history()
-    print(f"[C3 teacher-forced] steps={GEN} max rel logit err={worst:.3e} near_ties={near_ties}", flush=True)
+    print(f"[28-layer decode teacher-forced] steps={GEN} max rel logit err={worst:.3e} near_ties={near_ties}", flush=True)
     assert worst < 5e-3
     assert dec.status() == 0
 
@@ -90,7 +90,7 @@ def test_free_running_graph_matches_oracle(full):
     assert len(gen) == GEN
     first_diff = next((i for i, (a, b) in enumerate(zip(gen, ref_tokens)) if a != b), None)
     gaps = [o.top2_gap(r) for r in ref_logits]
-    print(f"[C3 free-running] identical={first_diff is None} first_diff={first_diff} "
+    print(f"[28-layer decode free-running] identical={first_diff is None} first_diff={first_diff} "
           f"min_gap={min(gaps):.3e}", flush=True)
     if first_diff is not None:
         # divergence must start at a near-tie of the oracle trajectory

@@ -52,7 +52,7 @@ def test_reference_fixture_fp32_activation(dev, golden, name):
 
 
 def test_gate_proj_fixture_fp16_activation(dev, golden):
-    """C1 shape, fp16 activation: matches the oracle on the fp16-rounded x."""
+    """3072x1024 benchmark shape, fp16 activation: matches the oracle on the fp16-rounded x."""
     d = golden("mlp_gate_proj_real")
     x16 = (d["activation"].astype(np.float64) / 4096.0).astype(np.float16)
     y = linear(q4(d["weight_packed"], d["scale_q2_14"], dev), torch.from_numpy(x16).to(dev)[None],
@@ -64,7 +64,7 @@ def test_gate_proj_fixture_fp16_activation(dev, golden):
 
 
 def test_c1_synthetic_fp16_in_fp16_out(dev):
-    """W 3072x1024 Q4 random, x fp16 ~ N(0,1), y fp16."""
+    """The benchmark GEMV: W 3072x1024 Q4 random, x fp16 ~ N(0,1), y fp16."""
     from llm_accelerator_amd.model import random_q4
     rng = np.random.default_rng(0)
     packed, scale = random_q4(rng, 3072, 1024)
@@ -72,7 +72,7 @@ def test_c1_synthetic_fp16_in_fp16_out(dev):
     y = linear(q4(packed, scale, dev), torch.from_numpy(x16).to(dev)[None], Q4D_F16)[0].float().cpu().numpy()
     W = o.dequantize_q4(packed, scale, dtype=np.float64)
     ref = W @ x16.astype(np.float64)
-    report("C1 fp16", y, ref)
+    report("gemv 3072x1024 fp16", y, ref)
     ulp_half = np.abs(ref) * 2.0 ** -11 + 2.0 ** -25
     assert np.all(np.abs(y - ref) <= ulp_half + ACC * abs_dot_bound(W, x16))
 

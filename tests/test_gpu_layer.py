@@ -1,4 +1,4 @@
-"""One decoder layer and the primitive ops on the GPU vs
+"""One decoder layer (one decode step at context 512) and the primitive ops on the GPU vs
 the oracle restatement of common.py:129-298.
 
 Config 2: hidden 1024, 16 q / 8 kv heads, head_dim 128, intermediate 3072,

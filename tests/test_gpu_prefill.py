@@ -1,4 +1,4 @@
-"""Prefill (many tokens of one sequence per call, BASELINE config 4 at small
+"""Prefill (many tokens of one sequence per call, 2048 tokens in the benchmark, small
 size) on the GPU vs the oracle's serial run_manual_one_token loop
 (10_validate_full_run_one_token.py:17-56, driven one token at a time as in
 :81-135).
