@@ -742,6 +742,7 @@ int q4d_prefill(const q4d_model_t* model, const int32_t* tokens, int32_t n_token
     g.seg_end[0] = H; g.nseg = 1;
     g.N = H; g.K = qh * d; g.M = n;
     g.x = ws_ptr<uint16_t>(ws, P.attn); g.y = hidden; g.ldy = H; g.resid = hidden;
+    g.part = ws_ptr<float>(ws, P.part); g.part_cap = (size_t)kPrefillSplit * n * H; g.ksplit = kPrefillSplit;
     if ((rc = launch_gemm(g, EP_RESID, false, st))) return rc;
     if ((rc = launch_rms_norm(hidden, L.post_attention_layernorm, model->rms_norm_eps, n, H, xh, Q4D_F16, st)))
       return rc;
@@ -757,6 +758,7 @@ int q4d_prefill(const q4d_model_t* model, const int32_t* tokens, int32_t n_token
     g.seg_end[0] = H; g.nseg = 1;
     g.N = H; g.K = I; g.M = n;
     g.x = act; g.y = hidden; g.ldy = H; g.resid = hidden;
+    g.part = ws_ptr<float>(ws, P.part); g.part_cap = (size_t)kPrefillSplit * n * H; g.ksplit = kPrefillSplit;
     if ((rc = launch_gemm(g, EP_RESID, false, st))) return rc;
   }
   // final RMSNorm + LM head + argmax for the last token

@@ -284,6 +284,10 @@ int launch_prefill_attention(const PrefillArgs& a, hipStream_t st);
 
 // Prefill workspace: the single-token layout (status, counters, LM-head argmax)
 // followed by the per-token buffers.
+// K splits of the prefill o_proj / down GEMMs (N = hidden gives too few output tiles to
+// keep two blocks on every CU); fixed, so a row's sums do not depend on the token count.
+constexpr int kPrefillSplit = 2;
+
 struct PrefillLayout {
   WsLayout base;
   size_t hidden;  // f32 [n][hidden]
@@ -292,6 +296,7 @@ struct PrefillLayout {
   size_t q16;     // f16 [qh][n][d]
   size_t attn;    // f16 [n][qh * d]
   size_t act;     // f16 [n][intermediate]
+  size_t part;    // f32 [2][n][hidden]: split-K partials of the o_proj / down GEMMs
   size_t total;
 };
 
@@ -308,6 +313,7 @@ inline PrefillLayout prefill_layout(const q4d_model_t* m, int n) {
   P.q16 = o;    o = align_up(o + (size_t)qh * n * d * 2, A);
   P.attn = o;   o = align_up(o + (size_t)n * qh * d * 2, A);
   P.act = o;    o = align_up(o + (size_t)n * m->intermediate_size * 2, A);
+  P.part = o;   o = align_up(o + (size_t)kPrefillSplit * n * m->hidden_size * 4, A);
   P.total = o;
   return P;
 }

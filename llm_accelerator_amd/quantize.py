@@ -121,40 +121,35 @@ def check_checkpoint(names_shapes: dict, cfg: Qwen3Config) -> None:
 
 def convert_checkpoint(path: str | Path, cfg: Qwen3Config | None = None, device="cuda") -> tuple:
     """(cfg, host weights) from a Hugging Face Qwen3 checkpoint, Q4 on ``device``'s kernel."""
+    from contextlib import ExitStack
+
     from safetensors import safe_open
     p = Path(path)
     if cfg is None:
         cfg = Qwen3Config.from_json((p if p.is_dir() else p.parent) / "config.json")
-    files = checkpoint_files(p)
-    where, shapes = {}, {}
-    for f in files:
-        with safe_open(str(f), framework="pt", device="cpu") as h:
+    with ExitStack() as stack:
+        handles = [stack.enter_context(safe_open(str(f), framework="pt", device="cpu")) for f in checkpoint_files(p)]
+        where, shapes = {}, {}
+        for h in handles:
             for name in h.keys():
-                where[name] = f
+                where[name] = h
                 shapes[name] = tuple(h.get_slice(name).get_shape())
-    check_checkpoint(shapes, cfg)
-    handles = {}
+        check_checkpoint(shapes, cfg)
 
-    def get(name):
-        f = where[name]
-        if f not in handles:
-            handles[f] = safe_open(str(f), framework="pt", device="cpu")
-        return handles[f].get_tensor(name)
+        def q4(name):
+            packed, scale, _ = quantize_weight_q4(where[name].get_tensor(name).to(device), return_codes=False)
+            return packed.cpu().numpy(), scale.cpu().numpy()
 
-    def q4(name):
-        packed, scale, _ = quantize_weight_q4(get(name).to(device), return_codes=False)
-        return packed.cpu().numpy(), scale.cpu().numpy()
+        def vec(name):
+            return where[name].get_tensor(name).float().numpy().astype(np.float32)
 
-    def vec(name):
-        return get(name).float().numpy().astype(np.float32)
-
-    layers = []
-    for li in range(cfg.num_hidden_layers):
-        pre = f"model.layers.{li}."
-        L = {k: q4(pre + v + ".weight") for k, v in _LAYER_MATS.items()}
-        L.update({k: vec(pre + v + ".weight") for k, v in _LAYER_VECS.items()})
-        layers.append(L)
-    host = {"layers": layers, "embed_tokens": q4("model.embed_tokens.weight"), "norm": vec("model.norm.weight")}
+        layers = []
+        for li in range(cfg.num_hidden_layers):
+            pre = f"model.layers.{li}."
+            L = {k: q4(pre + v + ".weight") for k, v in _LAYER_MATS.items()}
+            L.update({k: vec(pre + v + ".weight") for k, v in _LAYER_VECS.items()})
+            layers.append(L)
+        host = {"layers": layers, "embed_tokens": q4("model.embed_tokens.weight"), "norm": vec("model.norm.weight")}
     return cfg, host
 
 
