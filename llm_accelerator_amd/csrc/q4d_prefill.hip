@@ -24,8 +24,8 @@
 //   query), so P never leaves registers.  V is transposed into LDS as it is
 //   staged: each thread loads a 4-key x 8-dim block, transposes it in
 //   registers and writes 8-byte rows of V^T.
-// Row strides of the LDS tiles (136 and 72 fp16) put every LDS access at
-// its minimum number of bank passes.
+// Row strides of the LDS tiles: 136 and 68 fp16 (measured best of the 16-byte /
+// 8-byte aligned choices; SQ_LDS_BANK_CONFLICT fell with the row-contiguous K stores).
 #include <math.h>
 
 #include "q4d_device.h"
@@ -41,8 +41,8 @@ typedef _Float16 h4 __attribute__((ext_vector_type(4)));
 constexpr int kD = 128;
 constexpr int kBQ = 64;   // queries per block
 constexpr int kBK = 64;   // keys per tile
-constexpr int kLdk = kD + 8;    // fp16 row stride of the K tile
-constexpr int kLdv = kBK + 8;   // fp16 row stride of the V^T tile
+constexpr int kLdk = kD + 8;   // fp16 row stride of the K tile
+constexpr int kLdv = kBK + 4;  // fp16 row stride of the V^T tile (+4 beat +8, +12 and +16 when measured)
 
 __device__ __forceinline__ float wave_sum_bcast(float v) {
   return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wave_sum_dpp(v)), 63));
@@ -85,8 +85,10 @@ __global__ __launch_bounds__(256) void prefill_rope_kernel(const PrefillArgs a) 
   }
 }
 
-// Global loads of one K/V tile: thread (kq = t & 15, dc = t >> 4) holds keys
-// 4kq .. 4kq+3, dims 8dc .. 8dc+7 of K and of V.
+// Global loads of one K/V tile.  K: thread (kr = t >> 4, kc = t & 15) holds dims
+// 8kc .. 8kc+7 of keys kr + 16b, so 16 lanes store one whole 256-byte K row and the
+// LDS stores meet every bank once.  V: thread (kq = t & 15, dc = t >> 4) holds keys
+// 4kq .. 4kq+3, dims 8dc .. 8dc+7, the 4 x 8 block it transposes into V^T.
 struct KVRegs {
   u32x4 k[4], v[4];
 };
@@ -96,9 +98,11 @@ __device__ __forceinline__ void load_kv(const uint16_t* kb, const uint16_t* vb, 
   const int kq = t & 15, dc = t >> 4;
 #pragma unroll
   for (int b = 0; b < 4; ++b) {
+    int kk = key0 + dc + 16 * b;        // K row of piece b (dc doubles as the row index kr)
+    kk = kk < kend ? kk : kend - 1;     // rows past the end are masked out of the softmax
+    R.k[b] = *reinterpret_cast<const u32x4*>(kb + (size_t)kk * kD + kq * 8);
     int key = key0 + 4 * kq + b;
-    key = key < kend ? key : kend - 1;  // rows past the end are masked out of the softmax
-    R.k[b] = *reinterpret_cast<const u32x4*>(kb + (size_t)key * kD + dc * 8);
+    key = key < kend ? key : kend - 1;
     R.v[b] = *reinterpret_cast<const u32x4*>(vb + (size_t)key * kD + dc * 8);
   }
 }
@@ -106,7 +110,7 @@ __device__ __forceinline__ void load_kv(const uint16_t* kb, const uint16_t* vb, 
 __device__ __forceinline__ void store_kv(const KVRegs& R, int t, _Float16 (*Ks)[kLdk], _Float16 (*Vt)[kLdv]) {
   const int kq = t & 15, dc = t >> 4;
 #pragma unroll
-  for (int b = 0; b < 4; ++b) *reinterpret_cast<u32x4*>(&Ks[4 * kq + b][dc * 8]) = R.k[b];
+  for (int b = 0; b < 4; ++b) *reinterpret_cast<u32x4*>(&Ks[dc + 16 * b][kq * 8]) = R.k[b];
   // transpose the 4-key x 8-dim block: dim e of keys 4kq..4kq+3 -> one 8-byte row piece
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
