@@ -701,8 +701,10 @@ int q4d_prefill(const q4d_model_t* model, const int32_t* tokens, int32_t n_token
   const size_t seq_off = (size_t)seq * kvh * kv->max_ctx * d;
   for (int l = 0; l < model->num_layers; ++l) {
     const q4d_layer_t& L = model->layers[l];
-    // input RMSNorm -> fp16, then q|k|v as one three-segment GEMM
-    if ((rc = launch_rms_norm(hidden, L.input_layernorm, model->rms_norm_eps, n, H, xh, Q4D_F16, st))) return rc;
+    // input RMSNorm -> fp16 (layers after the first get it from the previous down GEMM's
+    // fused reduction), then q|k|v as one three-segment GEMM
+    if (l == 0 && (rc = launch_rms_norm(hidden, L.input_layernorm, model->rms_norm_eps, n, H, xh, Q4D_F16, st)))
+      return rc;
     GemmArgs g;
     memset(&g, 0, sizeof(g));
     g.w[0] = L.q_proj.w; g.s[0] = L.q_proj.s;
@@ -743,8 +745,10 @@ int q4d_prefill(const q4d_model_t* model, const int32_t* tokens, int32_t n_token
     g.N = H; g.K = qh * d; g.M = n;
     g.x = ws_ptr<uint16_t>(ws, P.attn); g.y = hidden; g.ldy = H; g.resid = hidden;
     g.part = ws_ptr<float>(ws, P.part); g.part_cap = (size_t)kPrefillSplit * n * H; g.ksplit = kPrefillSplit;
+    g.defer_reduce = 1;  // split sums + residual + post-attention RMSNorm in one pass
     if ((rc = launch_gemm(g, EP_RESID, false, st))) return rc;
-    if ((rc = launch_rms_norm(hidden, L.post_attention_layernorm, model->rms_norm_eps, n, H, xh, Q4D_F16, st)))
+    if ((rc = launch_splitk_resid_norm(g, kPrefillSplit, L.post_attention_layernorm, model->rms_norm_eps,
+                                       xh, st)))
       return rc;
     memset(&g, 0, sizeof(g));
     g.w[0] = L.gate_proj.w; g.s[0] = L.gate_proj.s;
@@ -759,7 +763,15 @@ int q4d_prefill(const q4d_model_t* model, const int32_t* tokens, int32_t n_token
     g.N = H; g.K = I; g.M = n;
     g.x = act; g.y = hidden; g.ldy = H; g.resid = hidden;
     g.part = ws_ptr<float>(ws, P.part); g.part_cap = (size_t)kPrefillSplit * n * H; g.ksplit = kPrefillSplit;
-    if ((rc = launch_gemm(g, EP_RESID, false, st))) return rc;
+    if (l + 1 < model->num_layers) {  // split sums + residual + the next layer's input RMSNorm
+      g.defer_reduce = 1;
+      if ((rc = launch_gemm(g, EP_RESID, false, st))) return rc;
+      if ((rc = launch_splitk_resid_norm(g, kPrefillSplit, model->layers[l + 1].input_layernorm,
+                                         model->rms_norm_eps, xh, st)))
+        return rc;
+    } else if ((rc = launch_gemm(g, EP_RESID, false, st))) {
+      return rc;
+    }
   }
   // final RMSNorm + LM head + argmax for the last token
   return run_lm_head(model, hidden + (size_t)(n - 1) * H, next_token, score, logits, ws, P.base, st);

@@ -350,6 +350,57 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const GemmArgs a, in
   }
 }
 
+// Split-K sum + residual fused with the next RMSNorm: one 256-thread block per row, up to
+// four f32x4 of the row per thread.
+__global__ __launch_bounds__(256) void splitk_resid_norm_kernel(const GemmArgs a, int ksplit, const float* gamma,
+                                                                float eps, _Float16* xn) {
+  __shared__ float sred[4];
+  const int m = blockIdx.x, t = threadIdx.x, lane = t & 63, wid = t >> 6;
+  const int nv = a.N / 4;  // f32x4 of the row
+  f32x4 y[4];
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int n = 4 * (t + 256 * i);
+    y[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+    if (t + 256 * i < nv) {
+      f32x4 v = f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int z = 0; z < ksplit; ++z) v += *reinterpret_cast<const f32x4*>(a.part + ((size_t)z * a.M + m) * a.N + n);
+      const size_t o = (size_t)m * a.ldy + n;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) y[i][e] = a.resid[o + e] + v[e];
+      *reinterpret_cast<f32x4*>(static_cast<float*>(a.y) + o) = y[i];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) ss = fmaf(y[i][e], y[i][e], ss);
+    }
+  }
+  ss = wave_sum(ss);
+  if (lane == 0) sred[wid] = ss;
+  __syncthreads();
+  const float inv = 1.0f / sqrtf(((sred[0] + sred[1]) + (sred[2] + sred[3])) / (float)a.N + eps);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int n = 4 * (t + 256 * i);
+    if (t + 256 * i < nv) {
+      h2 lo = make_h2((_Float16)((y[i][0] * inv) * gamma[n]), (_Float16)((y[i][1] * inv) * gamma[n + 1]));
+      h2 hi = make_h2((_Float16)((y[i][2] * inv) * gamma[n + 2]), (_Float16)((y[i][3] * inv) * gamma[n + 3]));
+      *reinterpret_cast<u32x2*>(xn + (size_t)m * a.N + n) = u32x2{__builtin_bit_cast(uint32_t, lo),
+                                                                 __builtin_bit_cast(uint32_t, hi)};
+    }
+  }
+}
+
+int launch_splitk_resid_norm(const GemmArgs& a, int ksplit, const float* gamma, float eps, uint16_t* xn,
+                             hipStream_t st) {
+  if (!a.part || !a.resid || !a.y || !gamma || !xn) return Q4D_ERR_NULL;
+  if (a.N % 4 || a.N > 4096 || a.M <= 0 || ksplit < 1 || (size_t)ksplit * a.M * a.N > a.part_cap) return Q4D_ERR_SHAPE;
+  if (a.ldy % 4 || !aligned(a.y, 16) || !aligned(a.resid, 16) || !aligned(xn, 8) || !aligned(a.part, 16))
+    return Q4D_ERR_BAD_ADDR;
+  hipLaunchKernelGGL(splitk_resid_norm_kernel, dim3(a.M), dim3(256), 0, st, a, ksplit, gamma, eps,
+                     reinterpret_cast<_Float16*>(xn));
+  return check_launch();
+}
+
 // Row-wise reduction of the argmax partials: one wave per activation row.
 __global__ __launch_bounds__(64) void argmax_rows_kernel(const float* part_score, const int* part_idx, int nparts,
                                                          int M, int32_t* out_token, float* out_score) {
@@ -405,7 +456,7 @@ static int launch_gemm_inst(const GemmArgs& a, hipStream_t st) {
   constexpr int NW = BM == 128 ? kGemmWaves128 : kGemmWaves64;
   hipLaunchKernelGGL((q4_gemm_kernel<BM, EP, PAIR, NW>), dim3(nblk, mblk, ks), dim3(NW * 64), 0, st, a);
   int rc = check_launch();
-  if (rc || ks == 1) return rc;
+  if (rc || ks == 1 || a.defer_reduce) return rc;
   if constexpr (EP != EP_ARGMAX) {
     const int n4 = a.M * (a.N / 4);
     hipLaunchKernelGGL((splitk_reduce_kernel<EP, PAIR>), dim3((n4 + 255) / 256), dim3(256), 0, st, a, ks);

@@ -217,9 +217,15 @@ struct GemmArgs {
   float* part;
   size_t part_cap;
   int ksplit;
+  int defer_reduce;  // with a split, leave the partials for launch_splitk_resid_norm
 };
 constexpr int kGemmMaxSplit = 16;
 int launch_gemm(const GemmArgs& a, int ep, bool pair, hipStream_t st);
+// The deferred reduction of an EP_RESID split GEMM fused with the RMSNorm that follows it:
+// y = resid + sum_z part[z] (fp32, in order of z), then xn = fp16(y * rsqrt(mean(y^2) + eps)
+// * gamma) per row.  N % 4 == 0, N <= 4096.
+int launch_splitk_resid_norm(const GemmArgs& a, int ksplit, const float* gamma, float eps, uint16_t* xn,
+                             hipStream_t st);
 int launch_argmax_rows(const float* part_score, const int* part_idx, int nparts, int M, int32_t* out_token,
                        float* out_score, hipStream_t st);
 
