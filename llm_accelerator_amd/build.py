@@ -34,6 +34,13 @@ HIPCC_FLAGS = [
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
 ]
 
+# Per-source additions.  The prefill attention kernel rescales and reads its MFMA
+# accumulators with VALU code every key tile; MFMA results kept in VGPRs avoid the
+# accumulator-register copies the default form adds around that code.
+SOURCE_FLAGS = {
+    "q4d_prefill.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
+}
+
 
 def hipcc() -> str:
     exe = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
@@ -44,7 +51,7 @@ def hipcc() -> str:
 
 def _compile(src: Path) -> Path:
     obj = BUILD / (src.stem + ".o")
-    cmd = [hipcc(), *HIPCC_FLAGS, "-c", str(src), "-o", str(obj)]
+    cmd = [hipcc(), *HIPCC_FLAGS, *SOURCE_FLAGS.get(src.name, []), "-c", str(src), "-o", str(obj)]
     r = subprocess.run(cmd, capture_output=True, text=True)
     # hipcc's host pass warns that it does not know the packed-fp32 feature
     err = "\n".join(l for l in r.stderr.splitlines() if "packed-fp32-ops" not in l)

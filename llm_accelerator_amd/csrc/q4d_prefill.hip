@@ -43,6 +43,7 @@ constexpr int kBQ = 64;   // queries per block
 constexpr int kBK = 64;   // keys per tile
 constexpr int kLdk = kD + 8;   // fp16 row stride of the K tile
 constexpr int kLdv = kBK + 4;  // fp16 row stride of the V^T tile (+4 beat +8, +12 and +16 when measured)
+constexpr float kRescale = 8.0f;  // log2 headroom of the lazily moved running max
 
 __device__ __forceinline__ float wave_sum_bcast(float v) {
   return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wave_sum_dpp(v)), 63));
@@ -174,36 +175,47 @@ __global__ __launch_bounds__(256) void prefill_attn_kernel(const PrefillArgs a) 
         st[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kop, qop[s], st[mt], 0, 0, 0);
       }
     }
-    // causal / range mask: lane holds keys kt*64 + 16mt + 4qq + i for query my_pos
+    // causal / range mask: lane holds keys kt*64 + 16mt + 4qq + i for query my_pos.  Only
+    // a tile that reaches past the wave's first query or past kend needs it.
     const int kbase = kt * kBK + 4 * qq;
+    if (kt * kBK + kBK - 1 > a.p0 + q_lo || kt * kBK + kBK > kend) {
+#pragma unroll
+      for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int key = kbase + 16 * mt + i;
+          if (key > my_pos || key >= kend) st[mt][i] = -INFINITY;
+        }
+    }
     float tmax = -INFINITY;
 #pragma unroll
-    for (int mt = 0; mt < 4; ++mt)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int key = kbase + 16 * mt + i;
-        if (key > my_pos || key >= kend) st[mt][i] = -INFINITY;
-        tmax = fmaxf(tmax, st[mt][i]);
-      }
+    for (int mt = 0; mt < 4; ++mt) tmax = fmaxf(tmax, fmaxf(fmaxf(st[mt][0], st[mt][1]), fmaxf(st[mt][2], st[mt][3])));
     tmax = fmaxf(tmax, __shfl_xor(tmax, 16, kWave));
     tmax = fmaxf(tmax, __shfl_xor(tmax, 32, kWave));
-    const float m_new = fmaxf(m_run, tmax);
-    // m_new is finite once the query has seen key 0 (always in the first tile)
-    const float alpha = exp2f(m_run - m_new);
-    m_run = m_new;
+    // Lazy rescaling: the running max moves only when a score exceeds it by more than
+    // kRescale (log2 units), so P = 2^(s - m_run) stays below 2^kRescale (far inside fp16's
+    // range) and the O / l rescale is skipped for the wave unless some query needs it.
+    // The first tile always moves it (m_run = -inf; key 0 is visible to every query).
+    const bool move = tmax > m_run + kRescale;
+    if (__builtin_amdgcn_ballot_w64(move)) {
+      const float m_new = move ? tmax : m_run;
+      const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+      m_run = m_new;
+      l_run *= alpha;
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt) o[dt] *= alpha;
+    }
     float psum = 0.f;
     h4 p[4];
 #pragma unroll
     for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const float e = exp2f(st[mt][i] - m_new);
+        const float e = __builtin_amdgcn_exp2f(st[mt][i] - m_run);
         psum += e;
         p[mt][i] = (_Float16)e;
       }
-    l_run = l_run * alpha + psum;
-#pragma unroll
-    for (int dt = 0; dt < 8; ++dt) o[dt] *= alpha;
+    l_run += psum;
     // O^T += V^T . P^T over two 32-key steps
 #pragma unroll
     for (int s2 = 0; s2 < 2; ++s2) {
