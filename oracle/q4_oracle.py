@@ -32,6 +32,7 @@ __all__ = [
     "manual_repeat_kv", "softmax", "silu", "manual_cached_attention",
     "OracleConfig", "OracleLayer", "OracleModel", "manual_decoder_layer_cached",
     "embed_tokens", "final_logits", "run_manual_one_token", "greedy_decode",
+    "serial_prompt_all_at_once",
     "top2_gap",
 ]
 
@@ -62,19 +63,28 @@ def pack_signed_int4(q: np.ndarray) -> np.ndarray:
     return (nib[:, 0::2] | (nib[:, 1::2] << 4)).astype(np.uint8)
 
 
-def unpack_signed_int4(packed: np.ndarray, k: int) -> np.ndarray:
-    """Inverse of :func:`pack_signed_int4`: nibble n -> n - 16 if n >= 8.
+def _nibble_pair_table() -> np.ndarray:
+    """[256, 2] int8: byte b -> (low nibble, high nibble), each n -> n - 16 if n >= 8."""
+    b = np.arange(256, dtype=np.int16)
+    pair = np.stack([b & 0x0F, (b >> 4) & 0x0F], axis=1)
+    pair[pair >= 8] -= 16
+    return pair.astype(np.int8)
 
-    Follows ``pem/13_export_q4_gemv_vectors.py:83-98``.
+
+_NIBBLE_PAIRS = _nibble_pair_table()
+
+
+def unpack_signed_int4(packed: np.ndarray, k: int) -> np.ndarray:
+    """Inverse of :func:`pack_signed_int4`: nibble n -> n - 16 if n >= 8, even
+    column from the low nibble.
+
+    Follows ``pem/13_export_q4_gemv_vectors.py:83-98`` (evaluated through a
+    256-entry byte table, which holds the same rule for every byte value).
     """
     packed = np.asarray(packed, dtype=np.uint8)
     if k % 2 or packed.shape[-1] != k // 2:
         raise ValueError(f"packed width {packed.shape[-1]} does not hold {k} int4 values")
-    out = np.empty(packed.shape[:-1] + (k,), dtype=np.int16)
-    out[..., 0::2] = packed & 0x0F
-    out[..., 1::2] = (packed >> 4) & 0x0F
-    out[out >= 8] -= 16
-    return out.astype(np.int8)
+    return _NIBBLE_PAIRS[packed].reshape(packed.shape[:-1] + (k,))
 
 
 def scale_q2_14_from_float(raw_scale: np.ndarray, nonzero: np.ndarray | None = None) -> np.ndarray:
@@ -123,9 +133,12 @@ def dequantize_q4(packed: np.ndarray, scale: np.ndarray, dtype=np.float32) -> np
     """
     packed = np.asarray(packed, dtype=np.uint8)
     k = packed.shape[-1] * 2
-    q = unpack_signed_int4(packed, k).astype(dtype)
+    q = unpack_signed_int4(packed, k)
     s = np.asarray(scale).astype(dtype) / dtype(1 << SCALE_FRAC)
-    return (q.reshape(q.shape[:-1] + (k // GROUP_SIZE, GROUP_SIZE)) * s[..., None]).reshape(q.shape)
+    out = np.empty(q.shape, dtype=dtype)
+    np.multiply(q.reshape(q.shape[:-1] + (k // GROUP_SIZE, GROUP_SIZE)), s[..., None],
+                out=out.reshape(q.shape[:-1] + (k // GROUP_SIZE, GROUP_SIZE)), dtype=dtype)
+    return out
 
 
 def words32_to_packed_bytes(words: np.ndarray, k: int) -> np.ndarray:
@@ -490,6 +503,68 @@ def run_manual_one_token(current_token_ids: np.ndarray, position: int | np.ndarr
     return logits, next_token
 
 
+def serial_prompt_all_at_once(model: OracleModel, token_ids: Sequence[int], kv_store_dtype=None,
+                              last_only: bool = False, _future_offset: int = 1):
+    """The serial prompt loop (``pem/10_validate_full_run_one_token.py:81-135``:
+    ``run_manual_one_token`` at positions 0 .. n-1 on an empty cache) evaluated for
+    all n positions at once, for prompts too long for the one-token loop.
+
+    At step i every layer appends token i's K/V row and attends over rows 0..i, and
+    those rows hold tokens 0..i's K/V, each computed by the same layer from its own
+    hidden state; no row of a later token exists yet.  So per layer, computing every
+    token's q/k/v first and masking keys j > i gives the serial loop's numbers up to
+    the order of floating-point sums.  Each stage is the one of
+    ``manual_decoder_layer_cached`` (``pem/common.py:231-298``) with the batch axis
+    used for the n positions.
+
+    Returns ``(logits [n, vocab] of every position (``last_only``: [1, vocab] of the
+    last), k_caches, v_caches)``; caches are [1, kv_heads, n, head_dim] per layer, as
+    the serial loop leaves them.
+    ``_future_offset`` exists for the tests that plant a wrong mask (0: a query misses
+    its own key; 2: it sees the next one); the default 1 masks exactly keys j > i.
+    """
+    cfg = model.config
+    dt = model.dtype
+    n = len(token_ids)
+    nq, nkv, hd, eps = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim, cfg.rms_norm_eps
+    hidden = embed_tokens(model, np.asarray(token_ids, dtype=np.int64).reshape(n, 1))   # [n, 1, H]
+    cos, sin = manual_rope_cos_sin(model.inv_freq, np.arange(n).reshape(n, 1))       # [n, 1, D]
+    cos, sin = cos.astype(dt), sin.astype(dt)
+    future = np.triu(np.ones((n, n), dtype=bool), k=_future_offset)                    # key j > query i
+    k_caches, v_caches = [], []
+    for layer in model.layers:
+        residual = hidden
+        xn = manual_rms_norm(hidden, layer.input_layernorm, eps, dt)
+        q = manual_linear_from_weight(xn, layer.q_proj, dtype=dt).reshape(n, 1, nq, hd)
+        k = manual_linear_from_weight(xn, layer.k_proj, dtype=dt).reshape(n, 1, nkv, hd)
+        v = manual_linear_from_weight(xn, layer.v_proj, dtype=dt).reshape(n, 1, nkv, hd)
+        qn = np.swapaxes(manual_rms_norm(q, layer.q_norm, eps, dt), 1, 2)              # [n, nq, 1, D]
+        kn = np.swapaxes(manual_rms_norm(k, layer.k_norm, eps, dt), 1, 2)
+        q_rope, k_rope = manual_apply_rope(qn, kn, cos, sin)
+        v_rows = np.swapaxes(v, 1, 2)
+        if kv_store_dtype is not None:
+            k_rope = k_rope.astype(kv_store_dtype).astype(dt)
+            v_rows = v_rows.astype(kv_store_dtype).astype(dt)
+        kc = np.swapaxes(k_rope[:, :, 0, :], 0, 1)[None]                                # [1, nkv, n, D]
+        vc = np.swapaxes(v_rows[:, :, 0, :], 0, 1)[None]
+        k_caches.append(kc)
+        v_caches.append(vc)
+        k_rep = manual_repeat_kv(kc, cfg.kv_repeat)[0]                                  # [nq, n, D]
+        v_rep = manual_repeat_kv(vc, cfg.kv_repeat)[0]
+        qh = np.swapaxes(q_rope[:, :, 0, :], 0, 1).astype(dt)                           # [nq, n, D]
+        scores = (qh @ np.swapaxes(k_rep, 1, 2)) * dt(cfg.scaling)                      # [nq, n(q), n(k)]
+        scores[:, future] = -np.inf
+        w = softmax(scores.astype(dt), axis=-1).astype(dt)
+        attn = np.swapaxes(w @ v_rep, 0, 1).reshape(n, 1, nq * hd).astype(dt)           # [n, 1, nq*D]
+        after_attention = (residual + manual_linear_from_weight(attn, layer.o_proj, dtype=dt)).astype(dt)
+        post = manual_rms_norm(after_attention, layer.post_attention_layernorm, eps, dt)
+        gate = manual_linear_from_weight(post, layer.gate_proj, dtype=dt)
+        up = manual_linear_from_weight(post, layer.up_proj, dtype=dt)
+        down = manual_linear_from_weight((silu(gate) * up).astype(dt), layer.down_proj, dtype=dt)
+        hidden = (after_attention + down).astype(dt)
+    return final_logits(model, hidden[-1:] if last_only else hidden)[:, 0], k_caches, v_caches
+
+
 def top2_gap(logits_row: np.ndarray) -> float:
     """Gap between the largest and second-largest logit (near-tie measure)."""
     part = np.partition(np.asarray(logits_row, dtype=np.float64), -2)
@@ -548,4 +623,6 @@ PINS = {
     "manual_cached_attention": "torch scaled_dot_product_attention with enable_gqa; brute force",
     "manual_decoder_layer_cached / run_manual_one_token": "transformers Qwen3ForCausalLM (eager, fp32) "
                                                           "loaded with the same dequantised weights",
+    "serial_prompt_all_at_once": "the one-token serial loop (run_manual_one_token) on the same prompts, every "
+                                 "position's logits and every cache row; planted non-causal / off-by-one masks fail",
 }

@@ -54,3 +54,15 @@ def pytest_collection_modifyitems(config, items):
     for it in items:
         if "gpu" in it.keywords:
             it.add_marker(skip)
+
+
+@pytest.fixture(scope="session")
+def qwen3_full():
+    """The full 28-layer Qwen3-0.6B shapes with seeded random Q4 weights (seed 0):
+    (config, host weights, fp32 oracle model), built once per session."""
+    import oracle as o
+    from llm_accelerator_amd.model import Qwen3Config, random_host_weights
+    cfg = Qwen3Config()
+    host = random_host_weights(cfg, seed=0)
+    om = o.OracleModel.from_q4(o.OracleConfig(), host["layers"], *host["embed_tokens"], host["norm"])
+    return cfg, host, om

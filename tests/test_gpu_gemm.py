@@ -73,6 +73,19 @@ def test_gemm_integer_exact(dev, N, K, M):
     np.testing.assert_array_equal(y, ref.astype(np.float32))
 
 
+@pytest.mark.parametrize("N,K,M", [(4096, 1024, 2048), (4096, 1024, 900), (4096, 2048, 1100), (4096, 3072, 1000)])
+def test_gemm_128_row_tiles_integer_exact(dev, N, K, M):
+    """Shapes whose 128-row tiles fill the device (N / 128 * ceil(M / 128) >= 256), so
+    q4d_gemm takes the 128-row-tile kernel the 2048-token prefill's q|k|v projection
+    runs (N = 4096, M = 2048); M = 900 / 1100 / 1000 end on a partial row tile."""
+    assert N // 128 * ((M + 127) // 128) >= 256
+    rng = np.random.default_rng(N + 3 * K + M)
+    packed, scale, x, ref = exact_case(rng, N, K, M)
+    print(f"[gemm exact 128-row tiles] M={M} N={N} K={K}", flush=True)
+    y = gemm(q4(packed, scale), torch.from_numpy(x).to(dev)).cpu().numpy()
+    np.testing.assert_array_equal(y, ref.astype(np.float32))
+
+
 def test_gemm_epilogues_exact(dev):
     rng = np.random.default_rng(11)
     packed, scale, x, ref = exact_case(rng, 256, 1024, 70)
@@ -279,4 +292,73 @@ def test_decode_batch_vs_oracle(dev, batch_setup, positions):
                 got = kvd[li, kind, b, :, p]
                 assert np.all(np.abs(got - want) <= 2e-2 * np.abs(want).max(axis=-1, keepdims=True)), (b, li, kind)
     print(f"[decode batch] B={B} max rel logit err={worst:.3e} near_ties={near}", flush=True)
+    assert worst < 5e-3
+
+
+LONG_CTX = 4097   # the batched-decode benchmark's cache: 4096 filled positions + the new one
+
+
+@pytest.fixture(scope="module")
+def batch_long_setup(dev):
+    cfg = Qwen3Config(num_hidden_layers=2, vocab_size=2048)
+    host = random_host_weights(cfg, seed=3, num_layers=2)
+    model = build_model(cfg, host, max_ctx=LONG_CTX, device=dev)
+    om = o.OracleModel.from_q4(o.OracleConfig(num_hidden_layers=2, vocab_size=2048), host["layers"],
+                               *host["embed_tokens"], host["norm"], dtype=np.float64)
+    return cfg, model, om
+
+
+def test_decode_batch_64_sequences_4096_positions(dev, batch_long_setup):
+    """The batched-decode benchmark's shape (64 sequences, caches of 4097 positions,
+    attention over up to 4096 + 1 positions per sequence) on 2 layers: the span
+    attention kernel with its double-buffered 64-position sub-chunks and its merge of
+    up to 8 splits, against the oracle's full-softmax attention per sequence
+    (common.py:219-228).  Positions cover an empty cache, sub-chunk and span edges
+    and the last slot."""
+    cfg, model, om = batch_long_setup
+    edges = [0, 1, 63, 64, 65, 575, 576, 2047, 2048, 4000, 4095, 4096]
+    rng = np.random.default_rng(64)
+    positions = edges + rng.integers(0, LONG_CTX, 64 - len(edges)).tolist()
+    B = len(positions)
+    tokens = rng.integers(0, cfg.vocab_size, B)
+    print(f"[decode batch long] B={B} max_ctx={LONG_CTX}: filling caches", flush=True)
+    pre = np.empty((2, 2, B, 8, LONG_CTX, 128), dtype=np.float16)
+    for li in range(2):
+        for kind in range(2):
+            pre[li, kind] = rng.standard_normal(size=(B, 8, LONG_CTX, 128), dtype=np.float32)
+    for b, p in enumerate(positions):
+        pre[:, :, b, :, p:] = 0
+    kv = KVCache(cfg, 2, B, LONG_CTX, dev)
+    kv.data.copy_(torch.from_numpy(pre).to(dev))
+    dec = BatchedDecoder(model, B, kv)
+    logits = torch.empty((B, cfg.vocab_size), dtype=torch.float32, device=dev)
+    nt, sc = dec.step(torch.tensor(tokens, dtype=torch.int32, device=dev),
+                      torch.tensor(positions, dtype=torch.int32, device=dev), logits)
+    torch.cuda.synchronize()
+    assert dec.status() == 0
+    nt, sc, lg = nt.cpu().numpy(), sc.cpu().numpy(), logits.cpu().numpy().astype(np.float64)
+    print("[decode batch long] comparing with the oracle per sequence", flush=True)
+    worst, near = 0.0, []
+    for b, p in enumerate(positions):
+        kc = [pre[li, 0, b][None, :, :p].astype(np.float64) for li in range(2)]
+        vc = [pre[li, 1, b][None, :, :p].astype(np.float64) for li in range(2)]
+        rl, rt = o.run_manual_one_token(np.array([[tokens[b]]]), p, om, kc, vc, kv_store_dtype=np.float16)
+        r = rl[0, -1]
+        err = np.abs(lg[b] - r)
+        worst = max(worst, float(err.max() / np.abs(r).max()))
+        first = int(np.argmax(lg[b]))
+        assert nt[b] == first and sc[b] == np.float32(lg[b, first])
+        if nt[b] != rt[0, 0]:
+            gap = r[rt[0, 0]] - r[nt[b]]
+            assert gap <= err[rt[0, 0]] + err[nt[b]], (b, p, gap)
+            near.append((b, int(rt[0, 0]), int(nt[b]), float(gap)))
+        for li in range(2):
+            for kind, ref_c in ((0, kc[li]), (1, vc[li])):
+                want = ref_c[0, :, p]
+                got = kv.data[li, kind, b, :, p].float().cpu().numpy()
+                assert np.all(np.abs(got - want) <= 2e-2 * np.abs(want).max(axis=-1, keepdims=True)), (b, li, kind)
+    # nothing written past each sequence's position
+    for b, p in enumerate(positions):
+        assert not kv.data[:, :, b, :, p + 1:].any(), (b, p)
+    print(f"[decode batch long] B={B} max rel logit err={worst:.3e} near_ties={near}", flush=True)
     assert worst < 5e-3

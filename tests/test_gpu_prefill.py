@@ -1,7 +1,9 @@
-"""Prefill (many tokens of one sequence per call, 2048 tokens in the benchmark, small
-size) on the GPU vs the oracle's serial run_manual_one_token loop
-(10_validate_full_run_one_token.py:17-56, driven one token at a time as in
-:81-135).
+"""Prefill (many tokens of one sequence per call) on the GPU vs the oracle's serial
+run_manual_one_token loop (10_validate_full_run_one_token.py:17-56, driven one token
+at a time as in :81-135): the one-token loop itself up to 130 tokens, and for 700 and
+2048 tokens the same loop evaluated for every position at once
+(oracle.serial_prompt_all_at_once, pinned against the loop and transformers).  The
+benchmark's workload (2048 tokens through all 28 layers) runs here too.
 
 Tolerances (stated): the prefill path rounds every projection's activations
 to fp16 (MFMA GEMMs with fp16-dequantised Q4 tiles) and runs attention with
@@ -10,6 +12,9 @@ fp16 q and probabilities, so against the fp64 oracle:
   oracle's top-2 gap lies within the measured error of the two logits;
 - every appended K/V row: within 2e-2 * max|row| (values of order 1 after
   the per-head RMSNorm, rounded to fp16 in the cache);
+- 28 layers, 2048 tokens, against the fp32 oracle with fp16 K/V: the last token's
+  logits within 2e-2 * max|ref| (28 layers of fp16-rounded projection inputs), the
+  argmax rule above, every K/V row of layers 0, 1 and 27 within 2e-2 * max|row|;
 - chunked prefill (two calls) equals one call bit for bit: each output row
   of the GEMMs and each query of the attention depends only on its own row /
   the cache, with the same accumulation order.
@@ -23,7 +28,7 @@ import oracle as o
 from gpu_helpers import report
 from llm_accelerator_amd._lib import Q4DecError
 from llm_accelerator_amd.decode import GreedyDecoder, Prefill
-from llm_accelerator_amd.model import KVCache, Qwen3Config, build_model, random_host_weights
+from llm_accelerator_amd.model import KVCache, Qwen3Config, build_model, random_host_weights, with_context
 
 pytestmark = pytest.mark.gpu
 
@@ -49,7 +54,7 @@ def oracle_serial(om, tokens):
 
 
 def gpu_prefill(cfg, model, tokens, chunks=None):
-    kv = KVCache(cfg, LAYERS, 1, CTX, model.device)
+    kv = KVCache(cfg, len(model.model.layers), 1, model.max_ctx, model.device)
     pf = Prefill(model, kv, max_tokens=len(tokens))
     logits = torch.empty(cfg.vocab_size, dtype=torch.float32, device=model.device)
     bounds = chunks or [0, len(tokens)]
@@ -59,12 +64,21 @@ def gpu_prefill(cfg, model, tokens, chunks=None):
     return int(nt.item()), float(sc.item()), logits.cpu().numpy().astype(np.float64), kv
 
 
-@pytest.mark.parametrize("n", [1, 37, 64, 130])
+@pytest.mark.parametrize("n", [1, 37, 64, 130, 700, 2048])
 def test_prefill_vs_oracle_serial(setup, n):
+    """n = 700 and 2048 run the 128-row-tile GEMMs (q|k|v, the gate/up pair), 11 and 32
+    query tiles x up to 32 key tiles of the causal attention, and the split-K
+    residual + RMSNorm at the benchmark's token count."""
     cfg, model, om = setup
     tokens = np.random.default_rng(n).integers(0, cfg.vocab_size, n).tolist()
     print(f"[prefill] n={n}", flush=True)
-    ref, ref_tok, kc, vc = oracle_serial(om, tokens)
+    if n <= 130:
+        ref, ref_tok, kc, vc = oracle_serial(om, tokens)
+    else:
+        model = with_context(model, 2048 + 64)
+        ref, kc, vc = o.serial_prompt_all_at_once(om, tokens, kv_store_dtype=np.float16, last_only=True)
+        ref = ref[0]
+        ref_tok = o.argmax_first(ref)[0]
     tok, score, lg, kv = gpu_prefill(cfg, model, tokens)
     _, rel = report(f"prefill n={n} logits", lg, ref)
     assert rel < 5e-3
@@ -127,3 +141,43 @@ def test_prefill_rejects_context_overflow(setup):
         pf.run(list(range(10)), start_pos=CTX - 5)
     assert e.value.code == -10
     assert not kv.data.any()  # nothing launched
+
+
+FULL_N = 2048
+
+
+def test_prefill_2048_tokens_28_layers(dev, qwen3_full):
+    """The benchmark's prefill (2048 uniform random tokens through all 28 layers)
+    against the fp32 oracle with fp16 K/V, evaluated for all positions at once; then
+    the same prompt in three calls equals one call bit for bit."""
+    cfg, host, om = qwen3_full
+    model = build_model(cfg, host, max_ctx=FULL_N + 16, device=dev)
+    tokens = np.random.default_rng(2048).integers(0, cfg.vocab_size, FULL_N).tolist()
+    print(f"[prefill 28 layers] n={FULL_N}: GPU", flush=True)
+    tok, score, lg, kv = gpu_prefill(cfg, model, tokens)
+    print(f"[prefill 28 layers] n={FULL_N}: oracle", flush=True)
+    ref, kc, vc = o.serial_prompt_all_at_once(om, tokens, kv_store_dtype=np.float16, last_only=True)
+    ref = ref[0].astype(np.float64)
+    ref_tok = o.argmax_first(ref)[0]
+    _, rel = report(f"prefill 28 layers n={FULL_N} logits", lg, ref)
+    assert rel < 2e-2
+    first = int(np.argmax(lg))
+    assert tok == first and score == np.float32(lg[first])
+    if tok != ref_tok:
+        gap = ref[ref_tok] - ref[tok]
+        assert gap <= abs(lg[ref_tok] - ref[ref_tok]) + abs(lg[tok] - ref[tok]), (gap, ref_tok, tok)
+        print(f"[prefill 28 layers] reported near-tie: oracle {ref_tok} gpu {tok} gap {gap:.3e}", flush=True)
+    for li in (0, 1, 27):
+        for kind, ref_c in ((0, kc[li]), (1, vc[li])):
+            want = ref_c[0].astype(np.float64)                              # [kvh, n, d]
+            got = kv.data[li, kind, 0, :, :FULL_N].float().cpu().numpy()
+            err = np.abs(got - want)
+            row = np.abs(want).max(axis=-1, keepdims=True)
+            print(f"[prefill 28 layers] layer {li} {'KV'[kind]}: max-abs {err.max():.3e}, "
+                  f"max rel to row {np.max(err / row):.3e}", flush=True)
+            assert np.all(err <= 2e-2 * row), (li, kind)
+    assert not kv.data[:, :, 0, :, FULL_N:].any()
+    t2, s2, l2, kv2 = gpu_prefill(cfg, model, tokens, chunks=[0, 700, 1500, FULL_N])
+    assert (t2, s2) == (tok, score)
+    np.testing.assert_array_equal(l2, lg)
+    assert torch.equal(kv2.data, kv.data)

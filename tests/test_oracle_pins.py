@@ -237,3 +237,44 @@ def test_greedy_decode_teacher_forcing_identity():
     gen, gaps, _ = o.greedy_decode(om, [1, 2, 3], 6)
     gen2, _, _ = o.greedy_decode(om, [1, 2, 3], 6, forced=gen[:-1])
     assert gen == gen2 and len(gaps) == 6 and min(gaps) >= 0
+
+
+def test_all_positions_prompt_equals_serial_loop_and_transformers():
+    """serial_prompt_all_at_once (the serial prompt loop of
+    10_validate_full_run_one_token.py:81-135 evaluated for every position at once)
+    against (a) the oracle's own one-token loop in fp64, every position's logits and
+    every cache row, and (b) transformers' Qwen3ForCausalLM run over the whole prompt
+    with its causal mask (fp32, the reference's 1e-5 class bar).  Planted mask
+    mistakes (a query that misses its own key, or sees the next one) fail (a)."""
+    layers, vocab = 2, 1024
+    host, om32 = _small_q4_model(layers, vocab)
+    om64 = o.OracleModel.from_q4(o.OracleConfig(num_hidden_layers=layers, vocab_size=vocab), host["layers"],
+                                 *host["embed_tokens"], host["norm"], dtype=np.float64)
+    for n in (1, 5, 37):
+        toks = np.random.default_rng(n).integers(0, vocab, n).tolist()
+        kc, vc = [None] * layers, [None] * layers
+        serial = []
+        for pos, t in enumerate(toks):
+            lg, _ = o.run_manual_one_token(np.array([[t]]), pos, om64, kc, vc)
+            serial.append(lg[0, 0])
+        serial = np.stack(serial)
+        allpos, ak, av = o.serial_prompt_all_at_once(om64, toks)
+        assert allpos.shape == (n, vocab)
+        np.testing.assert_allclose(allpos, serial, rtol=0, atol=1e-11 * np.abs(serial).max())
+        for li in range(layers):
+            np.testing.assert_allclose(ak[li], kc[li], rtol=0, atol=1e-12 * np.abs(kc[li]).max())
+            np.testing.assert_allclose(av[li], vc[li], rtol=0, atol=1e-12 * np.abs(vc[li]).max())
+        if n > 1:
+            for bad in (0, 2):
+                wrong, _, _ = o.serial_prompt_all_at_once(om64, toks, _future_offset=bad)
+                assert not np.allclose(wrong, serial, rtol=0, atol=1e-3 * np.abs(serial).max()), bad  # NaN counts as wrong
+    hf = _hf_model_from(host, layers, vocab)
+    toks = np.random.default_rng(3).integers(0, vocab, 23).tolist()
+    with torch.no_grad():
+        out = hf(input_ids=torch.tensor([toks]), use_cache=True)
+    ref = out.logits.numpy()[0]
+    got, ak, av = o.serial_prompt_all_at_once(om32, toks)
+    assert np.max(np.abs(got - ref)) <= 2e-5 * np.abs(ref).max()
+    for li in range(layers):
+        hk = out.past_key_values.layers[li].keys.numpy()
+        np.testing.assert_allclose(ak[li], hk, rtol=1e-4, atol=1e-4 * np.abs(hk).max())
