@@ -17,7 +17,7 @@ q4d_run_one_token makes), so every layer's output can be read.  Stated bars:
   - new K/V rows of layers 0/1/27: within 2^-9 * max|row| of A (the cache holds
     fp16; one rounding plus the fp32 error ahead of it) and one fp16 ulp of the
     row's largest element against B;
-  - logits of every generated step: max-abs <= 5e-3 * max|A|, 2e-4 * max|B|;
+  - logits of every generated step: max-abs <= 1e-3 * max|A|, 2e-4 * max|B|;
   - argmax equal to A's token unless a reported near-tie: A's top-2 gap lies
     within the measured error of the two logits involved.
 The measured per-layer max-abs and relative errors are printed (run with -s).
@@ -48,7 +48,7 @@ STEPS = PROMPT + GEN - 1          # positions 0 .. 318; generated tokens come fr
 KV_LAYERS = (0, 1, 27)
 HIDDEN_BAR_A, HIDDEN_BAR_B = 2.0 ** -10, 1e-4
 KV_BAR_A = 2.0 ** -9
-LOGIT_BAR_A, LOGIT_BAR_B = 5e-3, 2e-4
+LOGIT_BAR_A, LOGIT_BAR_B = 1e-3, 2e-4
 BITWISE_POSITIONS = (PROMPT - 1, 200, STEPS - 1)
 
 

@@ -13,7 +13,7 @@ fp16 q and probabilities, so against the fp64 oracle:
 - every appended K/V row: within 2e-2 * max|row| (values of order 1 after
   the per-head RMSNorm, rounded to fp16 in the cache);
 - 28 layers, 2048 tokens, against the fp32 oracle with fp16 K/V: the last token's
-  logits within 2e-2 * max|ref| (28 layers of fp16-rounded projection inputs), the
+  logits within 1e-3 * max|ref| (28 layers of fp16-rounded projection inputs), the
   argmax rule above, every K/V row of layers 0, 1 and 27 within 2e-2 * max|row|;
 - chunked prefill (two calls) equals one call bit for bit: each output row
   of the GEMMs and each query of the attention depends only on its own row /
@@ -160,7 +160,7 @@ def test_prefill_2048_tokens_28_layers(dev, qwen3_full):
     ref = ref[0].astype(np.float64)
     ref_tok = o.argmax_first(ref)[0]
     _, rel = report(f"prefill 28 layers n={FULL_N} logits", lg, ref)
-    assert rel < 2e-2
+    assert rel < 1e-3
     first = int(np.argmax(lg))
     assert tok == first and score == np.float32(lg[first])
     if tok != ref_tok:
