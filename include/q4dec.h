@@ -82,8 +82,7 @@ enum {
 /* Device status word bits (q4d_read_status). */
 enum {
   Q4D_STATUS_BAD_TOKEN = 1,
-  Q4D_STATUS_BAD_POSITION = 2,
-  Q4D_STATUS_SYNC_TIMEOUT = 4  /* a persistent decode kernel gave up waiting for another block */
+  Q4D_STATUS_BAD_POSITION = 2
 };
 
 enum { Q4D_F16 = 0, Q4D_F32 = 1, Q4D_BF16 = 2 };
@@ -143,14 +142,6 @@ int q4d_workspace_init(void* ws, size_t ws_bytes, const q4d_model_t* model, int3
  * enters as an fp16 hi + fp16 lo pair (~22 significant bits); 1 = rounded to
  * fp16.  Process-wide; set it before launching work. */
 int q4d_set_activation_precision(int32_t mode);
-/* Batch-1 decode path of q4d_decoder_layer / q4d_run_one_token: 0 (default)
- * = five kernels per layer; 1 = a persistent kernel runs up to 8 layers per
- * launch, blocks handing each other their outputs through the workspace,
- * when the model has the Qwen3-0.6B layer shapes, max_ctx <= 1024 and the
- * device holds its 128 blocks at once (else the five kernels run).  Same
- * results to fp32 rounding.  No counterpart in the reference (whose layer is
- * one Python call, common.py:231-298); process-wide. */
-int q4d_set_persistent_decode(int32_t on);
 /* Copy the device status word into *out (synchronises `stream`). */
 int q4d_read_status(const void* ws, size_t ws_bytes, const q4d_model_t* model, int32_t batch,
                     int32_t* out, void* stream);

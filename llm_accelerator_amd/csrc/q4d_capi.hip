@@ -15,11 +15,6 @@ namespace {
 // Activation precision inside the fused decode: 2 = fp32 activations enter
 // each GEMV as hi+lo fp16 halves (about 22 significant bits), 1 = rounded to fp16.
 int g_act_precision = 2;
-// Batch-1 decode layers run in the persistent kernel when this is set and the
-// model allows it (q4d_set_persistent_decode).  Off by default: measured on
-// MI355X, a device-wide handoff through memory costs as much as a kernel
-// boundary in a HIP graph, so the five-kernel layer is as fast or faster.
-int g_persistent = 0;
 
 inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 
@@ -189,50 +184,6 @@ int run_layer(const q4d_model_t* m, int l, const float* hin, float* hout, const 
   return Q4D_OK;
 }
 
-// Layers [l0, l1) of a batch-1 decode step in the persistent kernel, up to
-// kPersistMaxLayers per launch; hidden flows hin -> hout (may alias).
-int run_layers_persist(const q4d_model_t* m, int l0, int l1, const float* hin, float* hout,
-                       const q4d_kv_cache_t* kv, const int32_t* positions, void* ws, const WsLayout& W,
-                       hipStream_t st) {
-  for (int g0 = l0; g0 < l1; g0 += kPersistMaxLayers) {
-    PersistArgs p;
-    memset(&p, 0, sizeof(p));
-    p.nl = l1 - g0 < kPersistMaxLayers ? l1 - g0 : kPersistMaxLayers;
-    for (int i = 0; i < p.nl; ++i) {
-      const q4d_layer_t& L = m->layers[g0 + i];
-      const q4d_matrix_t* mats[7] = {&L.q_proj, &L.k_proj, &L.v_proj, &L.o_proj, &L.gate_proj, &L.up_proj,
-                                     &L.down_proj};
-      for (int k = 0; k < 7; ++k) {
-        p.L[i].w[k] = mats[k]->w;
-        p.L[i].s[k] = mats[k]->s;
-      }
-      p.L[i].in_norm = L.input_layernorm;
-      p.L[i].post_norm = L.post_attention_layernorm;
-      p.L[i].q_norm = L.q_norm;
-      p.L[i].k_norm = L.k_norm;
-    }
-    p.h_in = g0 == l0 ? hin : hout;
-    p.h_out = hout;
-    uint16_t *kp, *vp;
-    kv_planes(kv, g0, &kp, &vp);
-    p.kcache = kp;
-    p.kind_stride = (size_t)(vp - kp);
-    p.layer_stride = 2 * p.kind_stride;
-    p.max_ctx = kv->max_ctx;
-    p.positions = positions;
-    p.rope_cos = m->rope_cos;
-    p.rope_sin = m->rope_sin;
-    p.eps = m->rms_norm_eps;
-    p.scaling = m->attn_scaling;
-    p.xbuf = ws_ptr<uint64_t>(ws, W.pxbuf);
-    p.seq = ws_ptr<int32_t>(ws, W.pseq);
-    p.status = ws_ptr<int32_t>(ws, W.status);
-    const int rc = launch_persist(p, g_act_precision, st);
-    if (rc) return rc;
-  }
-  return Q4D_OK;
-}
-
 int run_lm_head(const q4d_model_t* m, const float* hidden, int32_t* tok, float* score, float* logits,
                 void* ws, const WsLayout& W, hipStream_t st) {
   GemvArgs a = one_matrix(&m->embed_tokens, 1);
@@ -276,12 +227,6 @@ const char* q4d_status_string(int code) {
 int q4d_set_activation_precision(int32_t mode) {
   if (mode != 1 && mode != 2) return Q4D_ERR_DTYPE;
   g_act_precision = mode;
-  return Q4D_OK;
-}
-
-int q4d_set_persistent_decode(int32_t on) {
-  if (on != 0 && on != 1) return Q4D_ERR_SHAPE;
-  g_persistent = on;
   return Q4D_OK;
 }
 
@@ -415,9 +360,6 @@ int q4d_decoder_layer(const q4d_model_t* model, int32_t layer, const float* hidd
   if ((rc = check_kv(kv, model, 1))) return rc;
   if (kv->batch != 1) return Q4D_ERR_CAPACITY;
   if ((rc = check_ws(ws, ws_bytes, model, 1))) return rc;
-  if (g_persistent && persist_eligible(model))
-    return run_layers_persist(model, layer, layer + 1, hidden_in, hidden_out, kv, positions, ws,
-                              ws_layout(model, 1), as_stream(stream));
   return run_layer(model, layer, hidden_in, hidden_out, kv, positions, ws, ws_layout(model, 1), as_stream(stream));
 }
 
@@ -660,13 +602,8 @@ int q4d_run_one_token(const q4d_model_t* model, const int32_t* tokens, const int
   float* hidden = ws_ptr<float>(ws, W.hidden);
   if ((rc = launch_embedding(&model->embed_tokens, tokens, 1, hidden, ws_ptr<int32_t>(ws, W.status), st)))
     return rc;
-  if (g_persistent && persist_eligible(model)) {
-    if ((rc = run_layers_persist(model, 0, model->num_layers, hidden, hidden, kv, positions, ws, W, st)))
-      return rc;
-  } else {
-    for (int l = 0; l < model->num_layers; ++l)
-      if ((rc = run_layer(model, l, hidden, hidden, kv, positions, ws, W, st))) return rc;
-  }
+  for (int l = 0; l < model->num_layers; ++l)
+    if ((rc = run_layer(model, l, hidden, hidden, kv, positions, ws, W, st))) return rc;
   return run_lm_head(model, hidden, next_token, score, logits, ws, W, st);
 }
 

@@ -1,6 +1,5 @@
-// Device building blocks of the Q4 GEMVs shared by the one-shot / streaming
-// kernels (q4d_gemv.hip) and the persistent decode kernel (q4d_persist.hip):
-// buffer-resource weight tiles (2 rows x 1024 columns per wave, lane l reads
+// Device building blocks of the Q4 GEMVs (the one-shot decode kernels and the
+// streaming LM head of q4d_gemv.hip): buffer-resource weight tiles (2 rows x 1024 columns per wave, lane l reads
 // the 16-byte chunk l % 32 of row l / 32 and the word holding its Q2.14
 // scale), the hi/lo dequant dot products, and the block-cooperative
 // activation staging in LDS (stage x and gamma, RMSNorm, conversion into the

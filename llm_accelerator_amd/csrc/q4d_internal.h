@@ -17,26 +17,6 @@ constexpr int kAttnChunkLong = 128;
 // Upper bound on the LM-head grid (one partial argmax per block).
 constexpr int kLmMaxBlocks = 2048;
 
-// Persistent batch-1 decode kernel (q4d_persist.hip): grid, layers per
-// launch, and the 64-bit exchange words one layer uses (q|k|v 4096; chunk
-// partials 16 heads x 8 chunks x (max, sum, 128 dims) as fp32 in the first
-// half of their region; hidden after attention 1024, SwiGLU 3072, hidden
-// after the MLP 1024; attention unit flags).  It serves
-// models with the Qwen3-0.6B layer shapes and at most kPersistMaxCtx
-// positions (8 chunks of 128).
-constexpr int kPersistBlocks = 128;
-constexpr int kPersistWaves = 16;
-constexpr int kPersistMaxLayers = 8;
-constexpr int kPersistMaxCtx = 1024;
-constexpr int kPersistChunks = kPersistMaxCtx / kAttnChunkLong;
-constexpr int kPxQkv = 0;
-constexpr int kPxPart = kPxQkv + 4096;
-constexpr int kPxH1 = kPxPart + 16 * kPersistChunks * 130;
-constexpr int kPxAct = kPxH1 + 1024;
-constexpr int kPxH2 = kPxAct + 3072;
-constexpr int kPxFlags = kPxH2 + 1024;  // one ready flag per attention unit (kv head, chunk)
-constexpr int kPxLayerWords = kPxFlags + 8 * kPersistChunks;
-
 inline size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
 // Byte offsets of the regions of a caller-provided workspace.
@@ -44,8 +24,6 @@ struct WsLayout {
   size_t status;     // int32[64]: [0] = status bits
   size_t counters;   // int32[batch * kv_heads] attention split counters, then 1 LM counter
   size_t lm_key;     // u64 packed (score, index) running LM-head argmax (zeroed with the counters)
-  size_t pseq;       // i32 [kPersistBlocks] launch counters of the persistent kernel (zeroed)
-  size_t pxbuf;      // u64 [kPersistMaxLayers][kPxLayerWords] tagged exchange words (zeroed)
   size_t hidden;     // f32 [batch, hidden]          residual stream
   size_t qkv;        // f32 [batch, (qh + 2 kvh) * d] raw q|k|v projections
   size_t qrope;      // f32 [batch, qh * d]          q after norm + RoPE (primitive path)
@@ -73,8 +51,6 @@ inline WsLayout ws_layout(const q4d_model_t* m, int batch) {
   L.counters = o; o = align_up(o + (size_t)(batch * kvh + 1) * 4, A);
   L.lm_counter_index = batch * kvh;
   L.lm_key = o;   o = align_up(o + 8, A);
-  L.pseq = o;     o = align_up(o + (size_t)kPersistBlocks * 4, A);
-  L.pxbuf = o;    o = align_up(o + (size_t)kPersistMaxLayers * kPxLayerWords * 8, A);
   L.hidden = o;   o = align_up(o + (size_t)batch * m->hidden_size * 4, A);
   L.qkv = o;      o = align_up(o + (size_t)batch * (qh + 2 * kvh) * d * 4, A);
   L.qrope = o;    o = align_up(o + (size_t)batch * qh * d * 4, A);
@@ -244,42 +220,6 @@ struct PrefillArgs {
   _Float16* out;           // [n][qh * head_dim] attention output
   int n, p0, qh, kvh, max_ctx;
 };
-// ---- persistent batch-1 decode kernel ----------------------------------------
-// One decoder layer's device pointers (q k v o gate up down; codes, scales).
-struct PLayer {
-  const void* w[7];
-  const void* s[7];
-  const float* in_norm;
-  const float* post_norm;
-  const float* q_norm;
-  const float* k_norm;
-};
-
-struct PersistArgs {
-  PLayer L[kPersistMaxLayers];
-  int nl;                 // layers in this launch
-  const float* h_in;      // fp32 [1024] hidden entering L[0]
-  float* h_out;           // fp32 [1024] hidden leaving L[nl - 1] (may alias h_in)
-  uint16_t* kcache;       // K plane of L[0]: [kv_heads][max_ctx][128] fp16 (sequence 0)
-  size_t layer_stride;    // fp16 elements from one layer's K plane to the next
-  size_t kind_stride;     // fp16 elements from a layer's K plane to its V plane
-  int max_ctx;
-  const int32_t* positions;
-  const float* rope_cos;
-  const float* rope_sin;
-  float eps;
-  float scaling;
-  uint64_t* xbuf;         // tagged exchange words (WsLayout::pxbuf)
-  int32_t* seq;           // launch counters (WsLayout::pseq)
-  int32_t* status;
-};
-
-// Whether the persistent kernel can serve this model: the layer shapes it is
-// specialised for, at most kPersistMaxCtx positions, and kPersistBlocks
-// blocks resident at once on the current device.
-bool persist_eligible(const q4d_model_t* m);
-int launch_persist(const PersistArgs& a, int xp, hipStream_t st);
-
 // ---- integer Q4 GEMV of the fixed-point path (q4d_int.hip) ------------------
 int launch_gemv_q26(const q4d_matrix_t* w, const int32_t* x, int64_t* y_q26, int32_t* y_q12, int32_t* saturated,
                     hipStream_t st);

@@ -203,14 +203,3 @@ def test_prefill_validation_codes(lib):
 def test_activation_precision_setter(lib):
     assert lib.q4d_set_activation_precision(3) == -13
     assert lib.q4d_set_activation_precision(2) == 0
-
-
-def test_persistent_decode_switch(lib):
-    assert lib.q4d_set_persistent_decode(2) == -11
-    assert lib.q4d_set_persistent_decode(1) == 0
-    assert lib.q4d_set_persistent_decode(0) == 0  # the default, left for later tests
-
-
-def test_error_class_carries_code():
-    e = _lib.Q4DecError(-10, "x")
-    assert e.code == -10 and "CONTEXT" in str(e) and isinstance(e, RuntimeError)
