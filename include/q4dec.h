@@ -248,6 +248,19 @@ int q4d_layer_stage(const q4d_model_t* model, int32_t layer, int32_t stage, cons
 int q4d_run_one_token(const q4d_model_t* model, const int32_t* tokens, const int32_t* positions,
                       const q4d_kv_cache_t* kv, int32_t* next_token, float* score, float* logits,
                       void* ws, size_t ws_bytes, void* stream);
+/* q4d_run_one_token without a workspace argument, for callers that cannot allocate
+ * device memory (code under HIP graph capture, serving loops or harnesses that forbid
+ * hipMalloc).  No counterpart in the reference.  Its scratch is a 4 MiB device array
+ * inside the library, one per GPU, held until the process ends; the call allocates
+ * nothing.  Models whose batch-1 workspace (q4d_workspace_bytes(model, 1)) exceeds
+ * 4 MiB are rejected with Q4D_ERR_CAPACITY (Qwen3-0.6B shapes: max_ctx <= 30208).
+ * status: device int32[1], caller-owned and caller-cleared; the step ORs its
+ * Q4D_STATUS_* bits into it.  All calls on one GPU share that GPU's scratch, so calls
+ * that overlap on one GPU (two streams, two threads) race; serialise them.  Results
+ * equal q4d_run_one_token's bit for bit. */
+int q4d_run_one_token_noalloc(const q4d_model_t* model, const int32_t* tokens, const int32_t* positions,
+                              const q4d_kv_cache_t* kv, int32_t* next_token, float* score, float* logits,
+                              int32_t* status, void* stream);
 /* One decode step for `batch` independent sequences (batched decode): tokens[b] at
  * positions[b] (device int32 [batch], each sequence its own position) through embedding,
  * all layers (projections as MFMA GEMMs over the batch, GQA attention per sequence) and the

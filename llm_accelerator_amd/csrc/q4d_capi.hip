@@ -2,7 +2,14 @@
 // stream-ordered launches.  See include/q4dec.h for the contract.
 #include <string.h>
 
+#include <mutex>
+
 #include "q4d_internal.h"
+
+// Device scratch of q4d_run_one_token_noalloc (see noalloc_scratch below).
+constexpr size_t kNoallocScratchBytes = size_t(4) << 20;
+constexpr int kNoallocClearWords = 1024;  // status, counters and LM-head key region (4 KB)
+static __device__ __align__(256) unsigned char scratch[kNoallocScratchBytes];
 
 namespace q4d {
 int launch_gemv_xp(const GemvArgs& a, int xm, int xp, int ep, bool pair, hipStream_t st);
@@ -91,7 +98,8 @@ GemvArgs one_matrix(const q4d_matrix_t* w, int batch) {
 // One decoder layer, batch 1 (common.py:231-298), five launches; `only`
 // selects a single stage (Q4D_STAGE_*) or -1 for all.
 int run_layer(const q4d_model_t* m, int l, const float* hin, float* hout, const q4d_kv_cache_t* kv,
-              const int32_t* positions, void* ws, const WsLayout& W, hipStream_t st, int only = -1) {
+              const int32_t* positions, void* ws, const WsLayout& W, hipStream_t st, int only = -1,
+              int32_t* status = nullptr) {
   const q4d_layer_t& L = m->layers[l];
   const int xp = g_act_precision;
   float* qkv = ws_ptr<float>(ws, W.qkv);
@@ -142,7 +150,7 @@ int run_layer(const q4d_model_t* m, int l, const float* hin, float* hout, const 
   t.counters = ws_ptr<int>(ws, W.counters);
   t.out = attn;
   t.out_dtype = Q4D_F32;
-  t.status = ws_ptr<int32_t>(ws, W.status);
+  t.status = status ? status : ws_ptr<int32_t>(ws, W.status);
   t.merge = 0;  // partials only: merged by the o_proj prologue
   if ((only < 0 || only == Q4D_STAGE_ATTENTION) && (rc = launch_attention(t, st))) return rc;
 
@@ -196,6 +204,44 @@ int run_lm_head(const q4d_model_t* m, const float* hidden, int32_t* tok, float* 
   a.out_token = tok;
   a.out_score = score;
   return launch_gemv_xp(a, X_RMS, g_act_precision, EP_ARGMAX, false, st);
+}
+
+// Embedding -> all layers -> LM head argmax for one token (batch 1), the launches of
+// q4d_run_one_token; `status` receives the device-side status bits.
+int run_token(const q4d_model_t* m, const int32_t* tokens, const int32_t* positions, const q4d_kv_cache_t* kv,
+              int32_t* next_token, float* score, float* logits, void* ws, const WsLayout& W, int32_t* status,
+              hipStream_t st) {
+  float* hidden = ws_ptr<float>(ws, W.hidden);
+  int rc = launch_embedding(&m->embed_tokens, tokens, 1, hidden, status, st);
+  if (rc) return rc;
+  for (int l = 0; l < m->num_layers; ++l)
+    if ((rc = run_layer(m, l, hidden, hidden, kv, positions, ws, W, st, -1, status))) return rc;
+  return run_lm_head(m, hidden, next_token, score, logits, ws, W, st);
+}
+
+// Scratch of q4d_run_one_token_noalloc, for callers that cannot allocate: a
+// workspace of this library's layout in a device array (one copy per GPU, zero
+// from module load).  Host code never uses the array's name as an address: each
+// device's address comes from hipGetSymbolAddress, once per device, below.
+// Every call on one GPU shares that GPU's copy; calls that overlap on one GPU race.
+int noalloc_scratch(hipStream_t st, void** out) {
+  constexpr int kMaxDevices = 64;
+  static std::mutex mu;
+  static void* ptrs[kMaxDevices] = {};
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return Q4D_ERR_LAUNCH;
+  std::lock_guard<std::mutex> lock(mu);
+  if (!ptrs[dev]) {
+    void* p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) return Q4D_ERR_LAUNCH;
+    // the counters and the LM-head argmax key start at zero (the kernels leave them zero
+    // again); cleared once here with a fill kernel in case the module's zero fill is not relied on
+    const int rc = launch_fill_i32(static_cast<int32_t*>(p), 0, kNoallocClearWords, st);
+    if (rc) return rc;
+    ptrs[dev] = p;
+  }
+  *out = ptrs[dev];
+  return Q4D_OK;
 }
 
 }  // namespace
@@ -598,13 +644,25 @@ int q4d_run_one_token(const q4d_model_t* model, const int32_t* tokens, const int
   if (kv->batch != 1) return Q4D_ERR_CAPACITY;
   if ((rc = check_ws(ws, ws_bytes, model, 1))) return rc;
   const WsLayout W = ws_layout(model, 1);
+  return run_token(model, tokens, positions, kv, next_token, score, logits, ws, W, ws_ptr<int32_t>(ws, W.status),
+                   as_stream(stream));
+}
+
+int q4d_run_one_token_noalloc(const q4d_model_t* model, const int32_t* tokens, const int32_t* positions,
+                              const q4d_kv_cache_t* kv, int32_t* next_token, float* score, float* logits,
+                              int32_t* status, void* stream) {
+  if (!tokens || !positions || !next_token || !score || !status) return Q4D_ERR_NULL;
+  int rc = check_model(model);
+  if (rc) return rc;
+  if ((rc = check_kv(kv, model, 1))) return rc;
+  if (kv->batch != 1) return Q4D_ERR_CAPACITY;
+  if (!aligned(status, 4)) return Q4D_ERR_BAD_ADDR;
+  const WsLayout W = ws_layout(model, 1);
+  if (W.total > kNoallocScratchBytes || W.hidden > kNoallocClearWords * 4) return Q4D_ERR_CAPACITY;
   hipStream_t st = as_stream(stream);
-  float* hidden = ws_ptr<float>(ws, W.hidden);
-  if ((rc = launch_embedding(&model->embed_tokens, tokens, 1, hidden, ws_ptr<int32_t>(ws, W.status), st)))
-    return rc;
-  for (int l = 0; l < model->num_layers; ++l)
-    if ((rc = run_layer(model, l, hidden, hidden, kv, positions, ws, W, st))) return rc;
-  return run_lm_head(model, hidden, next_token, score, logits, ws, W, st);
+  void* ws = nullptr;
+  if ((rc = noalloc_scratch(st, &ws))) return rc;
+  return run_token(model, tokens, positions, kv, next_token, score, logits, ws, W, status, st);
 }
 
 size_t q4d_prefill_workspace_bytes(const q4d_model_t* model, int32_t max_tokens) {
