@@ -66,7 +66,7 @@ constexpr int kAttnMergeWaves = 8;   // waves per block of the GEMV merging atte
 template <int K, int NWB, int XM, int XP>
 __device__ __forceinline__ void act_load(const GemvArgs& a, int bat, ActRegs<K, NWB, XM, XP>& r) {
   using R = ActRegs<K, NWB, XM, XP>;
-  if constexpr (XM == X_ATTN) return;  // loaded after the weights (act_load_attn)
+  if constexpr (XM == X_ATTN) return;  // chunk partials: attn_issue / attn_finish
 #pragma unroll
   for (int i = 0; i < R::XPT; ++i) {
     const int v = threadIdx.x + i * NWB * 64;
@@ -85,31 +85,38 @@ __device__ __forceinline__ void act_load(const GemvArgs& a, int bat, ActRegs<K, 
 // own merge does it).  The loads of up to kMergeBatch chunks go out together.
 constexpr int kMergeBatch = 8;
 
-// One batch of kMergeBatch chunks of partials for dims d..d+3 of one head,
-// folded into the running (M, L, o).
-__device__ __forceinline__ void merge_batch(const GemvArgs& a, size_t base, int d, int c0, int ns, float& M, float& L,
-                                            f32x4& o) {
-  constexpr int D = 128;
+// One batch of kMergeBatch chunks of partials for dims d..d+3 of one head:
+// the loads (issued on their own so they can go out before the weights) and
+// the fold into the running (M, L, o).
+struct MergeLoads {
   float2 ml[kMergeBatch];
   f32x4 ac[kMergeBatch];
+};
+
+__device__ __forceinline__ void merge_issue(const GemvArgs& a, size_t base, int d, int c0, MergeLoads& m) {
+  constexpr int D = 128;
   // addresses clamp to the workspace, not to ns: ns comes from a device
   // load, and addresses depending on it would wait for that load first
 #pragma unroll
   for (int k = 0; k < kMergeBatch; ++k) {
     const int c = c0 + k < a.nsplit_max ? c0 + k : a.nsplit_max - 1;
-    ml[k] = *reinterpret_cast<const float2*>(a.part_ml + (base + c) * 2);
-    ac[k] = *reinterpret_cast<const f32x4*>(a.part_acc + (base + c) * D + d);
+    m.ml[k] = *reinterpret_cast<const float2*>(a.part_ml + (base + c) * 2);
+    m.ac[k] = *reinterpret_cast<const f32x4*>(a.part_acc + (base + c) * D + d);
   }
+}
+
+__device__ __forceinline__ void merge_fold(const MergeLoads& m, int c0, int ns, float& M, float& L, f32x4& o) {
   // chunks past ns are masked with selects, not branches: a branch lets the
   // compiler sink their loads into it, behind a wait for everything in flight
   float mk[kMergeBatch], lk[kMergeBatch];
+  f32x4 ac[kMergeBatch];
   float Mn = M;
 #pragma unroll
   for (int k = 0; k < kMergeBatch; ++k) {
     const bool valid = c0 + k < ns;
-    mk[k] = valid ? ml[k].x : -INFINITY;
-    lk[k] = valid ? ml[k].y : 0.f;
-    ac[k] = valid ? ac[k] : f32x4{0.f, 0.f, 0.f, 0.f};
+    mk[k] = valid ? m.ml[k].x : -INFINITY;
+    lk[k] = valid ? m.ml[k].y : 0.f;
+    ac[k] = valid ? m.ac[k] : f32x4{0.f, 0.f, 0.f, 0.f};
     Mn = fmaxf(Mn, mk[k]);
   }
   const float so = M == -INFINITY ? 0.f : exp2f(M - Mn);
@@ -124,25 +131,53 @@ __device__ __forceinline__ void merge_batch(const GemvArgs& a, size_t base, int 
   M = Mn;
 }
 
+// X_ATTN activations: the first batch of chunk partials of this thread's
+// vectors is loaded by attn_issue (before the weights), the merge runs in
+// attn_finish (after the weights are issued); further batches, past
+// kMergeBatch chunks, load and fold in turn.
 template <int K, int NWB>
-__device__ __forceinline__ void act_load_attn(const GemvArgs& a, int bat, f32x4 (&xr)[(K / 4 + NWB * 64 - 1) /
-                                                                                          (NWB * 64)]) {
-  constexpr int XV = K / 4, NT = NWB * 64, XPT = (XV + NT - 1) / NT, D = 128;
-  const int pos = a.positions[bat];
-  int ns = (pos + a.attn_chunk) / a.attn_chunk;  // chunks holding positions 0..pos
+struct AttnPre {
+  static constexpr int XV = K / 4, NT = NWB * 64, XPT = (XV + NT - 1) / NT;
+  MergeLoads m[XPT];
+  int pos;
+};
+
+template <int K, int NWB>
+__device__ __forceinline__ void attn_issue(const GemvArgs& a, int bat, AttnPre<K, NWB>& p) {
+  using P = AttnPre<K, NWB>;
+  constexpr int D = 128;
+  p.pos = a.positions[bat];
+#pragma unroll
+  for (int i = 0; i < P::XPT; ++i) {
+    const int v = threadIdx.x + i * P::NT;
+    const int vc = P::XV % P::NT != 0 && v >= P::XV ? P::XV - 1 : v;
+    const int h = (4 * vc) / D, d = (4 * vc) % D;
+    const size_t base = ((size_t)bat * (K / D) + h) * a.nsplit_max;
+    merge_issue(a, base, d, 0, p.m[i]);
+  }
+}
+
+template <int K, int NWB>
+__device__ __forceinline__ void attn_finish(const GemvArgs& a, int bat, const AttnPre<K, NWB>& p,
+                                            f32x4 (&xr)[(K / 4 + NWB * 64 - 1) / (NWB * 64)]) {
+  using P = AttnPre<K, NWB>;
+  constexpr int D = 128;
+  int ns = (p.pos + a.attn_chunk) / a.attn_chunk;  // chunks holding positions 0..pos
   ns = ns < 1 ? 1 : (ns > a.nsplit_max ? a.nsplit_max : ns);
 #pragma unroll
-  for (int i = 0; i < XPT; ++i) {
-    const int v = threadIdx.x + i * NT;
-    if (XV % NT != 0 && v >= XV) continue;
+  for (int i = 0; i < P::XPT; ++i) {
+    const int v = threadIdx.x + i * P::NT;
+    if (P::XV % P::NT != 0 && v >= P::XV) continue;
     const int h = (4 * v) / D, d = (4 * v) % D;
     const size_t base = ((size_t)bat * (K / D) + h) * a.nsplit_max;
     float M = -INFINITY, L = 0.f;
     f32x4 o = f32x4{0.f, 0.f, 0.f, 0.f};
-    // the first batch is straight-line code, so its loads go out right after
-    // the weights' (a loop here makes the compiler wait for those first)
-    merge_batch(a, base, d, 0, ns, M, L, o);
-    for (int c0 = kMergeBatch; c0 < ns; c0 += kMergeBatch) merge_batch(a, base, d, c0, ns, M, L, o);
+    merge_fold(p.m[i], 0, ns, M, L, o);
+    for (int c0 = kMergeBatch; c0 < ns; c0 += kMergeBatch) {
+      MergeLoads m;
+      merge_issue(a, base, d, c0, m);
+      merge_fold(m, c0, ns, M, L, o);
+    }
     xr[i] = o * (1.0f / L);
   }
 }
@@ -170,6 +205,11 @@ __global__ __launch_bounds__(NWB * 64) void gemv_kernel(const GemvArgs a) {
   // ---- activation loads go out first, then every weight load -----------------
   ActRegs<K, NWB, XM, XP> ar;
   act_load(a, bat, ar);
+  AttnPre<K, NWB> ap;
+  if constexpr (XM == X_ATTN) {
+    attn_issue<K, NWB>(a, bat, ap);
+    __builtin_amdgcn_sched_barrier(0);
+  }
 
   const int e0 = a.seg_end[0], e1 = a.seg_end[1];
   const Rsrc rw0 = make_rsrc(a.w[0], (uint32_t)e0 * (K / 2));
@@ -204,12 +244,12 @@ __global__ __launch_bounds__(NWB * 64) void gemv_kernel(const GemvArgs a) {
       res_pre[u] = a.resid[(size_t)bat * a.rows + 2 * (t < NP ? t : NP - 1) + (lane >> 5)];
     }
   }
-  // attention partials go out after the weights: both round trips overlap
-  // (the barrier keeps the scheduler from moving the weight loads behind the
-  // merge arithmetic, which waits for the partials)
+  // the attention partials were loaded before the weights, so the merge can
+  // start as soon as they arrive (vmcnt retires in issue order); the barrier
+  // keeps the scheduler from moving weight loads behind the merge arithmetic
   if constexpr (XM == X_ATTN) {
     __builtin_amdgcn_sched_barrier(0);
-    act_load_attn<K, NWB>(a, bat, ar.x);
+    attn_finish<K, NWB>(a, bat, ap, ar.x);
   }
 
   act_prepare(a.eps, ar, s_act);
