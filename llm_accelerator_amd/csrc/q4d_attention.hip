@@ -652,6 +652,9 @@ int launch_attention(const AttnArgs& a, hipStream_t stream) {
       const int nsplit = (a.max_ctx + span - 1) / span;
       hipLaunchKernelGGL(attn_span_kernel, dim3(nsplit, a.kvh, a.batch), dim3(256), 0, stream, a, span);
     }
+  } else if (a.chunk == kAttnChunk) {
+    const int ns = (a.max_ctx + kAttnChunk - 1) / kAttnChunk;
+    hipLaunchKernelGGL(attn_kernel<kAttnChunk>, dim3(ns, a.kvh, a.batch), dim3(256), 0, stream, a);
   } else {
     const int ns = (a.max_ctx + kAttnChunkLong - 1) / kAttnChunkLong;
     hipLaunchKernelGGL(attn_kernel<kAttnChunkLong>, dim3(ns, a.kvh, a.batch), dim3(256), 0, stream, a);

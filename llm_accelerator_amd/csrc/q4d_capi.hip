@@ -152,6 +152,9 @@ int run_layer(const q4d_model_t* m, int l, const float* hin, float* hout, const 
   t.out_dtype = Q4D_F32;
   t.status = status ? status : ws_ptr<int32_t>(ws, W.status);
   t.merge = 0;  // partials only: merged by the o_proj prologue
+  // 64-position chunks give twice the attention blocks; the o_proj prologue merges
+  // up to 8 chunks in one batch of loads, so they are used while 8 cover max_ctx
+  t.chunk = (m->max_ctx + kAttnChunk - 1) / kAttnChunk <= 8 ? kAttnChunk : kAttnChunkLong;
   if ((only < 0 || only == Q4D_STAGE_ATTENTION) && (rc = launch_attention(t, st))) return rc;
 
   // 3. merge the attention partials, o_proj + residual
@@ -160,7 +163,7 @@ int run_layer(const q4d_model_t* m, int l, const float* hin, float* hout, const 
   a.part_acc = t.part_acc;
   a.positions = positions;
   a.nsplit_max = W.nsplit_max;
-  a.attn_chunk = kAttnChunkLong;
+  a.attn_chunk = t.chunk;
   a.y = hout;
   a.resid = hin;
   if ((only < 0 || only == Q4D_STAGE_O_PROJ) && (rc = launch_gemv_xp(a, X_ATTN, xp, EP_RESID, false, st)))

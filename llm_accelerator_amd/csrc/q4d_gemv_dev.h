@@ -211,6 +211,13 @@ __device__ __forceinline__ void act_prepare(float eps, const ActRegs<K, NWB, XM,
       }
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
+        // The hi / lo split needs every use of v to see one fp32 number.  Left
+        // visible, the product above goes into hi's fp16 conversion as one fused
+        // rounding (v_fma_mix) while the stored pair takes the fp32 product, so at
+        // fp16 rounding ties hi, lo and the chunk sums disagree by one fp16 ulp of
+        // hi (found as a 1e-3 relative error of a gate/up row); the empty asm makes
+        // the rounded fp32 value the only one.
+        asm("" : "+v"(v[j]));
         h[j] = (_Float16)v[j];
         if constexpr (XP == 2) l[j] = (_Float16)(v[j] - (float)h[j]);
       }

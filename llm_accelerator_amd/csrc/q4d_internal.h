@@ -144,9 +144,10 @@ struct AttnArgs {
   // fused = 0: q is ready ([batch, qh*d], normed, roped); cache already holds pos.
   int fused;
   // merge = 1: the last block of each (kv head, sequence) merges the chunk
-  // partials into `out`.  merge = 0: partials only (128-position chunks), merged
-  // by the consumer (the o_proj GEMV with X_ATTN).
+  // partials into `out`.  merge = 0: partials only (`chunk` = 64 or 128 positions
+  // per chunk), merged by the consumer (the o_proj GEMV with X_ATTN).
   int merge;
+  int chunk;
   const float* qkv;
   const float* q;
   const float* q_gamma;

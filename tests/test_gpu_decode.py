@@ -13,11 +13,11 @@ GPU, teacher-forced on A's tokens through the C ABI one layer at a time
 q4d_run_one_token makes), so every layer's output can be read.  Stated bars:
   - every layer's hidden state at every position: max-abs error <= 2^-10 * max|A|
     of that layer (one fp16 ulp at the vector's largest element: the fp16 K/V
-    cache is the only fp16 rounding on this path) and <= 1e-4 * max|B| against B;
+    cache is the only fp16 rounding on this path) and <= 2e-5 * max|B| against B;
   - new K/V rows of layers 0/1/27: within 2^-9 * max|row| of A (the cache holds
     fp16; one rounding plus the fp32 error ahead of it) and one fp16 ulp of the
     row's largest element against B;
-  - logits of every generated step: max-abs <= 1e-3 * max|A|, 2e-4 * max|B|;
+  - logits of every generated step: max-abs <= 1e-4 * max|A|, 4e-5 * max|B|;
   - argmax equal to A's token unless a reported near-tie: A's top-2 gap lies
     within the measured error of the two logits involved.
 The measured per-layer max-abs and relative errors are printed (run with -s).
@@ -46,9 +46,9 @@ pytestmark = pytest.mark.gpu
 PROMPT, GEN = 64, 256
 STEPS = PROMPT + GEN - 1          # positions 0 .. 318; generated tokens come from positions 63 .. 318
 KV_LAYERS = (0, 1, 27)
-HIDDEN_BAR_A, HIDDEN_BAR_B = 2.0 ** -10, 1e-4
+HIDDEN_BAR_A, HIDDEN_BAR_B = 2.0 ** -10, 2e-5
 KV_BAR_A = 2.0 ** -9
-LOGIT_BAR_A, LOGIT_BAR_B = 1e-3, 2e-4
+LOGIT_BAR_A, LOGIT_BAR_B = 1e-4, 4e-5
 BITWISE_POSITIONS = (PROMPT - 1, 200, STEPS - 1)
 
 

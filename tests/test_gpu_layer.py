@@ -253,3 +253,36 @@ def test_decoder_layer_long_context(dev, layer_setup, position):
         got = kv.data[0, kind, 0, :, position].float().cpu().numpy()
         ulp_row = np.spacing(np.abs(want).max(axis=-1, keepdims=True).astype(np.float16)).astype(np.float64)
         assert np.all(np.abs(got - want) <= ulp_row), kind
+
+
+@pytest.mark.parametrize("position", [0, 63, 64, 200, 511])
+def test_decoder_layer_64_position_chunks(dev, layer_setup, position):
+    """A context capacity of 512 positions splits batch-1 attention into 64-position
+    chunks (at most 8, merged by the o_proj prologue in one batch of loads); chunk
+    edges and the last slot against the fp16-KV oracle at the layer-test bar."""
+    from llm_accelerator_amd.model import with_context
+    cfg, model, om64, _, _, _, hidden = layer_setup
+    m = with_context(model, 512)
+    rng = np.random.default_rng(1000 + position)
+    kv_k = rng.normal(size=(1, 8, position, 128)).astype(np.float16)
+    kv_v = rng.normal(size=(1, 8, position, 128)).astype(np.float16)
+    kv = KVCache(cfg, 1, 1, m.max_ctx, dev)
+    kv.data[0, 0, 0, :, :position] = torch.from_numpy(kv_k[0]).to(dev)
+    kv.data[0, 1, 0, :, :position] = torch.from_numpy(kv_v[0]).to(dev)
+    lib = _lib.load()
+    desc, kvd = m.descriptor(), kv.descriptor()
+    ws = torch.zeros(int(lib.q4d_workspace_bytes(ctypes.byref(desc), 1)), dtype=torch.uint8, device=dev)
+    check(lib.q4d_workspace_init(ws.data_ptr(), ws.numel(), ctypes.byref(desc), 1, current_stream()), "ws init")
+    h = torch.from_numpy(hidden.reshape(1, 1024)).to(dev)
+    out = torch.empty_like(h)
+    pos = torch.tensor([position], dtype=torch.int32, device=dev)
+    print(f"[layer 64-position chunks] position={position}", flush=True)
+    check(lib.q4d_decoder_layer(ctypes.byref(desc), 0, h.data_ptr(), out.data_ptr(), ctypes.byref(kvd),
+                                pos.data_ptr(), ws.data_ptr(), ws.numel(), current_stream()), "q4d_decoder_layer")
+    ref, kc, vc = o.manual_decoder_layer_cached(hidden.astype(np.float64), om64.layers[0], om64.config, om64.inv_freq,
+                                                np.array([[position]]),
+                                                kv_k.astype(np.float64) if position else None,
+                                                kv_v.astype(np.float64) if position else None,
+                                                kv_store_dtype=np.float16)
+    mx, rel = report(f"layer at position {position} (64-position chunks)", out.cpu().numpy(), ref)
+    assert rel <= 1e-4
