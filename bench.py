@@ -1,37 +1,46 @@
 #!/usr/bin/env python3
 """Benchmark of the Qwen3-0.6B Q4 decode hot path on one MI355X.
 
-Default workload (the headline line): one Qwen3-0.6B decoder layer, one
-decode step at context 512 (hidden 1024, 16 q / 8 kv heads, head_dim 128,
-intermediate 3072, Q4 random-init weights, fp16 KV cache pre-filled with
-N(0,1) for 512 positions).  A "step" is one such layer step.  Weights are
-rotated over ``--copies`` distinct layers (40 x 8.36 MB > the 256 MB
-Infinity Cache), so the headline is the cache-flushed rate; the
-cache-resident rate (one layer repeated) is reported beside it.
+Headline (``value``): one 3072 x 1024 Q4 dequant-GEMV, the Qwen3-0.6B MLP
+gate_proj shape (4-bit codes uniform over 0..15, Q2.14 scales ~ |N(0, 0.02)|
+per 64 columns, fp16 x ~ N(0, 1), batch 1, fp16 y).  A "step" is one GEMV
+launch.  Consecutive steps read distinct copies of the matrix (``--copies`` x
+1.68 MB, above the 256 MB Infinity Cache), so each step streams its weights
+from HBM: the cache-flushed rate.  ``value`` = algorithmic bytes per step
+(1,679,360 B: codes + scales + x + y) / average step time; the step time is
+HIP events around exactly ``--steps`` launches replayed from HIP graphs, after
+an untimed lead-in replay that keeps the GPU busy while the host enqueues the
+timed graphs.  Beside it: the cache-resident rate (one copy, repeated) and a
+measured single-launch floor (the same kernel on a 2 x 1024 matrix: launch,
+one dependent memory round trip and the completion, with no bytes to speak of).
 
-``value`` = algorithmic HBM bytes per step (10,461,184 B: Q4 weights +
-scales, K/V read of 512 positions, new K/V row, hidden in/out) / step time.
-Steps run as HIP-graph replays of ``--copies`` captured layer steps.
+``roofline``: that GEMV kernel; ``traffic`` = its HBM bytes per launch from the
+rocprofv3 FETCH_SIZE / WRITE_SIZE summary under profiles/ (copy-calibrated).
 
-``roofline`` is that of the dominant kernel of the layer step (the stage
-with the largest time, HIP events around graph replays of that stage alone):
-its algorithmic bytes per launch (model.stage_bytes_layer) over its average
-launch time; every stage's rate is listed beside it.
+``decode``: full 28-layer greedy decode, batch 1 (64-token prompt of uniform
+random ids, then 256 generated tokens, the LM-head argmax fed back on the
+device; HIP graphs of 15 steps).  tok/s from HIP events over the 255 feedback
+steps, and its HBM roofline fraction (Q4 weights + the tied table + fp16 K/V
+of every attended position, averaged over the steps, over 8 TB/s).  The
+model's 306 MB of weights exceed the 256 MB cache; ``resident`` repeats the
+loop with every layer aliased to layer 0's weights (91 MB working set) for the
+cache-resident figure.
 
-Also reported (same run, under "extras"): the 3072x1024 Q4 GEMV
-GB/s flushed and resident; the LM head alone; full 28-layer greedy decode
-tok/s (64-token prompt, 256 generated); prefill of one 2048-token
-sequence (tok/s and TFLOP/s against the dense fp16 MFMA peak);
-batched decode of 64 sequences over 4096 cached positions (tok/s
-and GB/s of K/V + weights); the fixed-point (RTL-exact) layer and token;
-bf16 -> Q4 conversion of every matrix of the model (GB/s of bf16 read plus
-codes and scales written); a measured HBM rate (torch's device copy of
-512 MiB windows, read + written bytes) that ``roofline`` also quotes its
-rate against, beside the 8 TB/s vendor figure; and the oracle's CPU rates on
-the host cores (``cpu_baseline``: the layer step on all cores;
-``extras.cpu_legs``: the 3072x1024 GEMV as an fp32 matvec and as the int64 Q26
-restatement, the layer step on one thread, the 28-layer decode per token, the oracle's
-quantizer on a 3072x1024 fp32 matrix).
+``lm_head``: final RMSNorm + 151936 x 1024 Q4 GEMV + argmax alone, flushed
+(rotating over 4 copies of the table, 331 MB) and repeated.
+
+``extras``: one decoder layer's decode step at context 512 (flushed over 40
+distinct layers, resident, per-stage times and rates); prefill of one
+2048-token sequence through 28 layers (tok/s, TFLOP/s against the dense fp16
+MFMA peak); batched decode of 64 sequences over 4096 cached positions; the
+fixed-point (RTL-exact) layer and token; bf16 -> Q4 conversion of every
+matrix; torch's device copy of 512 MiB windows (a measured HBM rate, also
+quoted in ``roofline``); and more CPU legs (``extras.cpu_legs``).
+
+``cpu_baseline``: the oracle's fp32 matvec for the same GEMV (y = x @ W.T on
+the pre-dequantised fp32 matrix, as manual_linear_from_weight computes it,
+common.py:137-145) on the host cores, a ~10 s sample, in GB/s of the same
+algorithmic bytes.
 """
 
 from __future__ import annotations
@@ -39,19 +48,22 @@ from __future__ import annotations
 import argparse
 import ctypes
 import json
-import math
 import os
 import sys
 import time
 
 METRIC = "Q4 GEMV HBM GB/s (% peak) + batch-1 decode tok/s, Qwen3-0.6B-Q4"
+HBM_PEAK_GBPS = 8000.0
 MFMA_PEAK_TFLOPS = 2500.0  # dense fp16
+GEMV_ROWS, GEMV_COLS = 3072, 1024
+PROMPT = 64
+PREFILL_TOKENS = 2048              # prefill of one 2048-token sequence
+BATCH_SEQS, BATCH_CTX = 64, 4096  # batched decode: 64 sequences over 4096 cached positions
 STAGE_KERNELS = {"qkv": "input RMSNorm + q|k|v Q4 GEMV", "attention": "q/k norm + RoPE + KV append + split-K GQA attention",
                  "o_proj": "o_proj Q4 GEMV + residual", "gate_up": "post-norm + gate/up Q4 GEMV + SwiGLU",
                  "down": "down Q4 GEMV + residual"}
-HBM_PEAK_GBPS = 8000.0
-PREFILL_TOKENS = 2048              # prefill of one 2048-token sequence
-BATCH_SEQS, BATCH_CTX = 64, 4096  # batched decode: 64 sequences over 4096 cached positions
+GEMV_KERNEL = "gemv_kernel<1, 4, 0, 1, 0, false, 1>"
+PROFILES = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles")
 
 
 def log(*a):
@@ -61,17 +73,20 @@ def log(*a):
 def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=2000)
-    ap.add_argument("--warmup", type=int, default=200)
-    ap.add_argument("--ctx", type=int, default=512)
-    ap.add_argument("--copies", type=int, default=40)
-    ap.add_argument("--precision", type=int, default=2, choices=(1, 2))
-    ap.add_argument("--no-extras", action="store_true", help="skip every leg beside the layer step")
-    ap.add_argument("--extras", default="gemv,decode,prefill,batch,fx,q4c",
-                    help="comma list of the legs to run beside the layer step: gemv (3072x1024 GEMV), "
-                         "decode (28-layer decode + LM head), prefill, batch (batched decode), "
-                         "fx fixed-point (RTL-exact) layer and token, "
-                         "q4c float -> Q4 conversion of the whole model")
+    ap.add_argument("--steps", type=int, default=2000, help="timed GEMV launches")
+    ap.add_argument("--warmup", type=int, default=200, help="untimed GEMV launches before the timed ones")
+    ap.add_argument("--copies", type=int, default=200, help="distinct copies of the GEMV matrix (flushed rate)")
+    ap.add_argument("--ctx", type=int, default=512, help="context of the decoder-layer leg")
+    ap.add_argument("--layer-copies", type=int, default=40)
+    ap.add_argument("--precision", type=int, default=2, choices=(1, 2),
+                    help="fp32 activations enter the decode GEMVs as fp16 hi+lo pairs (2) or fp16 (1)")
+    ap.add_argument("--no-extras", action="store_true", help="run the GEMV headline only")
+    ap.add_argument("--legs", default="decode,lm,layer,prefill,batch,fx,q4c",
+                    help="comma list of the legs beside the GEMV headline: decode (28-layer decode), "
+                         "lm (LM head alone), "
+                         "layer (one decoder layer at --ctx), prefill, batch (batched decode), "
+                         "fx fixed-point (RTL-exact) layer and token, q4c float -> Q4 conversion of the model")
+    ap.add_argument("--extras", dest="legs", default=argparse.SUPPRESS, help="the same as --legs")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--decode-gen", type=int, default=256)
@@ -104,24 +119,80 @@ def time_graph(g, replays, torch):
     return e0.elapsed_time(e1) / replays
 
 
-def main():
-    args = parse()
-    if args.gpus != 1:
-        sys.exit(f"bench.py measures one GPU only (got --gpus {args.gpus}); this build has no multi-GPU path")
-    import numpy as np
-    import torch
+def load_json(name):
+    path = os.path.join(PROFILES, name)
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        return json.load(f)
 
-    from llm_accelerator_amd import _lib
+
+# ------------------------------------------------------------------ GEMV headline
+def leg_gemv(args, lib, torch, np, dev, st):
+    from llm_accelerator_amd._lib import check
+    from llm_accelerator_amd.model import Q4Tensor, gemv_bytes, random_q4
+    rng = np.random.default_rng(0)
+    packed, scale = random_q4(rng, GEMV_ROWS, GEMV_COLS)
+    ncop = max(1, args.copies)
+    P = torch.from_numpy(packed).to(dev).unsqueeze(0).repeat(ncop, 1, 1).contiguous()
+    S = torch.from_numpy(scale).to(dev).unsqueeze(0).repeat(ncop, 1, 1).contiguous()
+    mats = [Q4Tensor(P[i], S[i]).descriptor() for i in range(ncop)]
+    gen = torch.Generator(device=dev).manual_seed(1)
+    x = torch.randn(1, GEMV_COLS, generator=gen, device=dev).half()
+    y = torch.empty(1, GEMV_ROWS, device=dev, dtype=torch.float16)
+    # the floor: the same kernel on a 2 x 1024 matrix
+    tiny = Q4Tensor(P[0, :2].contiguous(), S[0, :2].contiguous())
+    tiny_desc = tiny.descriptor()
+
+    def launch(m):
+        check(lib.q4d_linear(ctypes.byref(m), x.data_ptr(), 0, y.data_ptr(), 0, 1, st()), "q4d_linear")
+
+    gb = gemv_bytes(GEMV_ROWS, GEMV_COLS)
+    for i in range(args.warmup):
+        launch(mats[i % ncop])
+    torch.cuda.synchronize()
+    # step i of the timed region reads copy i % ncop: full rotations, then the rest
+    full, rest = divmod(args.steps, ncop)
+    g_rot = graph_of(lambda i: launch(mats[i]), ncop, torch)
+    g_rest = graph_of(lambda i: launch(mats[i]), rest, torch) if rest else None
+    g_rot.replay()
+    if g_rest is not None:
+        g_rest.replay()
+    timed = [g_rot] * full + ([g_rest] if g_rest is not None else [])
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    g_rot.replay()                # lead-in, untimed
+    e0.record()
+    for g in timed:
+        g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    us = e0.elapsed_time(e1) * 1e3 / args.steps
+    ok = bool(torch.isfinite(y.float()).all().item())
+    log(f"[bench] GEMV 3072x1024 flushed: {us:.3f} us/launch over {args.steps} launches, "
+        f"{gb / us / 1e3:.1f} GB/s (wall incl. lead-in {wall * 1e3:.2f} ms)")
+
+    g_res = graph_of(lambda i: launch(mats[0]), ncop, torch)
+    g_res.replay()
+    us_res = time_graph(g_res, max(2, args.steps // ncop), torch) / ncop * 1e3
+    g_tiny = graph_of(lambda i: launch(tiny_desc), ncop, torch)
+    g_tiny.replay()
+    us_floor = time_graph(g_tiny, max(2, args.steps // ncop), torch) / ncop * 1e3
+    log(f"[bench] GEMV resident {us_res:.3f} us, single-launch floor (2x1024) {us_floor:.3f} us")
+    out = {"us": us, "GBps": gb / us / 1e3, "bytes": gb, "wall_s": wall, "finite": ok,
+           "resident_us": us_res, "resident_GBps": gb / us_res / 1e3, "floor_us": us_floor}
+    del P, S, g_rot, g_rest, g_res, g_tiny, tiny
+    torch.cuda.empty_cache()
+    return out
+
+
+# ------------------------------------------------------------------ decoder layer
+def leg_layer(args, lib, torch, dev, st):
     from llm_accelerator_amd import model as M
     from llm_accelerator_amd._lib import check
-
-    lib = _lib.load()
-    check(lib.q4d_set_activation_precision(args.precision), "precision")
-    dev = torch.device("cuda:0")
-    st = lambda: torch.cuda.current_stream().cuda_stream  # noqa: E731
-
-    # ------------------------------------------------------------ layer step
-    ctx, copies = args.ctx, args.copies
+    ctx, copies = args.ctx, args.layer_copies
     cfg = M.Qwen3Config(num_hidden_layers=copies, vocab_size=2048)
     t = time.time()
     host = M.random_host_weights(cfg, seed=0, num_layers=copies)
@@ -135,39 +206,22 @@ def main():
     h_in = torch.randn(1, 1024, generator=gen, device=dev, dtype=torch.float32)
     h_out = torch.empty_like(h_in)
     desc, kvd = model.descriptor(), kv.descriptor()
-    log(f"[bench] layer-step setup {time.time() - t:.1f}s: {copies} layers, ctx {ctx}")
+    log(f"[bench] layer setup {time.time() - t:.1f}s: {copies} layers, ctx {ctx}")
 
     def layer_step(i):
         check(lib.q4d_decoder_layer(ctypes.byref(desc), i % copies, h_in.data_ptr(), h_out.data_ptr(),
                                     ctypes.byref(kvd), pos.data_ptr(), ws.ptr, ws.nbytes, st()),
               "q4d_decoder_layer")
 
-    for i in range(args.warmup):
-        layer_step(i)
-    torch.cuda.synchronize()
+    layer_step(0)
     g_flush = graph_of(layer_step, copies, torch)
     g_flush.replay()
-    torch.cuda.synchronize()
-    full, rest = divmod(args.steps, copies)
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(full):
-        g_flush.replay()
-    for i in range(rest):
-        layer_step(i)
-    torch.cuda.synchronize()
-    t1 = time.perf_counter()
-    ms_per_step = (t1 - t0) * 1e3 / args.steps
-    step_bytes = M.algorithmic_bytes_layer(M.Qwen3Config(), ctx)
-    value = step_bytes / (ms_per_step * 1e-3) / 1e9
-    log(f"[bench] layer step flushed: {ms_per_step * 1e3:.2f} us/step, {value:.1f} GB/s")
-
+    reps = 10
+    fl_us = time_graph(g_flush, reps, torch) / copies * 1e3
     g_res = graph_of(lambda i: layer_step(0), copies, torch)
-    res_ms = time_graph(g_res, max(1, args.steps // copies), torch) / copies
-    resident = step_bytes / (res_ms * 1e-3) / 1e9
-    log(f"[bench] layer step resident: {res_ms * 1e3:.2f} us/step, {resident:.1f} GB/s")
-
-    # per-stage durations (graphs of `copies` launches of one stage, HIP events)
+    g_res.replay()
+    res_us = time_graph(g_res, reps, torch) / copies * 1e3
+    step_bytes = M.algorithmic_bytes_layer(M.Qwen3Config(), ctx)
     stage_names = ["qkv", "attention", "o_proj", "gate_up", "down"]
     stage_us = {}
     for sidx, sname in enumerate(stage_names):
@@ -177,285 +231,370 @@ def main():
                   "q4d_layer_stage")
         g = graph_of(stage, copies, torch)
         g.replay()
-        stage_us[sname] = time_graph(g, max(1, args.steps // copies), torch) / copies * 1e3
-    log(f"[bench] stage us (flushed): {json.dumps({k: round(v, 2) for k, v in stage_us.items()})}")
-    # roofline of the dominant kernel (the slowest stage of the layer step):
-    # algorithmic bytes per launch in the dtypes each kernel reads and writes
+        stage_us[sname] = time_graph(g, reps, torch) / copies * 1e3
     stage_bytes = M.stage_bytes_layer(M.Qwen3Config(), ctx)
-    stage_rate = {k: stage_bytes[k] / (stage_us[k] * 1e-6) / 1e9 for k in stage_names}
-    dom = max(stage_names, key=lambda k: stage_us[k])
-    # HBM bytes per launch of that kernel, measured with rocprofv3 FETCH_SIZE /
-    # WRITE_SIZE (copy-calibrated) and committed under profiles/
-    traffic, traffic_src = None, None
-    tfile = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
-                         "decode_layer_ctx512_hbm_traffic.json")
-    if os.path.exists(tfile) and args.precision == 2:
-        with open(tfile) as f:
-            tj = json.load(f)
-        ent = tj["stages"].get(dom) if "stages" in tj else None
-        if ent:
-            traffic, traffic_src = ent["total_bytes"], tj["source"]
-    roofline = {"bound": "hbm", "kernel": f"{dom} stage ({STAGE_KERNELS[dom]})",
-                "achieved": round(stage_rate[dom], 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                "frac": round(stage_rate[dom] / HBM_PEAK_GBPS, 4), "traffic": traffic, "traffic_source": traffic_src,
-                "bytes_per_launch": stage_bytes[dom], "avg_launch_us": round(stage_us[dom], 3),
-                "per_stage_GBps": {k: round(v, 1) for k, v in stage_rate.items()}}
-
-    extras = {"layer_resident_GBps": round(resident, 1), "layer_resident_us_per_step": round(res_ms * 1e3, 3),
-              "layer_flushed_us_per_step": round(ms_per_step * 1e3, 3), "stage_us_flushed": stage_us}
+    out = {"workload": f"one Qwen3-0.6B decoder layer, one decode step at ctx {ctx}, weights rotated over "
+                       f"{copies} distinct layers (flushed) or one layer repeated (resident)",
+           "bytes_per_step": step_bytes, "flushed_us": round(fl_us, 3),
+           "flushed_GBps": round(step_bytes / fl_us / 1e3, 1), "resident_us": round(res_us, 3),
+           "resident_GBps": round(step_bytes / res_us / 1e3, 1),
+           "stage_us_flushed": {k: round(v, 3) for k, v in stage_us.items()},
+           "stage_GBps": {k: round(stage_bytes[k] / stage_us[k] / 1e3, 1) for k in stage_names},
+           "stage_kernels": STAGE_KERNELS}
+    tj = load_json("decode_layer_ctx512_hbm_traffic.json")
+    if tj and ctx == 512 and args.precision == 2:
+        out["stage_traffic_bytes"] = {k: v["total_bytes"] for k, v in tj["stages"].items()}
+        out["stage_traffic_source"] = tj["source"]
+    log(f"[bench] decoder layer: {json.dumps(out)}")
     del model, kv, ws, g_flush, g_res
     torch.cuda.empty_cache()
+    return out
 
-    legs = set() if args.no_extras else {x.strip() for x in args.extras.split(",") if x.strip()}
-    known = {"gemv", "decode", "prefill", "batch", "fx", "q4c"}
+
+# ------------------------------------------------------------------ 28-layer decode
+def aliased_descriptor(model):
+    """The model's descriptor with every layer pointing at layer 0's weights."""
+    from llm_accelerator_amd._lib import Q4dLayer, Q4dModel
+    d0 = model.descriptor()
+    n = d0.num_layers
+    arr = (Q4dLayer * n)(*([d0.layers[0]] * n))
+    d = Q4dModel.from_buffer_copy(d0)
+    d.layers = ctypes.cast(arr, ctypes.POINTER(Q4dLayer))
+    d._layers_keepalive = arr  # type: ignore[attr-defined]
+    return d
+
+
+def run_decode(fmodel, prompt, gen_steps, per_graph, torch, desc=None):
+    from llm_accelerator_amd.decode import GreedyDecoder
+    dec = GreedyDecoder(fmodel, steps_per_graph=per_graph, use_graph=True)
+    if desc is not None:
+        dec._desc = desc   # noqa: SLF001  (the aliased-weights variant)
+    dec.prefill(prompt)
+    dec.generate(per_graph)        # captures and warms the graph
+    dec.prefill(prompt)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record()
+    dec.generate(gen_steps)
+    e1.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms = e0.elapsed_time(e1)
+    toks, _ = dec.history()
+    out = {"us_per_token": ms * 1e3 / gen_steps, "wall_us_per_token": wall * 1e6 / gen_steps,
+           "generated": len(toks), "status": dec.status()}
+    del dec
+    return out
+
+
+def leg_decode(args, torch, np, fmodel):
+    from llm_accelerator_amd import model as M
+    fcfg = fmodel.config
+    prompt = np.random.default_rng(1).integers(0, fcfg.vocab_size, PROMPT).tolist()
+    steps = args.decode_gen - 1                     # token 0 comes from the last prompt step
+    per_graph = max(d for d in range(1, 17) if steps % d == 0)
+    flushed = run_decode(fmodel, prompt, steps, per_graph, torch)
+    resident = run_decode(fmodel, prompt, steps, per_graph, torch, desc=aliased_descriptor(fmodel))
+    # step p feeds position p and attends p + 1 positions
+    tok_bytes = sum(M.batched_step_bytes(fcfg, 1, p + 1) for p in range(PROMPT, PROMPT + steps)) / steps
+    wb = fmodel.weight_bytes()
+    res_bytes = tok_bytes - (wb["per_layer"] * (fcfg.num_hidden_layers - 1))
+    tok_s = 1e6 / flushed["us_per_token"]
+    out = {"workload": f"28-layer greedy decode, batch 1: {PROMPT}-token uniform random prompt, "
+                       f"{args.decode_gen} generated (argmax fed back on the device, HIP graphs of {per_graph} steps)",
+           "tok_s": round(tok_s, 1), "us_per_token": round(flushed["us_per_token"], 2),
+           "wall_us_per_token": round(flushed["wall_us_per_token"], 2),
+           "bytes_per_token": int(tok_bytes), "GBps": round(tok_bytes * tok_s / 1e9, 1),
+           "roofline_frac": round(tok_bytes * tok_s / 1e9 / HBM_PEAK_GBPS, 4),
+           "generated": flushed["generated"], "status": flushed["status"],
+           "launches_per_token": 2 + 5 * fcfg.num_hidden_layers + 1,
+           "resident": {"note": "every layer aliased to layer 0's weights: 91 MB per token, inside the 256 MB cache",
+                        "tok_s": round(1e6 / resident["us_per_token"], 1),
+                        "us_per_token": round(resident["us_per_token"], 2),
+                        "bytes_per_token": int(res_bytes), "status": resident["status"]}}
+    log(f"[bench] 28-layer decode: {json.dumps(out)}")
+    return out
+
+
+def leg_lm(lib, torch, dev, st, fmodel):
+    """Final RMSNorm + 151936x1024 Q4 GEMV + argmax alone, rotating over 4 copies
+    of the table (flushed) and on one copy (repeated)."""
+    from llm_accelerator_amd import model as M
+    from llm_accelerator_amd._lib import Q4dMatrix, Q4dModel, check
+    fcfg = fmodel.config
+    lw = fmodel.lm_head.weight
+    copies = [lw] + [type(lw)(lw.packed.clone(), lw.scale.clone()) for _ in range(3)]
+    base = fmodel.descriptor()
+    descs = []
+    for c in copies:
+        d = Q4dModel.from_buffer_copy(base)
+        d.embed_tokens = Q4dMatrix(c.packed.data_ptr(), c.scale.data_ptr(), fcfg.vocab_size, fcfg.hidden_size)
+        descs.append(d)
+    gen = torch.Generator(device=dev).manual_seed(3)
+    hid = torch.randn(1, fcfg.hidden_size, generator=gen, device=dev)
+    lm_tok = torch.zeros(1, dtype=torch.int32, device=dev)
+    lm_score = torch.zeros(1, dtype=torch.float32, device=dev)
+    lws = M.Workspace(fmodel, 1)
+
+    def lm_head(d):
+        check(lib.q4d_lm_head_argmax(ctypes.byref(d), hid.data_ptr(), lm_tok.data_ptr(), lm_score.data_ptr(),
+                                     None, lws.ptr, lws.nbytes, st()), "lm_head")
+    g_fl = graph_of(lambda i: lm_head(descs[i % 4]), 8, torch)
+    g_rp = graph_of(lambda i: lm_head(descs[0]), 8, torch)
+    g_fl.replay()
+    g_rp.replay()
+    fl_us = time_graph(g_fl, 10, torch) / 8 * 1e3
+    rp_us = time_graph(g_rp, 10, torch) / 8 * 1e3
+    lm_bytes = lw.nbytes + 4 * fcfg.hidden_size * 2
+    lm = {"workload": "final RMSNorm + 151936x1024 Q4 GEMV + argmax; flushed = rotating over 4 copies of the "
+                      "table (331 MB), repeated = one copy", "bytes": lm_bytes,
+          "flushed_us": round(fl_us, 2), "flushed_GBps": round(lm_bytes / fl_us / 1e3, 1),
+          "flushed_frac": round(lm_bytes / fl_us / 1e3 / HBM_PEAK_GBPS, 4),
+          "repeated_us": round(rp_us, 2), "repeated_GBps": round(lm_bytes / rp_us / 1e3, 1)}
+    tj = load_json("lm_head_hbm_traffic.json")
+    if tj:
+        lm["traffic"] = tj.get("total_bytes")
+        lm["traffic_source"] = tj.get("source")
+    log(f"[bench] LM head: {json.dumps(lm)}")
+    del copies, descs, lws, g_fl, g_rp
+    torch.cuda.empty_cache()
+    return lm
+
+
+# ------------------------------------------------------------------ prefill, batched, fixed point, Q4 conversion
+def leg_prefill(torch, np, dev, fmodel):
+    from llm_accelerator_amd import model as M
+    from llm_accelerator_amd.decode import Prefill
+    fcfg = fmodel.config
+    T = PREFILL_TOKENS
+    pkv = M.KVCache(fcfg, fcfg.num_hidden_layers, 1, fmodel.max_ctx, dev)
+    pf = Prefill(fmodel, pkv, T)
+    ptok = torch.from_numpy(np.random.default_rng(4).integers(0, fcfg.vocab_size, T).astype(np.int32)).to(dev)
+    pf.run(ptok)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(5):
+        pf.run(ptok)
+    e1.record()
+    torch.cuda.synchronize()
+    pms = e0.elapsed_time(e1) / 5
+    pflops = M.prefill_flops(fcfg, T)
+    out = {"tokens": T, "ms": round(pms, 3), "tok_s": round(T / pms * 1e3, 1),
+           "TFLOPs": round(pflops / pms / 1e9, 1), "flops": pflops,
+           "mfma_frac": round(pflops / pms / 1e9 / MFMA_PEAK_TFLOPS, 4)}
+    log(f"[bench] prefill 2048: {json.dumps(out)}")
+    del pkv, pf
+    torch.cuda.empty_cache()
+    return out
+
+
+def leg_batch(torch, np, dev, fmodel):
+    from llm_accelerator_amd import model as M
+    from llm_accelerator_amd.decode import BatchedDecoder
+    fcfg = fmodel.config
+    B = BATCH_SEQS
+    gen = torch.Generator(device=dev).manual_seed(5)
+    bkv = M.KVCache(fcfg, fcfg.num_hidden_layers, B, BATCH_CTX + 1, dev)
+    bkv.data[..., :BATCH_CTX, :].normal_(generator=gen)
+    bd = BatchedDecoder(fmodel, B, bkv)
+    btok = torch.from_numpy(np.random.default_rng(3).integers(0, fcfg.vocab_size, B).astype(np.int32)).to(dev)
+    bpos = torch.full((B,), BATCH_CTX, dtype=torch.int32, device=dev)
+    bd.step(btok, bpos)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(5):
+        bd.step(btok, bpos)
+    e1.record()
+    torch.cuda.synchronize()
+    bms = e0.elapsed_time(e1) / 5
+    bbytes = M.batched_step_bytes(fcfg, B, BATCH_CTX)
+    out = {"batch": B, "ctx": BATCH_CTX, "ms_per_step": round(bms, 3), "tok_s": round(B / bms * 1e3, 1),
+           "bytes_per_step": bbytes, "GBps": round(bbytes / bms / 1e6, 1),
+           "hbm_frac": round(bbytes / bms / 1e6 / HBM_PEAK_GBPS, 4), "status": bd.status()}
+    log(f"[bench] batched decode 64x4096: {json.dumps(out)}")
+    del bkv, bd
+    torch.cuda.empty_cache()
+    return out
+
+
+def leg_fixed(args, lib, torch, dev, st, fmodel, fnorms):
+    from llm_accelerator_amd import model as M
+    from llm_accelerator_amd._lib import check
+    from llm_accelerator_amd.fixed import FixedQ4Model
+    fcfg = fmodel.config
+    ctx = args.ctx
+    gen = torch.Generator(device=dev).manual_seed(6)
+    fxm = FixedQ4Model(M.with_context(fmodel, ctx + 1), fnorms)
+    fkv = fxm.new_cache()
+    fkv.data.copy_(torch.randint(-8192, 8192, fkv.data.shape, generator=gen, device=dev, dtype=torch.int32))
+    fdesc, fkvd = fxm.descriptor(), fkv.descriptor()
+    fpos = torch.tensor([ctx], dtype=torch.int32, device=dev)
+    fh = torch.randint(-4096, 4096, (1024,), generator=gen, device=dev, dtype=torch.int32)
+    fo = torch.empty_like(fh)
+
+    def fx_layer(i):
+        check(lib.q4d_fixed_decoder_layer(ctypes.byref(fdesc), i, fh.data_ptr(), fo.data_ptr(),
+                                          ctypes.byref(fkvd), fpos.data_ptr(), fxm.ws.data_ptr(), fxm.ws_bytes,
+                                          st()), "q4d_fixed_decoder_layer")
+    L = fcfg.num_hidden_layers
+    g_fx = graph_of(fx_layer, L, torch)
+    g_fx.replay()
+    fx_us = time_graph(g_fx, 10, torch) / L * 1e3
+    fx_bytes = M.fixed_layer_bytes(fcfg, ctx)
+    # one-token steps: serial prompt of 64 tokens, then graphs of 16 steps feeding the argmax back
+    ftok = torch.tensor([1], dtype=torch.int32, device=dev)
+    fnxt = torch.zeros(1, dtype=torch.int32, device=dev)
+    fscore = torch.zeros(1, dtype=torch.int64, device=dev)
+    fpos.zero_()
+
+    def fx_token(i):
+        check(lib.q4d_fixed_run_one_token(ctypes.byref(fdesc), ftok.data_ptr(), fpos.data_ptr(),
+                                          ctypes.byref(fkvd), fnxt.data_ptr(), fscore.data_ptr(), None, None,
+                                          fxm.ws.data_ptr(), fxm.ws_bytes, st()), "q4d_fixed_run_one_token")
+        ftok.copy_(fnxt)
+        fpos.add_(1)
+    for i in range(64):
+        fx_token(i)
+    g_tok = graph_of(fx_token, 16, torch)
+    g_tok.replay()
+    tok_ms = time_graph(g_tok, (args.decode_gen - 16) // 16, torch) / 16
+    counts = fxm.counts()
+    out = {"layer_us": round(fx_us, 3), "layer_bytes": fx_bytes, "layer_GBps": round(fx_bytes / fx_us / 1e3, 1),
+           "token_ms": round(tok_ms, 4), "tok_s": round(1e3 / tok_ms, 1), "positions": [64, int(fpos.item())],
+           "status": counts["status"]}
+    log(f"[bench] fixed-point decode: {json.dumps(out)}")
+    del fxm, fkv, g_fx, g_tok
+    torch.cuda.empty_cache()
+    return out
+
+
+def leg_q4c(lib, torch, dev, st):
+    from llm_accelerator_amd import model as M
+    from llm_accelerator_amd._lib import check
+    qcfg = M.Qwen3Config()
+    gen = torch.Generator(device=dev).manual_seed(7)
+    h, I = qcfg.hidden_size, qcfg.intermediate_size
+    shapes = [(2048, h), (1024, h), (1024, h), (h, 2048), (I, h), (I, h), (h, I)] * qcfg.num_hidden_layers
+    shapes.append((qcfg.vocab_size, h))
+    mats = [(torch.randn(r, c, generator=gen, device=dev) * 0.03).to(torch.bfloat16) for r, c in shapes]
+    outs = [(torch.empty(r, c // 2, dtype=torch.uint8, device=dev),
+             torch.empty(r, c // 64, dtype=torch.uint16, device=dev)) for r, c in shapes]
+    qstatus = torch.zeros(2, dtype=torch.int32, device=dev)
+
+    def quant(i):
+        w, (pk, sc) = mats[i], outs[i]
+        check(lib.q4d_quantize_q4(w.data_ptr(), 2, w.shape[1], w.shape[0], w.shape[1], pk.data_ptr(),
+                                  sc.data_ptr(), qstatus.data_ptr(), st()), "q4d_quantize_q4")
+    for i in range(len(shapes)):
+        quant(i)
+    torch.cuda.synchronize()
+    # HIP graphs: one of the 197 conversions, one of the table alone
+    g_all = graph_of(quant, len(shapes), torch)
+    g_tab = graph_of(lambda i: quant(len(shapes) - 1), 1, torch)
+    g_all.replay()
+    g_tab.replay()
+    all_ms = time_graph(g_all, 10, torch)
+    emb_us = time_graph(g_tab, 20, torch) * 1e3
+    params = sum(r * c for r, c in shapes)
+    qbytes = params * 2 + params // 2 + params // 64 * 2   # bf16 in, codes + Q2.14 scales out
+    er, ec = shapes[-1]
+    ebytes = er * ec * 2 + er * ec // 2 + er * ec // 64 * 2
+    out = {"workload": "bf16 -> Q4 of every Qwen3-0.6B projection and the tied table (197 matrices)",
+           "params": params, "bytes": qbytes, "ms": round(all_ms, 4), "GBps": round(qbytes / all_ms / 1e6, 1),
+           "hbm_frac": round(qbytes / all_ms / 1e6 / HBM_PEAK_GBPS, 4), "table_us": round(emb_us, 2),
+           "table_GBps": round(ebytes / emb_us / 1e3, 1), "status": qstatus.tolist()}
+    log(f"[bench] Q4 conversion: {json.dumps(out)}")
+    del mats, outs, g_all, g_tab
+    torch.cuda.empty_cache()
+    return out
+
+
+def leg_copy(torch, dev):
+    """torch's device copy of 512 MiB windows rotating over 2 GiB (past the 256 MB
+    cache): read + written bytes over the time."""
+    buf = torch.empty(2 << 30, dtype=torch.uint8, device=dev)
+    w = 512 << 20
+    for _ in range(2):
+        buf[w:2 * w].copy_(buf[:w])
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for i in range(8):
+        k = i % 2
+        buf[(2 * k + 1) * w:(2 * k + 2) * w].copy_(buf[2 * k * w:(2 * k + 1) * w])
+    e1.record()
+    torch.cuda.synchronize()
+    cms = e0.elapsed_time(e1) / 8
+    out = {"bytes_moved": 2 * w, "us": round(cms * 1e3, 1), "GBps": round(2 * w / (cms * 1e-3) / 1e9, 1)}
+    log(f"[bench] measured copy: {json.dumps(out)}")
+    del buf
+    torch.cuda.empty_cache()
+    return out
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        sys.exit(f"bench.py measures one GPU only (got --gpus {args.gpus}); this build has no multi-GPU path")
+    if args.steps < 1 or args.warmup < 0:
+        sys.exit("--steps must be >= 1 and --warmup >= 0")
+    import numpy as np
+    import torch
+
+    from llm_accelerator_amd import _lib
+    from llm_accelerator_amd import model as M
+    from llm_accelerator_amd._lib import check
+
+    lib = _lib.load()
+    check(lib.q4d_set_activation_precision(args.precision), "precision")
+    dev = torch.device("cuda:0")
+    st = lambda: torch.cuda.current_stream().cuda_stream  # noqa: E731
+
+    legs = set() if args.no_extras else {x.strip() for x in args.legs.split(",") if x.strip()}
+    known = {"decode", "lm", "layer", "prefill", "batch", "fx", "q4c"}
     if legs - known:
         sys.exit(f"unknown legs {sorted(legs - known)}")
-    if "gemv" in legs:
-        # -------------------------------------------------------- 3072x1024 GEMV
-        from llm_accelerator_amd.model import Q4Tensor, gemv_bytes, random_q4
-        rng = np.random.default_rng(0)
-        packed, scale = random_q4(rng, 3072, 1024)
-        ncop = 200
-        P = torch.from_numpy(packed).to(dev).unsqueeze(0).repeat(ncop, 1, 1).contiguous()
-        S = torch.from_numpy(scale).to(dev).unsqueeze(0).repeat(ncop, 1, 1).contiguous()
-        mats = [Q4Tensor(P[i], S[i]).descriptor() for i in range(ncop)]
-        x = torch.randn(1, 1024, generator=gen, device=dev).half()
-        y = torch.empty(1, 3072, device=dev, dtype=torch.float16)
 
-        def gemv(i, fixed=False):
-            m = mats[0 if fixed else i]
-            check(lib.q4d_linear(ctypes.byref(m), x.data_ptr(), 0, y.data_ptr(), 0, 1, st()), "q4d_linear")
-        gb = gemv_bytes(3072, 1024)
-        g1 = graph_of(gemv, ncop, torch)
-        us_fl = time_graph(g1, 20, torch) / ncop * 1e3
-        g2 = graph_of(lambda i: gemv(i, True), ncop, torch)
-        us_res = time_graph(g2, 20, torch) / ncop * 1e3
-        extras["gemv_3072x1024"] = {"shape": "3072x1024 q4, fp16 x/y", "bytes": gb,
-                             "flushed_us": round(us_fl, 3), "flushed_GBps": round(gb / us_fl / 1e3, 1),
-                             "resident_us": round(us_res, 3), "resident_GBps": round(gb / us_res / 1e3, 1)}
-        log(f"[bench] GEMV 3072x1024: {json.dumps(extras['gemv_3072x1024'])}")
-        del P, S, g1, g2
-        torch.cuda.empty_cache()
+    gemv = leg_gemv(args, lib, torch, np, dev, st)
+    extras = {"gemv_resident_us": round(gemv["resident_us"], 3),
+              "gemv_resident_GBps": round(gemv["resident_GBps"], 1)}
+    if "layer" in legs:
+        extras["decoder_layer"] = leg_layer(args, lib, torch, dev, st)
 
-    if legs & {"decode", "prefill", "batch", "fx"}:
+    decode = lm = None
+    if legs & {"decode", "lm", "prefill", "batch", "fx"}:
         fcfg = M.Qwen3Config()
         t = time.time()
         fhost = M.random_host_weights(fcfg, seed=0)
-        fmodel = M.build_model(fcfg, fhost, max_ctx=max(64 + args.decode_gen + 16, BATCH_CTX + 1), device=dev)
+        fmodel = M.build_model(fcfg, fhost, max_ctx=max(PROMPT + args.decode_gen + 16, BATCH_CTX + 1), device=dev)
         norm_keys = ("input_layernorm", "post_attention_layernorm", "q_norm", "k_norm")
         fnorms = {"layers": [{k: L[k] for k in norm_keys} for L in fhost["layers"]], "norm": fhost["norm"]}
         del fhost
         log(f"[bench] 28-layer model setup {time.time() - t:.1f}s")
-    if "decode" in legs:
-        # -------------------------------------------------------- 28-layer decode tok/s
-        from llm_accelerator_amd.decode import GreedyDecoder
-        prompt = np.random.default_rng(1).integers(0, fcfg.vocab_size, 64).tolist()
-        dec = GreedyDecoder(fmodel, steps_per_graph=16, use_graph=True)
-        dec.prefill(prompt)
-        dec.generate(16)  # captures and warms the graph
-        torch.cuda.synchronize()
-        dec.prefill(prompt)
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        dec.prefill(prompt)
-        torch.cuda.synchronize()
-        t_pre = time.perf_counter() - t0
-        t0 = time.perf_counter()
-        dec.generate(args.decode_gen - 1)
-        torch.cuda.synchronize()
-        t_gen = time.perf_counter() - t0
-        toks, _ = dec.history()
-        # LM head alone: final RMSNorm + 151936x1024 Q4 GEMV + argmax
-        lm_desc = fmodel.descriptor()
-        hid = torch.randn(1, 1024, generator=gen, device=dev)
-        lm_tok = torch.zeros(1, dtype=torch.int32, device=dev)
-        lm_score = torch.zeros(1, dtype=torch.float32, device=dev)
-        lws = M.Workspace(fmodel, 1)
-
-        def lm_head(i):
-            check(lib.q4d_lm_head_argmax(ctypes.byref(lm_desc), hid.data_ptr(), lm_tok.data_ptr(),
-                                         lm_score.data_ptr(), None, lws.ptr, lws.nbytes, st()), "lm_head")
-        g_lm = graph_of(lm_head, 10, torch)
-        g_lm.replay()
-        lm_us = time_graph(g_lm, 10, torch) / 10 * 1e3
-        lm_bytes = wb_lm = fmodel.lm_head.weight.nbytes + 4 * 1024
-        extras["lm_head"] = {"us": round(lm_us, 2), "bytes": wb_lm, "GBps": round(lm_bytes / lm_us / 1e3, 1)}
-        log(f"[bench] LM head: {json.dumps(extras['lm_head'])}")
-        wb = fmodel.weight_bytes()
-        avg_ctx = 64 + args.decode_gen / 2
-        tok_bytes = wb["total"] + 2 * 2 * 1024 * avg_ctx * 28
-        tok_s = (args.decode_gen - 1) / t_gen
-        extras["decode_28_layers"] = {"prompt": 64, "generated": len(toks), "tok_s": round(tok_s, 1),
-                               "us_per_token": round(1e6 / tok_s, 2),
-                               "serial_prefill_tok_s": round(64 / t_pre, 1),
-                               "GBps_equiv": round(tok_bytes * tok_s / 1e9, 1),
-                               "hbm_frac": round(tok_bytes * tok_s / 1e9 / HBM_PEAK_GBPS, 4),
-                               "status": dec.status()}
-        log(f"[bench] 28-layer decode: {json.dumps(extras['decode_28_layers'])}")
-        del dec, lws
-        torch.cuda.empty_cache()
-
-    if "prefill" in legs:
-        # -------------------------------------------------------- prefill of 2048 tokens
-        from llm_accelerator_amd.decode import Prefill
-        T = PREFILL_TOKENS
-        pkv = M.KVCache(fcfg, fcfg.num_hidden_layers, 1, fmodel.max_ctx, dev)
-        pf = Prefill(fmodel, pkv, T)
-        ptok = torch.from_numpy(np.random.default_rng(4).integers(0, fcfg.vocab_size, T).astype(np.int32)).to(dev)
-        pf.run(ptok)
-        torch.cuda.synchronize()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record()
-        for _ in range(5):
-            pf.run(ptok)
-        e1.record()
-        torch.cuda.synchronize()
-        pms = e0.elapsed_time(e1) / 5
-        pflops = M.prefill_flops(fcfg, T)
-        extras["prefill_2048"] = {"tokens": T, "ms": round(pms, 3), "tok_s": round(T / pms * 1e3, 1),
-                                "TFLOPs": round(pflops / pms / 1e9, 1), "flops": pflops,
-                                "mfma_frac": round(pflops / pms / 1e9 / MFMA_PEAK_TFLOPS, 4)}
-        log(f"[bench] prefill 2048: {json.dumps(extras['prefill_2048'])}")
-        del pkv, pf
-        torch.cuda.empty_cache()
-
-    if "batch" in legs:
-        # -------------------------------------------------------- batched decode 64 x 4096
-        from llm_accelerator_amd.decode import BatchedDecoder
-        B = BATCH_SEQS
-        bkv = M.KVCache(fcfg, fcfg.num_hidden_layers, B, BATCH_CTX + 1, dev)
-        bkv.data[..., :BATCH_CTX, :].normal_(generator=gen)
-        bd = BatchedDecoder(fmodel, B, bkv)
-        btok = torch.from_numpy(np.random.default_rng(3).integers(0, fcfg.vocab_size, B).astype(np.int32)).to(dev)
-        bpos = torch.full((B,), BATCH_CTX, dtype=torch.int32, device=dev)
-        bd.step(btok, bpos)
-        torch.cuda.synchronize()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record()
-        for _ in range(5):
-            bd.step(btok, bpos)
-        e1.record()
-        torch.cuda.synchronize()
-        bms = e0.elapsed_time(e1) / 5
-        bbytes = M.batched_step_bytes(fcfg, B, BATCH_CTX)
-        extras["batched_decode_64x4096"] = {"batch": B, "ctx": BATCH_CTX, "ms_per_step": round(bms, 3),
-                                       "tok_s": round(B / bms * 1e3, 1), "bytes_per_step": bbytes,
-                                       "GBps": round(bbytes / bms / 1e6, 1),
-                                       "hbm_frac": round(bbytes / bms / 1e6 / HBM_PEAK_GBPS, 4),
-                                       "status": bd.status()}
-        log(f"[bench] batched decode 64x4096: {json.dumps(extras['batched_decode_64x4096'])}")
-        del bkv, bd
-    if "fx" in legs:
-        # -------------------------------------------------------- fixed-point (RTL-exact) decode
-        from llm_accelerator_amd.fixed import FixedQ4Model
-        fxm = FixedQ4Model(M.with_context(fmodel, ctx + 1), fnorms)
-        fkv = fxm.new_cache()
-        fkv.data.copy_(torch.randint(-8192, 8192, fkv.data.shape, generator=gen, device=dev, dtype=torch.int32))
-        fdesc, fkvd = fxm.descriptor(), fkv.descriptor()
-        fpos = torch.tensor([ctx], dtype=torch.int32, device=dev)
-        fh = torch.randint(-4096, 4096, (1024,), generator=gen, device=dev, dtype=torch.int32)
-        fo = torch.empty_like(fh)
-
-        def fx_layer(i):
-            check(lib.q4d_fixed_decoder_layer(ctypes.byref(fdesc), i, fh.data_ptr(), fo.data_ptr(),
-                                              ctypes.byref(fkvd), fpos.data_ptr(), fxm.ws.data_ptr(), fxm.ws_bytes,
-                                              st()), "q4d_fixed_decoder_layer")
-        L = fcfg.num_hidden_layers
-        g_fx = graph_of(fx_layer, L, torch)
-        g_fx.replay()
-        fx_us = time_graph(g_fx, 10, torch) / L * 1e3
-        fx_bytes = M.fixed_layer_bytes(fcfg, ctx)
-        # one-token steps: serial prompt of 64 tokens, then graphs of 16 steps feeding the argmax back
-        ftok = torch.tensor([1], dtype=torch.int32, device=dev)
-        fnxt = torch.zeros(1, dtype=torch.int32, device=dev)
-        fscore = torch.zeros(1, dtype=torch.int64, device=dev)
-        fpos.zero_()
-
-        def fx_token(i):
-            check(lib.q4d_fixed_run_one_token(ctypes.byref(fdesc), ftok.data_ptr(), fpos.data_ptr(),
-                                              ctypes.byref(fkvd), fnxt.data_ptr(), fscore.data_ptr(), None, None,
-                                              fxm.ws.data_ptr(), fxm.ws_bytes, st()), "q4d_fixed_run_one_token")
-            ftok.copy_(fnxt)
-            fpos.add_(1)
-        for i in range(64):
-            fx_token(i)
-        g_tok = graph_of(fx_token, 16, torch)
-        g_tok.replay()
-        tok_ms = time_graph(g_tok, (args.decode_gen - 16) // 16, torch) / 16
-        counts = fxm.counts()
-        extras["fx_fixed_point"] = {
-            "layer_us": round(fx_us, 3), "layer_bytes": fx_bytes, "layer_GBps": round(fx_bytes / fx_us / 1e3, 1),
-            "token_ms": round(tok_ms, 4), "tok_s": round(1e3 / tok_ms, 1), "positions": [64, int(fpos.item())],
-            "status": counts["status"]}
-        log(f"[bench] fixed-point decode: {json.dumps(extras['fx_fixed_point'])}")
-        del fxm, fkv, g_fx, g_tok
-    if legs & {"decode", "prefill", "batch", "fx"}:
+        if "decode" in legs:
+            # decode at its own context capacity (prompt + generated), as a caller would size it
+            decode = leg_decode(args, torch, np, M.with_context(fmodel, PROMPT + args.decode_gen + 16))
+        if "lm" in legs:
+            lm = leg_lm(lib, torch, dev, st, fmodel)
+        if "prefill" in legs:
+            extras["prefill_2048"] = leg_prefill(torch, np, dev, fmodel)
+        if "batch" in legs:
+            extras["batched_decode_64x4096"] = leg_batch(torch, np, dev, fmodel)
+        if "fx" in legs:
+            extras["fx_fixed_point"] = leg_fixed(args, lib, torch, dev, st, fmodel, fnorms)
         del fmodel
         torch.cuda.empty_cache()
     if "q4c" in legs:
-        # -------------------------------------------------------- float -> Q4 conversion of the whole model
-        qcfg = M.Qwen3Config()
-        h, I = qcfg.hidden_size, qcfg.intermediate_size
-        shapes = [(2048, h), (1024, h), (1024, h), (h, 2048), (I, h), (I, h), (h, I)] * qcfg.num_hidden_layers
-        shapes.append((qcfg.vocab_size, h))
-        mats = [(torch.randn(r, c, generator=gen, device=dev) * 0.03).to(torch.bfloat16) for r, c in shapes]
-        outs = [(torch.empty(r, c // 2, dtype=torch.uint8, device=dev),
-                 torch.empty(r, c // 64, dtype=torch.uint16, device=dev)) for r, c in shapes]
-        qstatus = torch.zeros(2, dtype=torch.int32, device=dev)
-
-        def quant(i):
-            w, (pk, sc) = mats[i], outs[i]
-            check(lib.q4d_quantize_q4(w.data_ptr(), 2, w.shape[1], w.shape[0], w.shape[1], pk.data_ptr(),
-                                      sc.data_ptr(), qstatus.data_ptr(), st()), "q4d_quantize_q4")
-        for i in range(len(shapes)):
-            quant(i)
-        torch.cuda.synchronize()
-        # HIP graphs: one of the 197 conversions, one of the table alone
-        g_all = graph_of(quant, len(shapes), torch)
-        g_tab = graph_of(lambda i: quant(len(shapes) - 1), 1, torch)
-        g_all.replay()
-        g_tab.replay()
-        all_ms = time_graph(g_all, 10, torch)
-        emb_us = time_graph(g_tab, 20, torch) * 1e3
-        params = sum(r * c for r, c in shapes)
-        qbytes = params * 2 + params // 2 + params // 64 * 2   # bf16 in, codes + Q2.14 scales out
-        er, ec = shapes[-1]
-        ebytes = er * ec * 2 + er * ec // 2 + er * ec // 64 * 2
-        extras["q4c_quantize"] = {
-            "workload": "bf16 -> Q4 of every Qwen3-0.6B projection and the tied table (197 matrices)",
-            "params": params, "bytes": qbytes, "ms": round(all_ms, 4), "GBps": round(qbytes / all_ms / 1e6, 1),
-            "hbm_frac": round(qbytes / all_ms / 1e6 / HBM_PEAK_GBPS, 4), "table_us": round(emb_us, 2),
-            "table_GBps": round(ebytes / emb_us / 1e3, 1), "status": qstatus.tolist()}
-        log(f"[bench] Q4 conversion: {json.dumps(extras['q4c_quantize'])}")
-        del mats, outs, g_all, g_tab
-        torch.cuda.empty_cache()
-
+        extras["q4c_quantize"] = leg_q4c(lib, torch, dev, st)
     if legs:
-        # measured HBM ceiling beside the 8 TB/s vendor figure: torch's device
-        # copy of 512 MiB windows rotating over 2 GiB (past the 256 MB cache),
-        # read + written bytes over the time
-        buf = torch.empty(2 << 30, dtype=torch.uint8, device=dev)
-        w = 512 << 20
-        for _ in range(2):
-            buf[w:2 * w].copy_(buf[:w])
-        torch.cuda.synchronize()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record()
-        for i in range(8):
-            k = i % 2
-            buf[(2 * k + 1) * w:(2 * k + 2) * w].copy_(buf[2 * k * w:(2 * k + 1) * w])
-        e1.record()
-        torch.cuda.synchronize()
-        cms = e0.elapsed_time(e1) / 8
-        extras["hbm_copy"] = {"bytes_moved": 2 * w, "us": round(cms * 1e3, 1),
-                              "GBps": round(2 * w / (cms * 1e-3) / 1e9, 1)}
-        log(f"[bench] measured copy: {json.dumps(extras['hbm_copy'])}")
-        del buf
-        torch.cuda.empty_cache()
+        extras["hbm_copy"] = leg_copy(torch, dev)
 
     if args.copy_calibration:
         # a plain copy of known size: its FETCH_SIZE / WRITE_SIZE per dispatch
-        # converts the counters of the GEMV dispatches to bytes
+        # converts the counters of the other dispatches to bytes
         src = torch.empty(256 << 20, dtype=torch.uint8, device=dev)
         dst = torch.empty_like(src)
         for _ in range(3):
@@ -465,30 +604,50 @@ def main():
         del src, dst
 
     cpu = None
-    if not args.no_cpu and legs:
-        cpu = cpu_baseline(args.cpu_seconds, ctx, step_bytes)
+    if not args.no_cpu:
+        cpu = cpu_baseline(args.cpu_seconds)
         log(f"[bench] CPU baseline: {json.dumps(cpu)}")
-        extras["cpu_legs"] = cpu_extra_legs(ctx, step_bytes)
-        log(f"[bench] CPU legs: {json.dumps(extras['cpu_legs'])}")
+        if legs:
+            extras["cpu_legs"] = cpu_extra_legs(args.ctx, M.algorithmic_bytes_layer(M.Qwen3Config(), args.ctx))
+            log(f"[bench] CPU legs: {json.dumps(extras['cpu_legs'])}")
 
+    gb = gemv["bytes"]
+    value = gemv["GBps"]
+    floor_us = gemv["floor_us"]
+    roofline = {"bound": "hbm", "kernel": f"{GEMV_KERNEL} (3072x1024 Q4 GEMV, fp16 x / y)",
+                "achieved": round(value, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                "frac": round(value / HBM_PEAK_GBPS, 4), "traffic": None,
+                "bytes_per_launch": gb, "avg_launch_us": round(gemv["us"], 3),
+                "single_launch_floor_us": round(floor_us, 3),
+                "single_launch_ceiling_GBps": round(gb / (floor_us * 1e3 + gb / HBM_PEAK_GBPS), 1)}
+    tj = load_json("gemv_3072x1024_hbm_traffic.json")
+    if tj:
+        roofline["traffic"] = tj["total_bytes"]
+        roofline["traffic_source"] = tj["source"]
+        roofline["tcc_hit_rate"] = tj.get("tcc_hit_rate")
     if "hbm_copy" in extras:
         roofline["measured_copy_GBps"] = extras["hbm_copy"]["GBps"]
-        roofline["frac_of_measured_copy"] = round(roofline["achieved"] / extras["hbm_copy"]["GBps"], 4)
+        roofline["frac_of_measured_copy"] = round(value / extras["hbm_copy"]["GBps"], 4)
     line = {"metric": METRIC, "value": round(value, 2), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
-            "warmup": args.warmup, "ms_per_step": round(ms_per_step, 6), "higher_is_better": True,
-            "scaling": "weak", "vs_baseline": None, "dtype": "q4xf32",
-            "data": "synthetic (seeded random-init Q4 weights, N(0,1) fp16 KV, N(0,1) hidden)",
-            "config": {"workload": "one Qwen3-0.6B decoder layer, one decode step at ctx 512, "
-                                   f"weights rotated over {copies} distinct layers (cache-flushed)",
-                       "hidden": 1024, "q_heads": 16, "kv_heads": 8, "head_dim": 128, "intermediate": 3072,
-                       "ctx": ctx, "batch": 1, "bytes_per_step": step_bytes, "activation_precision": args.precision},
-            "roofline": roofline, "cpu_baseline": cpu, "extras": extras}
+            "warmup": args.warmup, "ms_per_step": round(gemv["us"] * 1e-3, 6), "higher_is_better": True,
+            "scaling": "weak", "vs_baseline": None,
+            "dtype": "q4 weights x f16 activations, f32 accumulate",
+            "data": "synthetic (seeded random-init Q4 weights, N(0,1) fp16 x; decode: random prompt ids)",
+            "config": {"workload": f"one 3072x1024 Q4 dequant-GEMV (Qwen3-0.6B gate_proj shape), fp16 x ~ N(0,1), "
+                                   f"batch 1, fp16 y; each step reads another of {max(1, args.copies)} copies of the "
+                                   f"matrix ({max(1, args.copies) * gb / 1e6:.0f} MB > the 256 MB cache: flushed)",
+                       "rows": GEMV_ROWS, "cols": GEMV_COLS, "batch": 1, "bytes_per_step": gb,
+                       "copies": max(1, args.copies), "value_pct_of_peak": round(100 * value / HBM_PEAK_GBPS, 2),
+                       "decode_activation_precision": "fp16 hi+lo pairs (~22 bits)" if args.precision == 2
+                       else "fp16", "kv_cache": "fp16"},
+            "roofline": roofline, "cpu_baseline": cpu, "decode": decode, "lm_head": lm, "extras": extras}
     print(json.dumps(line), flush=True)
 
 
-def cpu_baseline(seconds, ctx, step_bytes):
-    """The oracle's fp32 layer step (the reference's CPU path, common.py:231-298)
-    on a bounded sample of the same workload, timed on the host cores."""
+def cpu_baseline(seconds):
+    """The oracle's fp32 matvec for the 3072x1024 GEMV (manual_linear_from_weight,
+    common.py:137-145, on the matrix dequantised once) on the host cores, a
+    bounded sample, in GB/s of the GEMV's algorithmic bytes."""
     import numpy as np
 
     import oracle as o
@@ -498,24 +657,23 @@ def cpu_baseline(seconds, ctx, step_bytes):
         threads = max([p.get("num_threads", 1) for p in threadpool_info()] or [1])
     except Exception:  # threadpoolctl missing: numpy default
         threads = os.cpu_count() or 1
-    cfg = M.Qwen3Config(num_hidden_layers=1, vocab_size=2048)
-    host = M.random_host_weights(cfg, seed=0, num_layers=1)
-    om = o.OracleModel.from_q4(o.OracleConfig(num_hidden_layers=1, vocab_size=2048), host["layers"],
-                               *host["embed_tokens"], host["norm"])
-    rng = np.random.default_rng(2)
-    k = rng.normal(size=(1, 8, ctx, 128)).astype(np.float32)
-    v = rng.normal(size=(1, 8, ctx, 128)).astype(np.float32)
-    h = rng.normal(size=(1, 1, 1024)).astype(np.float32)
-    pos = np.array([[ctx]])
-    o.manual_decoder_layer_cached(h, om.layers[0], om.config, om.inv_freq, pos, k, v)
+    rng = np.random.default_rng(0)
+    packed, scale = M.random_q4(rng, GEMV_ROWS, GEMV_COLS)
+    W = o.dequantize_q4(packed, scale, np.float32)
+    x = rng.normal(size=(1, GEMV_COLS)).astype(np.float32)
+    o.manual_linear_from_weight(x, W)
     n, t0 = 0, time.perf_counter()
     while time.perf_counter() - t0 < seconds:
-        o.manual_decoder_layer_cached(h, om.layers[0], om.config, om.inv_freq, pos, k, v)
-        n += 1
+        for _ in range(100):
+            o.manual_linear_from_weight(x, W)
+        n += 100
     dt = (time.perf_counter() - t0) / n
-    return {"value": round(step_bytes / dt / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
-            "sample": f"{n} fp32 numpy layer steps at ctx {ctx} (oracle restatement of common.py:231-298), "
-                      f"{dt * 1e3:.2f} ms/step; os.cpu_count()={os.cpu_count()}, "
+    gb = M.gemv_bytes(GEMV_ROWS, GEMV_COLS)
+    return {"value": round(gb / dt / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"{n} fp32 matvecs y = x @ W.T, W 3072x1024 dequantised once (oracle restatement of "
+                      f"manual_linear_from_weight, common.py:137-145), {dt * 1e6:.2f} us each = "
+                      f"{GEMV_ROWS * GEMV_COLS * 4 / dt / 1e9:.1f} GB/s of fp32 weights; rate quoted over the Q4 "
+                      f"GEMV's {gb} algorithmic bytes; os.cpu_count()={os.cpu_count()}, "
                       f"affinity={len(os.sched_getaffinity(0))}"}
 
 
@@ -532,12 +690,13 @@ def _median_time(fn, reps, budget_s):
 
 
 def cpu_extra_legs(ctx, step_bytes):
-    """The other CPU baselines: the 3072x1024 GEMV (fp32 matvec on pre-dequantised
-    weights as manual_linear_from_weight holds them, common.py:137-145, and the
-    int64 Q26 restatement of compute_q4_gemv_q26, 28_export_mlp_gate_up_vectors.py:124-133),
-    the layer step on one thread, and the 28-layer decode (run_manual_one_token,
-    10_validate_full_run_one_token.py:17-56, 8 serial steps of the 28-layer
-    model, per token).  Medians of >= 10 timed runs after a warm-up."""
+    """The other CPU baselines: the int64 Q26 restatement of the GEMV
+    (compute_q4_gemv_q26, 28_export_mlp_gate_up_vectors.py:124-133), the
+    decoder-layer step at context ``ctx`` on all threads and on one
+    (manual_decoder_layer_cached, common.py:231-298), the 28-layer decode
+    (run_manual_one_token, 10_validate_full_run_one_token.py:17-56, 8 serial
+    steps of the 28-layer model, per token) and the oracle's quantizer.
+    Medians of >= 10 timed runs after a warm-up."""
     import numpy as np
 
     import oracle as o
@@ -548,30 +707,30 @@ def cpu_extra_legs(ctx, step_bytes):
         threadpool_limits = None
     out = {"cores": os.cpu_count(), "affinity": len(os.sched_getaffinity(0))}
     rng = np.random.default_rng(0)
-    packed, scale = M.random_q4(rng, 3072, 1024)
-    W = o.dequantize_q4(packed, scale, np.float32)
-    q = o.unpack_signed_int4(packed, 1024)
-    x = rng.normal(size=1024).astype(np.float32)
-    xi = rng.integers(-(1 << 20), 1 << 20, size=1024)
-    gb = M.gemv_bytes(3072, 1024)
-    t, n = _median_time(lambda: W @ x, 10, 2.0)
-    out["gemv_fp32"] = {"us": round(t * 1e6, 1), "GBps": round(gb / t / 1e9, 2), "runs": n}
+    packed, scale = M.random_q4(rng, GEMV_ROWS, GEMV_COLS)
+    q = o.unpack_signed_int4(packed, GEMV_COLS)
+    xi = rng.integers(-(1 << 20), 1 << 20, size=GEMV_COLS)
+    gb = M.gemv_bytes(GEMV_ROWS, GEMV_COLS)
     t, n = _median_time(lambda: o.q4_gemv_q26(xi, q, scale), 10, 2.0)
     out["gemv_int64_q26"] = {"us": round(t * 1e6, 1), "GBps": round(gb / t / 1e9, 3), "runs": n}
+    cfg = M.Qwen3Config(num_hidden_layers=1, vocab_size=2048)
+    host = M.random_host_weights(cfg, seed=0, num_layers=1)
+    om = o.OracleModel.from_q4(o.OracleConfig(num_hidden_layers=1, vocab_size=2048), host["layers"],
+                               *host["embed_tokens"], host["norm"])
+    k = rng.normal(size=(1, 8, ctx, 128)).astype(np.float32)
+    v = rng.normal(size=(1, 8, ctx, 128)).astype(np.float32)
+    h = rng.normal(size=(1, 1, 1024)).astype(np.float32)
+    pos = np.array([[ctx]])
+
+    def layer():
+        o.manual_decoder_layer_cached(h, om.layers[0], om.config, om.inv_freq, pos, k, v)
+    t, n = _median_time(layer, 10, 3.0)
+    out["layer_all_threads"] = {"ms_per_step": round(t * 1e3, 3), "GBps": round(step_bytes / t / 1e9, 3), "runs": n}
     if threadpool_limits is not None:
-        cfg = M.Qwen3Config(num_hidden_layers=1, vocab_size=2048)
-        host = M.random_host_weights(cfg, seed=0, num_layers=1)
-        om = o.OracleModel.from_q4(o.OracleConfig(num_hidden_layers=1, vocab_size=2048), host["layers"],
-                                   *host["embed_tokens"], host["norm"])
-        k = rng.normal(size=(1, 8, ctx, 128)).astype(np.float32)
-        v = rng.normal(size=(1, 8, ctx, 128)).astype(np.float32)
-        h = rng.normal(size=(1, 1, 1024)).astype(np.float32)
-        pos = np.array([[ctx]])
         with threadpool_limits(limits=1):
-            t, n = _median_time(lambda: o.manual_decoder_layer_cached(h, om.layers[0], om.config, om.inv_freq,
-                                                                      pos, k, v), 10, 3.0)
+            t, n = _median_time(layer, 10, 3.0)
         out["layer_one_thread"] = {"ms_per_step": round(t * 1e3, 3), "GBps": round(step_bytes / t / 1e9, 3),
-                                "runs": n}
+                                   "runs": n}
     fcfg = M.Qwen3Config()
     fhost = M.random_host_weights(fcfg, seed=0)
     om = o.OracleModel.from_q4(o.OracleConfig(), fhost["layers"], *fhost["embed_tokens"], fhost["norm"])
@@ -585,10 +744,10 @@ def cpu_extra_legs(ctx, step_bytes):
         ts.append(time.perf_counter() - t0)
     tt = sorted(ts[1:])[len(ts[1:]) // 2]
     out["decode_per_token"] = {"ms": round(tt * 1e3, 1), "tok_s": round(1.0 / tt, 2), "steps": len(ts),
-                           "note": "median of steps 1-7 at positions 1-7 (the first step is the warm-up)"}
-    wq = (rng.standard_normal((3072, 1024)) * 0.03).astype(np.float32)
+                               "note": "median of steps 1-7 at positions 1-7 (the first step is the warm-up)"}
+    wq = (rng.standard_normal((GEMV_ROWS, GEMV_COLS)) * 0.03).astype(np.float32)
     t, n = _median_time(lambda: o.quantize_weight_q4(wq), 5, 2.0)
-    qb = 3072 * 1024 * 4 + 3072 * 512 + 3072 * 16 * 2
+    qb = GEMV_ROWS * GEMV_COLS * 4 + GEMV_ROWS * 512 + GEMV_ROWS * 16 * 2
     out["q4c_oracle"] = {"shape": "3072x1024 fp32 -> Q4", "ms": round(t * 1e3, 2), "GBps": round(qb / t / 1e9, 3),
                          "runs": n}
     return out
