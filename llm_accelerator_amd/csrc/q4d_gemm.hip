@@ -168,9 +168,24 @@ __global__ __launch_bounds__(NW * 64) void q4_gemm_kernel(const GemmArgs a) {
 
   const int t = threadIdx.x, lane = t & 63, w = t >> 6;
   const int wm = (w >> 1) * WM, wn = (w & 1);
-  const int nblk = blockIdx.x, m0 = blockIdx.y * BM;
+  // XCD-aware tile order: linear block b runs on XCD b % 8, and each XCD has its
+  // own L2.  Tiles are numbered n fastest, then m, then the K split, and XCD x
+  // takes the x-th contiguous eighth of them, so its blocks share a few rows of
+  // X (and a K range) instead of each XCD reading all of X.
+  int nblk = blockIdx.x, mblk = blockIdx.y, z = blockIdx.z;
+  {
+    const int gx = gridDim.x, gy = gridDim.y, total = gx * gy * (int)gridDim.z;
+    if ((total & 7) == 0) {
+      const int lin = (int)blockIdx.x + gx * ((int)blockIdx.y + gy * (int)blockIdx.z);
+      const int v = (lin & 7) * (total >> 3) + (lin >> 3);
+      nblk = v % gx;
+      mblk = (v / gx) % gy;
+      z = v / (gx * gy);
+    }
+  }
+  const int m0 = mblk * BM;
   // K steps [k_begin, k_end) of this split
-  const int nk_all = a.K / kGemmBK, z = blockIdx.z, ksplit = gridDim.z;
+  const int nk_all = a.K / kGemmBK, ksplit = gridDim.z;
   const int k_begin = z * nk_all / ksplit;
   const int nk = (z + 1) * nk_all / ksplit - k_begin;
 

@@ -21,7 +21,10 @@
 // loads are fully coalesced and a row is reduced over 16 lanes.  The hi and
 // lo activation products share one accumulator per nibble position.  This
 // halves the reduction and scale work per byte of the 2-row tile, which
-// matters because the streaming kernel is bound by VALU issue, not by HBM.
+// matters because between its prologue and its argmax hand-off the kernel
+// keeps the SIMDs' VALU nearly saturated (4 waves per SIMD at ~130 VALU
+// instructions per 2 KB tile), while the table streams at ~6.8 TB/s; the
+// fixed phases around that (activation prologue, argmax hand-off) cost ~8 µs.
 //
 // Loads are buffer loads: the matrix base is a wave-uniform resource, the
 // tile's row offset a scalar and the lane's offset a per-lane constant, so no
@@ -379,12 +382,16 @@ __global__ __launch_bounds__(NWB * 64) void lm_kernel(const GemvArgs a) {
   Tile4 A[U], B[U];
 #pragma unroll
   for (int u = 0; u < U; ++u) A[u] = load4(base + u * step);
-  // stage 1 goes out unconditionally (clamped): a conditional issue makes the
-  // wait-count pass assume at every later merge that it may be missing
+  // stage 1 goes out after the activation prologue: issued with stage 0 the
+  // grid's 15 MB of weight requests queue the activation loads behind them
+  // (measured ~1 µs later prologue).  It is unconditional (clamped): a
+  // conditional issue makes the wait-count pass assume at every later merge
+  // that it may be missing.
+  act_prepare(a.eps, ar, s_act);
+  __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
   for (int u = 0; u < U; ++u) B[u] = load4(base + (U + u) * step);
 
-  act_prepare(a.eps, ar, s_act);
   XChunk xh0, xl0, xh1, xl1;
   act_chunk(s_act, sub, xh0, xl0);
   act_chunk(s_act, 16 + sub, xh1, xl1);

@@ -129,9 +129,24 @@ __global__ __launch_bounds__(256) void prefill_attn_kernel(const PrefillArgs a) 
 
   const int t = threadIdx.x, lane = t & 63;
   const int w = __builtin_amdgcn_readfirstlane(t >> 6);
-  // heavier (later) query tiles first
-  const int qt = (int)gridDim.x - 1 - (int)blockIdx.x;
-  const int h = blockIdx.y, j = h / (a.qh / a.kvh);
+  // Block order.  Linear block b runs on XCD b % 8 (each XCD has its own L2), and an
+  // XCD's blocks go round robin over its 32 CUs, so its blocks i and i + 32 share a
+  // CU.  With 16 heads each XCD takes two consecutive q heads (one kv head: its
+  // K/V stay in that L2), the first heaviest query tile first and the second
+  // lightest first, so every CU gets a complementary pair of causal loads.
+  // Other head counts: linear order, heaviest query tile first.
+  const int gx = gridDim.x, gy = gridDim.y;
+  const int lin = (int)blockIdx.x + gx * (int)blockIdx.y;
+  int qt, h;
+  if (gy % 16 == 0) {
+    const int per = gx * gy / 8, i = lin >> 3, u = i % gx;
+    h = (gy / 8) * (lin & 7) + i / gx;
+    qt = i >= per / 2 ? u : gx - 1 - u;
+  } else {
+    h = blockIdx.y;
+    qt = gx - 1 - (int)blockIdx.x;
+  }
+  const int j = h / (a.qh / a.kvh);
   const int i0 = qt * kBQ;                 // first query (token index) of the block
   const int q_lo = i0 + 16 * w;            // first query of this wave
   const int kend = a.p0 + min(a.n, i0 + kBQ);  // keys [0, kend) can be attended by the block
