@@ -248,6 +248,18 @@ int q4d_layer_stage(const q4d_model_t* model, int32_t layer, int32_t stage, cons
 int q4d_run_one_token(const q4d_model_t* model, const int32_t* tokens, const int32_t* positions,
                       const q4d_kv_cache_t* kv, int32_t* next_token, float* score, float* logits,
                       void* ws, size_t ws_bytes, void* stream);
+/* q4d_run_one_token followed by the greedy feedback of q4d_advance, in the same
+ * launches: the LM head's last block also sets tokens[0] = next_token[0], positions[0] += 1
+ * and, if hist_tokens is not NULL and *hist_count < hist_capacity, records the token and
+ * score at index *hist_count and increments it.  The embedding of tokens[0] is built inside
+ * layer 0's q|k|v launch, so a step is two launches fewer than q4d_run_one_token +
+ * q4d_advance, with the same results bit for bit.  The generation loop it replaces feeds the
+ * argmax back as the next input (10_validate_full_run_one_token.py:135-172; on the board
+ * qot_decode_token_ids, qmap_one_token_runtime.h:399-497). */
+int q4d_run_one_token_feedback(const q4d_model_t* model, int32_t* tokens, int32_t* positions,
+                               const q4d_kv_cache_t* kv, int32_t* next_token, float* score, float* logits,
+                               int32_t* hist_tokens, float* hist_scores, int32_t* hist_count,
+                               int32_t hist_capacity, void* ws, size_t ws_bytes, void* stream);
 /* q4d_run_one_token without a workspace argument, for callers that cannot allocate
  * device memory (code under HIP graph capture, serving loops or harnesses that forbid
  * hipMalloc).  No counterpart in the reference.  Its scratch is a 4 MiB device array

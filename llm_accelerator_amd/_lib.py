@@ -147,6 +147,8 @@ SIGNATURES = {
                          c_int32),
     "q4d_run_one_token": ([POINTER(Q4dModel), _P, _P, POINTER(Q4dKVCache), _P, _P, _P, _P, c_size_t, _P],
                           c_int32),
+    "q4d_run_one_token_feedback": ([POINTER(Q4dModel), _P, _P, POINTER(Q4dKVCache), _P, _P, _P, _P, _P, _P,
+                                    c_int32, _P, c_size_t, _P], c_int32),
     "q4d_run_one_token_noalloc": ([POINTER(Q4dModel), _P, _P, POINTER(Q4dKVCache), _P, _P, _P, _P, _P], c_int32),
     "q4d_apply_rope": ([_P, _P, _P, _P, c_int32, c_int32, c_int32, _P], c_int32),
     "q4d_advance": ([_P, _P, _P, _P, _P, _P, _P, c_int32, _P], c_int32),

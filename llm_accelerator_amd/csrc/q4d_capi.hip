@@ -95,11 +95,25 @@ GemvArgs one_matrix(const q4d_matrix_t* w, int batch) {
   return a;
 }
 
+// Greedy feedback of a one-token step, stored by the LM head's last block (the
+// work of q4d_advance without its launch).
+struct Feedback {
+  int32_t* tokens;
+  int32_t* positions;
+  int32_t* hist_tokens;
+  float* hist_scores;
+  int32_t* hist_count;
+  int32_t hist_capacity;
+};
+
 // One decoder layer, batch 1 (common.py:231-298), five launches; `only`
-// selects a single stage (Q4D_STAGE_*) or -1 for all.
+// selects a single stage (Q4D_STAGE_*) or -1 for all.  With `emb_tokens` the
+// layer's input is the embedding row of emb_tokens[0], built in the q|k|v
+// launch's prologue, which also stores it to hout (the residual stream; hin
+// must then be hout).
 int run_layer(const q4d_model_t* m, int l, const float* hin, float* hout, const q4d_kv_cache_t* kv,
               const int32_t* positions, void* ws, const WsLayout& W, hipStream_t st, int only = -1,
-              int32_t* status = nullptr) {
+              int32_t* status = nullptr, const int32_t* emb_tokens = nullptr) {
   const q4d_layer_t& L = m->layers[l];
   const int xp = g_act_precision;
   float* qkv = ws_ptr<float>(ws, W.qkv);
@@ -124,7 +138,19 @@ int run_layer(const q4d_model_t* m, int l, const float* hin, float* hout, const 
   a.eps = m->rms_norm_eps;
   a.y = qkv;
   a.batch = 1;
-  if ((only < 0 || only == Q4D_STAGE_QKV) && (rc = launch_gemv_xp(a, X_RMS, xp, EP_F32, false, st))) return rc;
+  int xm = X_RMS;
+  if (emb_tokens) {
+    if (hin != hout) return Q4D_ERR_SHAPE;
+    a.x = nullptr;
+    a.emb_token = emb_tokens;
+    a.emb_w = m->embed_tokens.w;
+    a.emb_s = m->embed_tokens.s;
+    a.emb_vocab = m->embed_tokens.rows;
+    a.emb_out = hout;
+    a.emb_status = status ? status : ws_ptr<int32_t>(ws, W.status);
+    xm = X_EMB;
+  }
+  if ((only < 0 || only == Q4D_STAGE_QKV) && (rc = launch_gemv_xp(a, xm, xp, EP_F32, false, st))) return rc;
 
   // 2. q/k norm + RoPE + KV append + attention + split merge
   AttnArgs t;
@@ -196,7 +222,7 @@ int run_layer(const q4d_model_t* m, int l, const float* hin, float* hout, const 
 }
 
 int run_lm_head(const q4d_model_t* m, const float* hidden, int32_t* tok, float* score, float* logits,
-                void* ws, const WsLayout& W, hipStream_t st) {
+                void* ws, const WsLayout& W, hipStream_t st, const Feedback* fb = nullptr) {
   GemvArgs a = one_matrix(&m->embed_tokens, 1);
   a.x = hidden;
   a.gamma = m->final_norm;
@@ -206,20 +232,30 @@ int run_lm_head(const q4d_model_t* m, const float* hidden, int32_t* tok, float* 
   a.counter = ws_ptr<int>(ws, W.counters) + W.lm_counter_index;
   a.out_token = tok;
   a.out_score = score;
+  if (fb) {
+    a.adv_tokens = fb->tokens;
+    a.adv_positions = fb->positions;
+    a.hist_tokens = fb->hist_tokens;
+    a.hist_scores = fb->hist_scores;
+    a.hist_count = fb->hist_count;
+    a.hist_cap = fb->hist_capacity;
+  }
   return launch_gemv_xp(a, X_RMS, g_act_precision, EP_ARGMAX, false, st);
 }
 
 // Embedding -> all layers -> LM head argmax for one token (batch 1), the launches of
-// q4d_run_one_token; `status` receives the device-side status bits.
+// q4d_run_one_token: the embedding is built inside layer 0's q|k|v launch, and
+// with `fb` the LM head also stores the greedy feedback.  `status` receives the
+// device-side status bits.
 int run_token(const q4d_model_t* m, const int32_t* tokens, const int32_t* positions, const q4d_kv_cache_t* kv,
               int32_t* next_token, float* score, float* logits, void* ws, const WsLayout& W, int32_t* status,
-              hipStream_t st) {
+              hipStream_t st, const Feedback* fb = nullptr) {
   float* hidden = ws_ptr<float>(ws, W.hidden);
-  int rc = launch_embedding(&m->embed_tokens, tokens, 1, hidden, status, st);
-  if (rc) return rc;
+  int rc;
   for (int l = 0; l < m->num_layers; ++l)
-    if ((rc = run_layer(m, l, hidden, hidden, kv, positions, ws, W, st, -1, status))) return rc;
-  return run_lm_head(m, hidden, next_token, score, logits, ws, W, st);
+    if ((rc = run_layer(m, l, hidden, hidden, kv, positions, ws, W, st, -1, status, l == 0 ? tokens : nullptr)))
+      return rc;
+  return run_lm_head(m, hidden, next_token, score, logits, ws, W, st, fb);
 }
 
 // Scratch of q4d_run_one_token_noalloc, for callers that cannot allocate: a
@@ -649,6 +685,23 @@ int q4d_run_one_token(const q4d_model_t* model, const int32_t* tokens, const int
   const WsLayout W = ws_layout(model, 1);
   return run_token(model, tokens, positions, kv, next_token, score, logits, ws, W, ws_ptr<int32_t>(ws, W.status),
                    as_stream(stream));
+}
+
+int q4d_run_one_token_feedback(const q4d_model_t* model, int32_t* tokens, int32_t* positions,
+                               const q4d_kv_cache_t* kv, int32_t* next_token, float* score, float* logits,
+                               int32_t* hist_tokens, float* hist_scores, int32_t* hist_count,
+                               int32_t hist_capacity, void* ws, size_t ws_bytes, void* stream) {
+  if (!tokens || !positions || !next_token || !score) return Q4D_ERR_NULL;
+  if (hist_tokens && (!hist_count || hist_capacity < 0)) return Q4D_ERR_NULL;
+  int rc = check_model(model);
+  if (rc) return rc;
+  if ((rc = check_kv(kv, model, 1))) return rc;
+  if (kv->batch != 1) return Q4D_ERR_CAPACITY;
+  if ((rc = check_ws(ws, ws_bytes, model, 1))) return rc;
+  const WsLayout W = ws_layout(model, 1);
+  const Feedback fb = {tokens, positions, hist_tokens, hist_scores, hist_count, hist_capacity};
+  return run_token(model, tokens, positions, kv, next_token, score, logits, ws, W, ws_ptr<int32_t>(ws, W.status),
+                   as_stream(stream), &fb);
 }
 
 int q4d_run_one_token_noalloc(const q4d_model_t* model, const int32_t* tokens, const int32_t* positions,

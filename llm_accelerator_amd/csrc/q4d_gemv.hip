@@ -41,15 +41,20 @@
 // Doing this conversion per lane instead costs ~400 VALU instructions per
 // wave and dominated the decode-size GEMVs.
 //
-// Prologues: fp16 x, fp32 x, or RMSNorm of an fp32 hidden vector (reference
-// common.py:129-134).  Epilogues: fp16/fp32 store, residual add
+// Prologues: fp16 x, fp32 x, RMSNorm of an fp32 hidden vector (reference
+// common.py:129-134), or RMSNorm of the tied Q4 embedding row of a token id read
+// on the device (the first layer of a one-token step; its block 0 also stores
+// the row as the residual stream).  Epilogues: fp16/fp32 store, residual add
 // (common.py:284,297), SwiGLU over the gate/up pair (common.py:293-295), and
 // LM-head argmax with the lowest-index tie rule
 // (56_export_persistent_multitoken_layer_golden.py:860).  The argmax is
 // finished without fences: each block folds its best (score, index) into one
 // 64-bit key with a device-scope atomicMax, waits for it to complete, then
 // counts in; the last block to count in reads the key back with another
-// atomic, so every read goes to the coherence point.
+// atomic, so every read goes to the coherence point.  With greedy feedback the
+// last block also stores the token as the next step's input, advances the
+// position and records the history (what advance_kernel does as a launch of
+// its own).
 #include <math.h>
 
 #include "q4d_device.h"
@@ -70,6 +75,22 @@ template <int K, int NWB, int XM, int XP>
 __device__ __forceinline__ void act_load(const GemvArgs& a, int bat, ActRegs<K, NWB, XM, XP>& r) {
   using R = ActRegs<K, NWB, XM, XP>;
   if constexpr (XM == X_ATTN) return;  // chunk partials: attn_issue / attn_finish
+  if constexpr (XM == X_EMB) {
+    // vector v = columns 4v .. 4v+3: two bytes of codes and its group's scale code
+    // of the token's row (row 0 stands in for an id outside the table)
+    const int tok = __builtin_amdgcn_readfirstlane(a.emb_token[0]);
+    const size_t row = (tok >= 0 && tok < a.emb_vocab) ? (size_t)tok : 0;
+#pragma unroll
+    for (int i = 0; i < R::XPT; ++i) {
+      const int v = threadIdx.x + i * NWB * 64;
+      if (v < R::XV) {
+        r.ec[i] = *reinterpret_cast<const uint16_t*>(a.emb_w + row * (K / 2) + 2 * v);
+        r.es[i] = a.emb_s[row * (K / 64) + v / 16];
+        r.g[i] = reinterpret_cast<const f32x4*>(a.gamma)[v];
+      }
+    }
+    return;
+  }
 #pragma unroll
   for (int i = 0; i < R::XPT; ++i) {
     const int v = threadIdx.x + i * NWB * 64;
@@ -79,6 +100,33 @@ __device__ __forceinline__ void act_load(const GemvArgs& a, int bat, ActRegs<K, 
       if constexpr (XM == X_RMS) r.g[i] = reinterpret_cast<const f32x4*>(a.gamma)[v];
     }
   }
+}
+
+// X_EMB: the embedding row from the codes act_load fetched, q * scale / 2^14
+// exactly as embedding_kernel computes it; block 0 stores it as the residual
+// stream and reports an id outside the table.
+template <int K, int NWB, int XP>
+__device__ __forceinline__ void emb_convert(const GemvArgs& a, ActRegs<K, NWB, X_EMB, XP>& r) {
+  using R = ActRegs<K, NWB, X_EMB, XP>;
+  const int tok = __builtin_amdgcn_readfirstlane(a.emb_token[0]);
+  const bool ok = tok >= 0 && tok < a.emb_vocab;
+  const bool writer = blockIdx.x == 0 && blockIdx.y == 0;
+#pragma unroll
+  for (int i = 0; i < R::XPT; ++i) {
+    const int v = threadIdx.x + i * NWB * 64;
+    if (v < R::XV) {
+      const float sc = scale_q2_14(r.es[i]);
+      f32x4 x;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int nib = (int)((r.ec[i] >> (4 * e)) & 0xFu);
+        x[e] = ok ? (float)(nib - ((nib & 0x8) ? 16 : 0)) * sc : 0.0f;
+      }
+      r.x[i] = x;
+      if (writer) reinterpret_cast<f32x4*>(a.emb_out)[v] = x;
+    }
+  }
+  if (writer && !ok && threadIdx.x == 0 && a.emb_status) atomicOr(a.emb_status, Q4D_STATUS_BAD_TOKEN);
 }
 
 // X_ATTN: the attention output for this thread's vectors, merged from the
@@ -255,6 +303,7 @@ __global__ __launch_bounds__(NWB * 64) void gemv_kernel(const GemvArgs a) {
     attn_finish<K, NWB>(a, bat, ap, ar.x);
   }
 
+  if constexpr (XM == X_EMB) emb_convert(a, ar);
   act_prepare(a.eps, ar, s_act);
   XChunk xh, xl;
   act_chunk(s_act, ks * 32 + (lane & 31), xh, xl);
@@ -471,6 +520,18 @@ __global__ __launch_bounds__(NWB * 64) void lm_kernel(const GemvArgs a) {
       argmax_unkey(fin, &sc, &ix);
       a.out_token[0] = ix;
       a.out_score[0] = sc;
+      if (a.adv_tokens) {  // greedy feedback, as advance_kernel
+        a.adv_tokens[0] = ix;
+        a.adv_positions[0] += 1;
+        if (a.hist_tokens) {
+          const int32_t c = a.hist_count[0];
+          if (c < a.hist_cap) {
+            a.hist_tokens[c] = ix;
+            if (a.hist_scores) a.hist_scores[c] = sc;
+            a.hist_count[0] = c + 1;
+          }
+        }
+      }
       // ready for the next launch (stream order makes these visible to it)
       __hip_atomic_store(a.lm_key, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       __hip_atomic_store(a.counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -556,6 +617,8 @@ int dispatch_k(const GemvArgs& a, int xm, int xp, int ep, bool pair, hipStream_t
   if constexpr (KS == 1) {
     if (xm == X_RMS && ep == EP_F32 && !pair)
       return xp == 2 ? launch_sel<1, X_RMS, 2, EP_F32, false>(a, st) : launch_sel<1, X_RMS, 1, EP_F32, false>(a, st);
+    if (xm == X_EMB && ep == EP_F32 && !pair)
+      return xp == 2 ? launch_sel<1, X_EMB, 2, EP_F32, false>(a, st) : launch_sel<1, X_EMB, 1, EP_F32, false>(a, st);
     if (xm == X_RMS && ep == EP_SWIGLU && pair)
       return xp == 2 ? launch_sel<1, X_RMS, 2, EP_SWIGLU, true>(a, st)
                      : launch_sel<1, X_RMS, 1, EP_SWIGLU, true>(a, st);
@@ -597,12 +660,16 @@ int launch_gemv_xp(const GemvArgs& a, int xm, int xp, int ep, bool pair, hipStre
   if (xm == X_ATTN) {
     if (!a.part_ml || !a.part_acc || !a.positions || a.nsplit_max <= 0 || a.attn_chunk <= 0) return Q4D_ERR_NULL;
     if (a.cols % 128 || !aligned(a.part_acc, 16) || !aligned(a.part_ml, 8)) return Q4D_ERR_SHAPE;
+  } else if (xm == X_EMB) {
+    if (!a.emb_token || !a.emb_w || !a.emb_s || !a.emb_out || a.emb_vocab <= 0 || a.cols != 1024) return Q4D_ERR_NULL;
+    if (!aligned(a.emb_w, 2) || !aligned(a.emb_s, 2) || !aligned(a.emb_out, 16)) return Q4D_ERR_BAD_ADDR;
   } else if (!a.x) {
     return Q4D_ERR_NULL;
   }
   if (!a.y && ep != EP_ARGMAX) return Q4D_ERR_NULL;
-  if (xm != X_ATTN && !aligned(a.x, 16)) return Q4D_ERR_BAD_ADDR;
-  if (xm == X_RMS && (!a.gamma || !aligned(a.gamma, 16))) return Q4D_ERR_NULL;
+  if (xm != X_ATTN && xm != X_EMB && !aligned(a.x, 16)) return Q4D_ERR_BAD_ADDR;
+  if ((xm == X_RMS || xm == X_EMB) && (!a.gamma || !aligned(a.gamma, 16))) return Q4D_ERR_NULL;
+  if (a.adv_tokens && (ep != EP_ARGMAX || !a.adv_positions || (a.hist_tokens && !a.hist_count))) return Q4D_ERR_NULL;
   if (ep == EP_RESID && !a.resid) return Q4D_ERR_NULL;
   if (ep == EP_ARGMAX && (!a.lm_key || !a.counter || !a.out_token || !a.out_score || a.batch != 1))
     return Q4D_ERR_NULL;

@@ -126,13 +126,16 @@ __device__ __forceinline__ uint32_t pack_h2(_Float16 lo, _Float16 hi) {
 }
 
 // ---- activation prologue ------------------------------------------------------
+// Prologues that apply an RMSNorm (with gamma) to the activations.
+constexpr bool rms_mode(int xm) { return xm == X_RMS || xm == X_EMB; }
+
 // LDS a block needs for K columns of activations.
 template <int K, int NWB, int XM, int XP>
 struct ActLds {
   static constexpr int XV = (XM == X_F16) ? K / 8 : K / 4;  // 16-byte vectors of x
   static constexpr int CH = K / 32;                         // 32-column chunks
   f32x4 x[XV];
-  f32x4 g[XM == X_RMS ? XV : 1];
+  f32x4 g[rms_mode(XM) ? XV : 1];
   alignas(16) uint32_t ph[CH * 16];                // hi pairs, dequant order
   alignas(16) uint32_t pl[XP == 2 ? CH * 16 : 4];  // lo pairs
   float2 sm[CH];                                   // 8 * chunk sums (hi, lo)
@@ -144,7 +147,10 @@ struct ActRegs {
   static constexpr int XV = ActLds<K, NWB, XM, XP>::XV;
   static constexpr int XPT = (XV + NWB * 64 - 1) / (NWB * 64);  // vectors per thread
   f32x4 x[XPT];
-  f32x4 g[XM == X_RMS ? XPT : 1];
+  f32x4 g[rms_mode(XM) ? XPT : 1];
+  // X_EMB: the raw embedding codes (4 nibbles) and scale code of each vector
+  uint32_t ec[XM == X_EMB ? XPT : 1];
+  uint32_t es[XM == X_EMB ? XPT : 1];
 };
 
 // Stage x (and gamma) in LDS, reduce sum(x^2) for the RMSNorm, and convert
@@ -166,7 +172,7 @@ __device__ __forceinline__ void act_prepare(float eps, const ActRegs<K, NWB, XM,
     const int v = threadIdx.x + i * NT;
     if (v < R::XV) {
       s.x[v] = r.x[i];
-      if constexpr (XM == X_RMS) {
+      if constexpr (rms_mode(XM)) {
         s.g[v] = r.g[i];
         ss = fmaf(r.x[i][0], r.x[i][0], ss);
         ss = fmaf(r.x[i][1], r.x[i][1], ss);
@@ -175,14 +181,14 @@ __device__ __forceinline__ void act_prepare(float eps, const ActRegs<K, NWB, XM,
       }
     }
   }
-  if constexpr (XM == X_RMS) {
+  if constexpr (rms_mode(XM)) {
     ss = wave_sum_dpp(ss);
     if (lane == 63) s.red[threadIdx.x >> 6] = ss;
   }
   block_sync_lds();
 
   float inv_rms = 1.f;
-  if constexpr (XM == X_RMS) {
+  if constexpr (rms_mode(XM)) {
     float tot = 0.f;
 #pragma unroll
     for (int w = 0; w < NWB; ++w) tot += s.red[w];
@@ -203,7 +209,7 @@ __device__ __forceinline__ void act_prepare(float eps, const ActRegs<K, NWB, XM,
       h[3] = sxh[eb + 1];
     } else {
       float v[4] = {sxf[ea], sxf[eb], sxf[ea + 1], sxf[eb + 1]};
-      if constexpr (XM == X_RMS) {
+      if constexpr (rms_mode(XM)) {
         v[0] = (v[0] * inv_rms) * sgf[ea];
         v[1] = (v[1] * inv_rms) * sgf[eb];
         v[2] = (v[2] * inv_rms) * sgf[ea + 1];

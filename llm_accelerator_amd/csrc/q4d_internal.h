@@ -91,7 +91,11 @@ inline int check_launch() {
 // ---- GEMV launcher ---------------------------------------------------------
 // X_ATTN: fp32 activations merged in the prologue from split-K decode-attention
 // partials (part_ml / part_acc of the attention kernel run with merge = 0).
-enum XMode { X_F16 = 0, X_F32 = 1, X_RMS = 2, X_ATTN = 3 };
+// X_EMB: RMSNorm of the tied Q4 embedding row of token emb_token[0] (the first
+// layer's q|k|v projection of a one-token step); block 0 also writes the fp32 row
+// to emb_out (the residual stream), and an id outside the table gives zeros and
+// sets Q4D_STATUS_BAD_TOKEN in emb_status, as the embedding kernel does.
+enum XMode { X_F16 = 0, X_F32 = 1, X_RMS = 2, X_ATTN = 3, X_EMB = 4 };
 enum EpMode { EP_F16 = 0, EP_F32 = 1, EP_RESID = 2, EP_SWIGLU = 3, EP_ARGMAX = 4 };
 
 struct GemvArgs {
@@ -122,6 +126,22 @@ struct GemvArgs {
   const int32_t* positions;  // device [batch]: the attended positions are 0 .. positions[b]
   int nsplit_max;
   int attn_chunk;            // positions per chunk
+  // X_EMB.
+  const int32_t* emb_token;  // device [1]
+  const uint8_t* emb_w;      // tied table codes [emb_vocab, K/2] and Q2.14 scales [emb_vocab, K/64]
+  const uint16_t* emb_s;
+  int emb_vocab;
+  float* emb_out;            // block 0 writes the fp32 embedding row here
+  int32_t* emb_status;
+  // EP_ARGMAX with greedy feedback (adv_tokens set): the last block also stores the
+  // token as the next input, advances the position and records the history, as
+  // advance_kernel does.
+  int32_t* adv_tokens;
+  int32_t* adv_positions;
+  int32_t* hist_tokens;      // optional
+  float* hist_scores;        // optional
+  int32_t* hist_count;
+  int hist_cap;
 };
 
 // Validates geometry, picks the kernel instance and launches.  Returns Q4D_*.

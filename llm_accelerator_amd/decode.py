@@ -5,9 +5,11 @@ The loop is the reference's (``10_validate_full_run_one_token.py:81-172``,
 ``qot_decode_token_ids``, ``qmap_one_token_runtime.h:399+``): every prompt
 token runs one full step at its position, the argmax after the last prompt
 token is the first generated id, and each generated id is fed back at the
-next position.  Here the token and position live in device memory and
-``q4d_advance`` moves them forward, so a HIP graph of ``steps_per_graph``
-captured steps replays the loop with no host round trip per token.
+next position.  Here the token and position live in device memory and the
+step moves them forward itself (``q4d_run_one_token_feedback``: the LM head's
+last block stores the feedback; the session mode uses ``q4d_advance_session``
+for its stop rules), so a HIP graph of ``steps_per_graph`` captured steps
+replays the loop with no host round trip per token.
 """
 
 from __future__ import annotations
@@ -53,19 +55,26 @@ class GreedyDecoder:
     # -- one step, launched on the current stream ---------------------------------
     def _launch_step(self, logits: torch.Tensor | None = None, record: bool = True) -> None:
         st = current_stream()
+        if self._stop is None:
+            check(self._lib.q4d_run_one_token_feedback(
+                ctypes.byref(self._desc), self.tok.data_ptr(), self.pos.data_ptr(), ctypes.byref(self._kvd),
+                self.next_tok.data_ptr(), self.score.data_ptr(), logits.data_ptr() if logits is not None else None,
+                self.hist_tok.data_ptr() if record else None, self.hist_score.data_ptr() if record else None,
+                self.hist_count.data_ptr(), self.hist_cap, self.ws.ptr, self.ws.nbytes, st),
+                "q4d_run_one_token_feedback")
+            return
         check(self._lib.q4d_run_one_token(ctypes.byref(self._desc), self.tok.data_ptr(), self.pos.data_ptr(),
                                           ctypes.byref(self._kvd), self.next_tok.data_ptr(),
                                           self.score.data_ptr(), logits.data_ptr() if logits is not None else None,
                                           self.ws.ptr, self.ws.nbytes, st), "q4d_run_one_token")
-        if self._stop is not None and record:
+        if record:
             check(self._lib.q4d_advance_session(self.tok.data_ptr(), self.pos.data_ptr(), self.next_tok.data_ptr(),
                                                 self.score.data_ptr(), self.hist_tok.data_ptr(),
                                                 self.hist_score.data_ptr(), self.hist_count.data_ptr(), self.hist_cap,
                                                 self._stop.data_ptr(), st), "q4d_advance_session")
             return
         check(self._lib.q4d_advance(self.tok.data_ptr(), self.pos.data_ptr(), self.next_tok.data_ptr(),
-                                    self.score.data_ptr(), self.hist_tok.data_ptr() if record else None,
-                                    self.hist_score.data_ptr() if record else None, self.hist_count.data_ptr(),
+                                    self.score.data_ptr(), None, None, self.hist_count.data_ptr(),
                                     self.hist_cap, st), "q4d_advance")
 
     def reset(self) -> None:

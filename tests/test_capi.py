@@ -220,3 +220,23 @@ def test_noalloc_step_rejects_models_beyond_its_scratch(lib):
     kv2 = Q4dKVCache(FAKE, 1, 1, 8, 30208, 128)
     assert lib.q4d_run_one_token_noalloc(ctypes.byref(ok), FAKE, FAKE, ctypes.byref(kv2), FAKE, FAKE, None, None,
                                          None) == -7
+
+
+def test_feedback_step_validates_on_host(lib):
+    """q4d_run_one_token_feedback fails closed before any launch: missing token,
+    position or output pointers, a history without its count, a negative history
+    capacity, a cache of the wrong batch or a short workspace."""
+    arr = _layers()
+    m = _model(arr)
+    kv = Q4dKVCache(FAKE, 1, 1, 8, 512, 128)
+    ws_bytes = lib.q4d_workspace_bytes(ctypes.byref(m), 1)
+    f = lib.q4d_run_one_token_feedback
+
+    def call(tok=FAKE, pos=FAKE, nxt=FAKE, score=FAKE, ht=None, hc=None, cap=0, kvd=kv, wsb=ws_bytes):
+        return f(ctypes.byref(m), tok, pos, ctypes.byref(kvd), nxt, score, None, ht, None, hc, cap, FAKE, wsb, None)
+
+    assert call(tok=None) == -7 and call(pos=None) == -7 and call(nxt=None) == -7 and call(score=None) == -7
+    assert call(ht=FAKE, hc=None, cap=4) == -7
+    assert call(ht=FAKE, hc=FAKE, cap=-1) == -7
+    assert call(kvd=Q4dKVCache(FAKE, 1, 2, 8, 512, 128)) == -9
+    assert call(wsb=ws_bytes - 1) == -9
