@@ -105,6 +105,28 @@ def test_gemm_epilogues_exact(dev):
     np.testing.assert_array_equal(r.cpu().numpy(), resid + ref.astype(np.float32))
 
 
+def test_gemm_many_rows_epilogues_exact(dev):
+    """Prefill-sized M (300 rows, a partial last row tile): fp16 output, residual add
+    and the in-place residual (y aliasing resid)."""
+    rng = np.random.default_rng(12)
+    M = 300
+    packed, scale, x, ref = exact_case(rng, 512, 1024, M)
+    w = q4(packed, scale)
+    xd = torch.from_numpy(x).to(dev)
+    print(f"[gemm epilogues many rows] M={M} N=512 K=1024", flush=True)
+    y16 = gemm(w, xd, Q4D_F16).cpu().numpy()
+    np.testing.assert_array_equal(y16, ref.astype(np.float32).astype(np.float16))
+    resid = rng.normal(size=ref.shape).astype(np.float32)
+    r = torch.from_numpy(resid).to(dev)
+    y = gemm(w, xd, Q4D_F32, resid=r).cpu().numpy()
+    np.testing.assert_array_equal(y, resid + ref.astype(np.float32))
+    desc = w.descriptor()
+    check(_lib.load().q4d_gemm(ctypes.byref(desc), xd.data_ptr(), M, r.data_ptr(), Q4D_F32, r.data_ptr(),
+                               current_stream()), "q4d_gemm")
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(r.cpu().numpy(), resid + ref.astype(np.float32))
+
+
 def gemm_splitk(w, x: torch.Tensor, ksplit: int, y_dtype=Q4D_F32, resid: torch.Tensor | None = None,
                 y: torch.Tensor | None = None) -> torch.Tensor:
     rows, cols = w.shape
@@ -142,6 +164,22 @@ def test_gemm_splitk_integer_exact(dev, N, K, M, ksplit):
     r = torch.from_numpy(resid).to(dev)
     gemm_splitk(w, xd, ksplit, Q4D_F32, resid=r, y=r)  # in place, as the residual stream
     np.testing.assert_array_equal(r.cpu().numpy(), resid + ref.astype(np.float32))
+
+
+@pytest.mark.parametrize("ksplit", [0, 2, 4])
+@pytest.mark.parametrize("N,K,M", [(1024, 2048, 300), (1024, 3072, 2048)])
+def test_gemm_many_rows_splitk_integer_exact(dev, N, K, M, ksplit):
+    """Split-K at prefill-sized M with the residual epilogue: the prefill down shape
+    (N = 1024, K = 3072, M = 2048) with a 2-way split runs the pipelined kernel
+    (128 tiles x 2 splits fill the device in one round), 4-way and automatic splits
+    the 128-row-tile kernel; M = 300 ends on a partial row tile."""
+    rng = np.random.default_rng(N + K + M + ksplit)
+    packed, scale, x, ref = exact_case(rng, N, K, M)
+    print(f"[gemm splitk many rows] M={M} N={N} K={K} ksplit={ksplit}", flush=True)
+    resid = rng.normal(size=ref.shape).astype(np.float32)
+    y = gemm_splitk(q4(packed, scale), torch.from_numpy(x).to(dev), ksplit,
+                    resid=torch.from_numpy(resid).to(dev)).cpu().numpy()
+    np.testing.assert_array_equal(y, resid + ref.astype(np.float32))
 
 
 def test_gemm_splitk_real_weights_match_unsplit(dev, golden):
