@@ -563,10 +563,24 @@ int q4d_decode_batch(const q4d_model_t* model, const int32_t* tokens, const int3
   int32_t* status = ws_ptr<int32_t>(ws, W.status);
   float* part = ws_ptr<float>(ws, W.gemm_part);  // split-K tiles of the M = batch GEMMs
   if ((rc = launch_embedding(&model->embed_tokens, tokens, batch, hidden, status, st))) return rc;
+  // the first layer's input RMSNorm; later ones come out of the previous layer's down
+  // projection, whose split-K reduction and residual run fused with it
+  if ((rc = launch_rms_norm(hidden, model->layers[0].input_layernorm, model->rms_norm_eps, batch, H, xh, Q4D_F16,
+                            st)))
+    return rc;
+  // o_proj / down + residual, then the RMSNorm that follows (gamma): the split-K sums,
+  // the residual and the norm as one kernel when the GEMM was split
+  auto resid_then_norm = [&](GemmArgs& g, const float* gamma) -> int {
+    int ks = 1;
+    g.defer_reduce = 1;
+    g.ksplit_used = &ks;
+    int r = launch_gemm(g, EP_RESID, false, st);
+    if (r) return r;
+    if (ks > 1) return launch_splitk_resid_norm(g, ks, gamma, model->rms_norm_eps, xh, st);
+    return launch_rms_norm(hidden, gamma, model->rms_norm_eps, batch, H, xh, Q4D_F16, st);
+  };
   for (int l = 0; l < model->num_layers; ++l) {
     const q4d_layer_t& L = model->layers[l];
-    if ((rc = launch_rms_norm(hidden, L.input_layernorm, model->rms_norm_eps, batch, H, xh, Q4D_F16, st)))
-      return rc;
     GemmArgs g;
     memset(&g, 0, sizeof(g));
     g.w[0] = L.q_proj.w; g.s[0] = L.q_proj.s;
@@ -619,10 +633,8 @@ int q4d_decode_batch(const q4d_model_t* model, const int32_t* tokens, const int3
     g.N = H; g.K = qd; g.M = batch;
     g.x = attn; g.y = hidden; g.ldy = H; g.resid = hidden;
     g.part = part; g.part_cap = W.gemm_part_floats;
-    if ((rc = launch_gemm(g, EP_RESID, false, st))) return rc;
+    if ((rc = resid_then_norm(g, L.post_attention_layernorm))) return rc;
 
-    if ((rc = launch_rms_norm(hidden, L.post_attention_layernorm, model->rms_norm_eps, batch, H, xh, Q4D_F16, st)))
-      return rc;
     memset(&g, 0, sizeof(g));
     g.w[0] = L.gate_proj.w; g.s[0] = L.gate_proj.s;
     g.w[1] = L.up_proj.w;   g.s[1] = L.up_proj.s;
@@ -640,7 +652,11 @@ int q4d_decode_batch(const q4d_model_t* model, const int32_t* tokens, const int3
     g.N = H; g.K = I; g.M = batch;
     g.x = act; g.y = hidden; g.ldy = H; g.resid = hidden;
     g.part = part; g.part_cap = W.gemm_part_floats;
-    if ((rc = launch_gemm(g, EP_RESID, false, st))) return rc;
+    if (l + 1 < model->num_layers) {
+      if ((rc = resid_then_norm(g, model->layers[l + 1].input_layernorm))) return rc;
+    } else if ((rc = launch_gemm(g, EP_RESID, false, st))) {
+      return rc;
+    }
   }
   return run_lm_head_batch(model, hidden, batch, next_tokens, scores, logits, ws, W, st);
 }

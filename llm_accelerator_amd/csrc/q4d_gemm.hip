@@ -788,6 +788,7 @@ static int launch_gemm_inst(const GemmArgs& a, hipStream_t st) {
                  ks > a.K / kGemmBK))
     return Q4D_ERR_CAPACITY;
   constexpr int NW = BM == 128 ? kGemmWaves128 : kGemmWaves64;
+  if (a.ksplit_used) *a.ksplit_used = ks;
   hipLaunchKernelGGL((q4_gemm_kernel<BM, EP, PAIR, NW>), dim3(nblk, mblk, ks), dim3(NW * 64), 0, st, a);
   int rc = check_launch();
   if (rc || ks == 1 || a.defer_reduce) return rc;
@@ -836,6 +837,7 @@ static int launch_gemm_pipe(const GemmArgs& a, hipStream_t st) {
                  ks > a.K / kGemmBK))
     return Q4D_ERR_CAPACITY;
   const dim3 grid(nblk, mblk, ks);
+  if (a.ksplit_used) *a.ksplit_used = ks;
   switch (a.K / kGemmBK / ks) {
     case 16: hipLaunchKernelGGL((q4_gemm_pipe_kernel<EP, PAIR, 16>), grid, dim3(512), 0, st, a); break;
     case 24: hipLaunchKernelGGL((q4_gemm_pipe_kernel<EP, PAIR, 24>), grid, dim3(512), 0, st, a); break;

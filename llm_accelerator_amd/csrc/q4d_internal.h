@@ -215,6 +215,7 @@ struct GemmArgs {
   size_t part_cap;
   int ksplit;
   int defer_reduce;  // with a split, leave the partials for launch_splitk_resid_norm
+  int* ksplit_used;  // optional: receives the split launch_gemm ran (1: the epilogue was applied)
 };
 constexpr int kGemmMaxSplit = 16;
 int launch_gemm(const GemmArgs& a, int ep, bool pair, hipStream_t st);
