@@ -84,9 +84,22 @@ __device__ __forceinline__ float load_dev(const float* p) {
   return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// The argument block's fields, loaded as one batch of scalar loads at kernel entry
+// (left to itself the compiler interleaved the field loads with the position read
+// and the control flow around it: four dependent scalar round trips before the
+// first K/V load).
+__device__ __forceinline__ void attn_preload(const AttnArgs& a) {
+  asm volatile("" ::"s"(a.fused), "s"(a.merge), "s"(a.chunk), "s"(a.qkv), "s"(a.q), "s"(a.q_gamma),
+               "s"(a.k_gamma), "s"(a.eps), "s"(a.scaling), "s"(a.rope_cos), "s"(a.rope_sin), "s"(a.kcache),
+               "s"(a.vcache), "s"(a.positions), "s"(a.batch), "s"(a.qh), "s"(a.kvh), "s"(a.d), "s"(a.max_ctx),
+               "s"(a.nsplit_max), "s"(a.part_ml), "s"(a.part_acc), "s"(a.counters), "s"(a.out), "s"(a.out_dtype),
+               "s"(a.status));
+}
+
 // CH positions per chunk (64 or 128); thread t owns positions t/16 + 16 i, i < CH/16.
 template <int CH>
 __global__ __launch_bounds__(256) void attn_kernel(const AttnArgs a) {
+  attn_preload(a);
   constexpr int D = 128;
   constexpr int NPT = CH / 16;  // positions per thread
   const int s = blockIdx.x, j = blockIdx.y, b = blockIdx.z;
@@ -374,6 +387,7 @@ __global__ __launch_bounds__(256) void attn_kernel(const AttnArgs a) {
 // of loads.  Same thread mapping, prologue and partial format as
 // attn_kernel<64>.
 __global__ __launch_bounds__(256) void attn_span_kernel(const AttnArgs a, int span) {
+  attn_preload(a);
   constexpr int D = 128, CH = 64, NPT = CH / 16;
   const int s = blockIdx.x, j = blockIdx.y, b = blockIdx.z;
   const int t = threadIdx.x, lane = t & 63;
