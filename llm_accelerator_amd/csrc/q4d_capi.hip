@@ -761,7 +761,6 @@ int q4d_prefill(const q4d_model_t* model, const int32_t* tokens, int32_t n_token
   const int qh = model->num_q_heads, kvh = model->num_kv_heads, d = model->head_dim;
   float* hidden = ws_ptr<float>(ws, P.hidden);
   uint16_t* xh = ws_ptr<uint16_t>(ws, P.xh);
-  float* qkv = ws_ptr<float>(ws, P.qkv);
   uint16_t* act = ws_ptr<uint16_t>(ws, P.act);
   if ((rc = launch_embedding(&model->embed_tokens, tokens, n, hidden, ws_ptr<int32_t>(ws, P.base.status), st)))
     return rc;
@@ -769,26 +768,12 @@ int q4d_prefill(const q4d_model_t* model, const int32_t* tokens, int32_t n_token
   for (int l = 0; l < model->num_layers; ++l) {
     const q4d_layer_t& L = model->layers[l];
     // input RMSNorm -> fp16 (layers after the first get it from the previous down GEMM's
-    // fused reduction), then q|k|v as one three-segment GEMM
+    // fused reduction), then q|k|v as one three-segment GEMM whose epilogue applies the
+    // q/k RMSNorm and RoPE and appends K/V for all n positions
     if (l == 0 && (rc = launch_rms_norm(hidden, L.input_layernorm, model->rms_norm_eps, n, H, xh, Q4D_F16, st)))
       return rc;
-    GemmArgs g;
-    memset(&g, 0, sizeof(g));
-    g.w[0] = L.q_proj.w; g.s[0] = L.q_proj.s;
-    g.w[1] = L.k_proj.w; g.s[1] = L.k_proj.s;
-    g.w[2] = L.v_proj.w; g.s[2] = L.v_proj.s;
-    g.seg_end[0] = L.q_proj.rows;
-    g.seg_end[1] = g.seg_end[0] + L.k_proj.rows;
-    g.seg_end[2] = g.seg_end[1] + L.v_proj.rows;
-    g.nseg = 3;
-    g.N = g.seg_end[2]; g.K = H; g.M = n;
-    g.x = xh; g.y = qkv; g.ldy = g.N;
-    if ((rc = launch_gemm(g, EP_F32, false, st))) return rc;
-
-    // q/k RMSNorm + RoPE, K/V append for all n positions, causal GQA attention
     PrefillArgs pa;
     memset(&pa, 0, sizeof(pa));
-    pa.qkv = qkv;
     pa.q_gamma = L.q_norm;
     pa.k_gamma = L.k_norm;
     pa.eps = model->rms_norm_eps;
@@ -802,7 +787,21 @@ int q4d_prefill(const q4d_model_t* model, const int32_t* tokens, int32_t n_token
     pa.q16 = ws_ptr<_Float16>(ws, P.q16);
     pa.out = ws_ptr<_Float16>(ws, P.attn);
     pa.n = n; pa.p0 = start_pos; pa.qh = qh; pa.kvh = kvh; pa.max_ctx = model->max_ctx;
-    if ((rc = launch_prefill_rope(pa, st))) return rc;
+    GemmArgs g;
+    memset(&g, 0, sizeof(g));
+    g.w[0] = L.q_proj.w; g.s[0] = L.q_proj.s;
+    g.w[1] = L.k_proj.w; g.s[1] = L.k_proj.s;
+    g.w[2] = L.v_proj.w; g.s[2] = L.v_proj.s;
+    g.seg_end[0] = L.q_proj.rows;
+    g.seg_end[1] = g.seg_end[0] + L.k_proj.rows;
+    g.seg_end[2] = g.seg_end[1] + L.v_proj.rows;
+    g.nseg = 3;
+    g.N = g.seg_end[2]; g.K = H; g.M = n;
+    g.x = xh;
+    g.rope = pa;
+    if ((rc = launch_gemm(g, EP_ROPE, false, st))) return rc;
+
+    // causal GQA attention over positions [0, start_pos + n)
     if ((rc = launch_prefill_attention(pa, st))) return rc;
 
     // o_proj + residual, post-attention RMSNorm, gate/up + SwiGLU, down + residual

@@ -126,6 +126,11 @@ __device__ __forceinline__ float wave_sum_dpp(float v) {
   return v + dpp_f<kDppRowBcast31, 0xC>(v);
 }
 
+// Sum of all 64 lanes, in every lane.
+__device__ __forceinline__ float wave_sum_bcast(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wave_sum_dpp(v)), 63));
+}
+
 __device__ __forceinline__ float shfl_xor_f(float v, int mask) {
   return __shfl_xor(v, mask, kWave);
 }

@@ -19,8 +19,9 @@
 //
 // Epilogues: fp32 / fp16 store, residual add (common.py:284,297), SwiGLU of a
 // gate/up row pair (common.py:293-295; the B tile then holds 64 gate rows and
-// the matching 64 up rows), and per-row argmax partials over the block's
-// columns for the batched LM head (lowest index wins ties).
+// the matching 64 up rows), per-row argmax partials over the block's columns
+// for the batched LM head (lowest index wins ties), and prefill's q|k|v heads:
+// q/k RMSNorm + RoPE + K/V append straight from the accumulators (EP_ROPE).
 //
 // Split-K: when the output tiles alone cannot fill the device (batched
 // decode: M = 64 rows, N = 1024 gives 8 tiles), blockIdx.z takes a
@@ -152,6 +153,101 @@ __device__ __forceinline__ void gemm_store_lds(_Float16 (*As)[kGemmLds], _Float1
   for (int q = 0; q < 4; ++q) dst[q] = u32x4{out[4 * q], out[4 * q + 1], out[4 * q + 2], out[4 * q + 3]};
 }
 
+// ---- q|k|v epilogue of prefill (EP_ROPE) -------------------------------------------
+// An output tile's 128 columns are one head (head_dim = the N tile): head h = nblk,
+// q heads [0, qh), k heads [qh, qh + kvh), v heads after.  Per token row, q and k get
+// the per-head RMSNorm (common.py:258-262) and RoPE (common.py:264-268); q, scaled by
+// attention scaling * log2(e), goes to q16[h][token] as fp16; k and v go to the fp16
+// cache at position p0 + token (append_cache, common.py:186-189).  The tile's columns
+// are dealt to the waves as for a gate/up pair: wave wn holds dims d = 32 wn + 16 j + cl
+// (j = 0, 1) in acc[.][j] and their rotate-half partners d + 64 in acc[.][j + 2], so
+// the rotation is lane-local; the sum of squares of a row is a 16-lane reduction per
+// wave plus one exchange through LDS between the two waves of the row.
+template <int BM, int MI>
+__device__ __forceinline__ void rope_epilogue(const GemmArgs& a, const f32x4 (&acc)[MI][4], float* ssx, int m0,
+                                              int nblk, int wm, int wn, int lane) {
+  const PrefillArgs& R = a.rope;
+  const int h = nblk, cl = lane & 15, rq = (lane >> 4) * 4;
+  if (h >= R.qh + R.kvh) {  // v head: fp16 into the cache
+    uint16_t* vb = R.vcache + (size_t)(h - R.qh - R.kvh) * R.max_ctx * kGemmBN;
+#pragma unroll
+    for (int i = 0; i < MI; ++i)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int tok = m0 + wm + 16 * i + rq + r;
+        if (tok >= a.M) continue;
+        uint16_t* dst = vb + (size_t)(R.p0 + tok) * kGemmBN;
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          const int d = 32 * wn + 16 * j + cl;
+          dst[d] = __builtin_bit_cast(uint16_t, (_Float16)acc[i][j][r]);
+          dst[d + 64] = __builtin_bit_cast(uint16_t, (_Float16)acc[i][j + 2][r]);
+        }
+      }
+    return;
+  }
+  const bool isq = h < R.qh;
+  const float* gam = isq ? R.q_gamma : R.k_gamma;
+  float g0[2], g1[2], cs[MI][4][2], sn[MI][4][2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    g0[j] = gam[32 * wn + 16 * j + cl];
+    g1[j] = gam[64 + 32 * wn + 16 * j + cl];
+  }
+#pragma unroll
+  for (int i = 0; i < MI; ++i)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      int tok = m0 + wm + 16 * i + rq + r;
+      tok = tok < a.M ? tok : a.M - 1;
+      const size_t tb = (size_t)(R.p0 + tok) * (kGemmBN / 2) + 32 * wn + cl;
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        cs[i][r][j] = R.rope_cos[tb + 16 * j];
+        sn[i][r][j] = R.rope_sin[tb + 16 * j];
+      }
+    }
+  // sum of squares of each row over this wave's 64 columns, then over both waves
+#pragma unroll
+  for (int i = 0; i < MI; ++i)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      float v = acc[i][0][r] * acc[i][0][r];
+      v = fmaf(acc[i][1][r], acc[i][1][r], v);
+      v = fmaf(acc[i][2][r], acc[i][2][r], v);
+      v = fmaf(acc[i][3][r], acc[i][3][r], v);
+      v = row16_sum(v);
+      if (cl == 0) ssx[wn * BM + wm + 16 * i + rq + r] = v;
+    }
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < MI; ++i)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int row = wm + 16 * i + rq + r, tok = m0 + row;
+      if (tok >= a.M) continue;
+      const float ss = ssx[row] + ssx[BM + row];
+      const float inv = 1.0f / sqrtf(ss / (float)kGemmBN + R.eps);
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int d = 32 * wn + 16 * j + cl;
+        const float n0 = (acc[i][j][r] * inv) * g0[j], n1 = (acc[i][j + 2][r] * inv) * g1[j];
+        // rotate_half: dim d < 64 takes -x[d + 64], dim d + 64 takes x[d]
+        const float r0 = n0 * cs[i][r][j] - n1 * sn[i][r][j];
+        const float r1 = n1 * cs[i][r][j] + n0 * sn[i][r][j];
+        if (isq) {
+          _Float16* dst = R.q16 + ((size_t)h * R.n + tok) * kGemmBN;
+          dst[d] = (_Float16)(r0 * R.qscale);
+          dst[d + 64] = (_Float16)(r1 * R.qscale);
+        } else {
+          uint16_t* dst = R.kcache + ((size_t)(h - R.qh) * R.max_ctx + R.p0 + tok) * kGemmBN;
+          dst[d] = __builtin_bit_cast(uint16_t, (_Float16)r0);
+          dst[d + 64] = __builtin_bit_cast(uint16_t, (_Float16)r1);
+        }
+      }
+    }
+}
+
 // NW waves per block: NW / 2 along M x 2 along N; each wave owns
 // (BM / (NW / 2)) x 64 of the output.
 template <int BM, int EP, bool PAIR, int NW>
@@ -195,11 +291,13 @@ __global__ __launch_bounds__(NW * 64) void q4_gemm_kernel(const GemmArgs a) {
 #pragma unroll
     for (int j = 0; j < NI; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  // B-tile rows read by this wave's four 16-col tiles
+  // B-tile rows read by this wave's four 16-col tiles (a gate/up pair and EP_ROPE:
+  // 32 columns from each half of the tile)
   int brow[NI];
 #pragma unroll
   for (int j = 0; j < NI; ++j)
-    brow[j] = PAIR ? ((j < 2) ? (32 * wn + 16 * j) : (64 + 32 * wn + 16 * (j - 2))) : (64 * wn + 16 * j);
+    brow[j] = PAIR || EP == EP_ROPE ? ((j < 2) ? (32 * wn + 16 * j) : (64 + 32 * wn + 16 * (j - 2)))
+                                    : (64 * wn + 16 * j);
 
   const SegPtrs P = seg_ptrs(a);
   GemmTileLoad L;
@@ -228,6 +326,10 @@ __global__ __launch_bounds__(NW * 64) void q4_gemm_kernel(const GemmArgs a) {
   }
 
   // ---- epilogue: lane holds rows (lane/16)*4 + r of each 16x16 tile, column lane%16
+  if constexpr (EP == EP_ROPE) {  // no split (the launcher checks)
+    rope_epilogue<BM, MI>(a, acc, reinterpret_cast<float*>(&Bs[0][0][0]), m0, nblk, wm, wn, lane);
+    return;
+  }
   const int cl = lane & 15, rq = (lane >> 4) * 4;
   if (EP != EP_ARGMAX && ksplit > 1) {
     // raw split tile: [z][m][n], PAIR: gate columns n, up columns N + n
@@ -574,7 +676,8 @@ __global__ __launch_bounds__(512) void q4_gemm_pipe_kernel(const GemmArgs a) {
   int brow[NI];
 #pragma unroll
   for (int j = 0; j < NI; ++j)
-    brow[j] = PAIR ? ((j < 2) ? (32 * wn + 16 * j) : (64 + 32 * wn + 16 * (j - 2))) : (64 * wn + 16 * j);
+    brow[j] = PAIR || EP == EP_ROPE ? ((j < 2) ? (32 * wn + 16 * j) : (64 + 32 * wn + 16 * (j - 2)))
+                                    : (64 * wn + 16 * j);
 
   // scale codes stored; steps 0, 1, 2 go out; step 0 is dequantised once landed
   __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
@@ -596,6 +699,11 @@ __global__ __launch_bounds__(512) void q4_gemm_pipe_kernel(const GemmArgs a) {
   __builtin_amdgcn_s_waitcnt(0x0070);  // vmcnt(0) expcnt(7) lgkmcnt(0)
 
   // ---- epilogue (as in q4_gemm_kernel)
+  if constexpr (EP == EP_ROPE) {  // no split (the launcher checks)
+    __syncthreads();  // every wave's MFMAs are done with the B tiles
+    rope_epilogue<BM, MI>(a, acc, reinterpret_cast<float*>(&g_pb0[0][0]), m0, nblk, wm, wn, lane);
+    return;
+  }
   const int cl = lane & 15, rq = (lane >> 4) * 4;
   if (ksplit > 1) {
     const int wp = PAIR ? 2 * a.N : a.N;
@@ -792,7 +900,7 @@ static int launch_gemm_inst(const GemmArgs& a, hipStream_t st) {
   hipLaunchKernelGGL((q4_gemm_kernel<BM, EP, PAIR, NW>), dim3(nblk, mblk, ks), dim3(NW * 64), 0, st, a);
   int rc = check_launch();
   if (rc || ks == 1 || a.defer_reduce) return rc;
-  if constexpr (EP != EP_ARGMAX) {
+  if constexpr (EP != EP_ARGMAX && EP != EP_ROPE) {
     const int n4 = a.M * (a.N / 4);
     hipLaunchKernelGGL((splitk_reduce_kernel<EP, PAIR>), dim3((n4 + 255) / 256), dim3(256), 0, st, a, ks);
   }
@@ -847,8 +955,10 @@ static int launch_gemm_pipe(const GemmArgs& a, hipStream_t st) {
   }
   int rc = check_launch();
   if (rc || ks == 1 || a.defer_reduce) return rc;
-  const int n4 = a.M * (a.N / 4);
-  hipLaunchKernelGGL((splitk_reduce_kernel<EP, PAIR>), dim3((n4 + 255) / 256), dim3(256), 0, st, a, ks);
+  if constexpr (EP != EP_ROPE) {
+    const int n4 = a.M * (a.N / 4);
+    hipLaunchKernelGGL((splitk_reduce_kernel<EP, PAIR>), dim3((n4 + 255) / 256), dim3(256), 0, st, a, ks);
+  }
   return check_launch();
 }
 
@@ -860,6 +970,7 @@ static int launch_gemm_bm(const GemmArgs& a, int ep, bool pair, hipStream_t st) 
     case EP_F16: return launch_gemm_inst<BM, EP_F16, false>(a, st);
     case EP_RESID: return launch_gemm_inst<BM, EP_RESID, false>(a, st);
     case EP_ARGMAX: return launch_gemm_inst<BM, EP_ARGMAX, false>(a, st);
+    case EP_ROPE: return launch_gemm_inst<BM, EP_ROPE, false>(a, st);
     default: return Q4D_ERR_SHAPE;
   }
 }
@@ -881,6 +992,12 @@ int launch_gemm(const GemmArgs& a, int ep, bool pair, hipStream_t st) {
   if (!a.x || !aligned(a.x, 16)) return a.x ? Q4D_ERR_BAD_ADDR : Q4D_ERR_NULL;
   if (ep == EP_ARGMAX) {
     if (!a.part_score || !a.part_idx) return Q4D_ERR_NULL;
+  } else if (ep == EP_ROPE) {
+    const PrefillArgs& R = a.rope;
+    if (pair || a.part || a.ksplit > 1) return Q4D_ERR_SHAPE;  // the epilogue needs whole tiles
+    if (R.qh <= 0 || R.kvh <= 0 || a.N != (R.qh + 2 * R.kvh) * kGemmBN || R.n != a.M) return Q4D_ERR_SHAPE;
+    if (!R.q_gamma || !R.k_gamma || !R.rope_cos || !R.rope_sin || !R.kcache || !R.vcache || !R.q16)
+      return Q4D_ERR_NULL;
   } else if (!a.y) {
     return Q4D_ERR_NULL;
   }
@@ -892,6 +1009,7 @@ int launch_gemm(const GemmArgs& a, int ep, bool pair, hipStream_t st) {
       case EP_F32: return launch_gemm_pipe<EP_F32, false>(a, st);
       case EP_F16: return launch_gemm_pipe<EP_F16, false>(a, st);
       case EP_RESID: return launch_gemm_pipe<EP_RESID, false>(a, st);
+      case EP_ROPE: return launch_gemm_pipe<EP_ROPE, false>(a, st);
       default: return Q4D_ERR_SHAPE;
     }
   }

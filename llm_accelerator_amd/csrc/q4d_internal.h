@@ -96,7 +96,7 @@ inline int check_launch() {
 // to emb_out (the residual stream), and an id outside the table gives zeros and
 // sets Q4D_STATUS_BAD_TOKEN in emb_status, as the embedding kernel does.
 enum XMode { X_F16 = 0, X_F32 = 1, X_RMS = 2, X_ATTN = 3, X_EMB = 4 };
-enum EpMode { EP_F16 = 0, EP_F32 = 1, EP_RESID = 2, EP_SWIGLU = 3, EP_ARGMAX = 4 };
+enum EpMode { EP_F16 = 0, EP_F32 = 1, EP_RESID = 2, EP_SWIGLU = 3, EP_ARGMAX = 4, EP_ROPE = 5 };
 
 struct GemvArgs {
   // Up to three row segments stacked into one logical [rows, K] matrix.
@@ -190,6 +190,22 @@ struct AttnArgs {
 int launch_attention(const AttnArgs& a, hipStream_t stream);
 
 // ---- Q4 GEMM on MFMA (prefill / batched decode) ------------------------------
+// Prefill's per-head work on the q|k|v projections (q/k RMSNorm, RoPE, K/V append)
+// and its causal attention: the q|k|v GEMM's EP_ROPE epilogue and
+// launch_prefill_attention.
+struct PrefillArgs {
+  const float* q_gamma;
+  const float* k_gamma;
+  float eps;
+  float qscale;            // attention scaling * log2(e), folded into q
+  const float* rope_cos;   // [max_ctx][head_dim / 2]
+  const float* rope_sin;
+  uint16_t* kcache;        // K plane of the layer and sequence: [kvh][max_ctx][head_dim] fp16
+  uint16_t* vcache;
+  _Float16* q16;           // [qh][n][head_dim] normed, roped, pre-scaled q
+  _Float16* out;           // [n][qh * head_dim] attention output
+  int n, p0, qh, kvh, max_ctx;
+};
 struct GemmArgs {
   const uint8_t* w[3];
   const uint16_t* s[3];
@@ -216,6 +232,11 @@ struct GemmArgs {
   int ksplit;
   int defer_reduce;  // with a split, leave the partials for launch_splitk_resid_norm
   int* ksplit_used;  // optional: receives the split launch_gemm ran (1: the epilogue was applied)
+  // EP_ROPE (prefill q|k|v, no split): the 128 columns of an output tile are one
+  // head, q heads then k heads then v heads; q rows go normed, roped and scaled to
+  // rope.q16, k rows normed and roped and v rows as they are to the cache planes
+  // at positions rope.p0 + m.  y is not written.
+  PrefillArgs rope;
 };
 constexpr int kGemmMaxSplit = 16;
 int launch_gemm(const GemmArgs& a, int ep, bool pair, hipStream_t st);
@@ -227,27 +248,12 @@ int launch_splitk_resid_norm(const GemmArgs& a, int ksplit, const float* gamma, 
 int launch_argmax_rows(const float* part_score, const int* part_idx, int nparts, int M, int32_t* out_token,
                        float* out_score, hipStream_t st);
 
-// ---- prefill (many tokens of one sequence) ---------------------------------------
-struct PrefillArgs {
-  const float* qkv;        // [n][qh + 2 kvh][head_dim] fp32 raw projections
-  const float* q_gamma;
-  const float* k_gamma;
-  float eps;
-  float qscale;            // attention scaling * log2(e), folded into q
-  const float* rope_cos;   // [max_ctx][head_dim / 2]
-  const float* rope_sin;
-  uint16_t* kcache;        // K plane of the layer and sequence: [kvh][max_ctx][head_dim] fp16
-  uint16_t* vcache;
-  _Float16* q16;           // [qh][n][head_dim] normed, roped, pre-scaled q
-  _Float16* out;           // [n][qh * head_dim] attention output
-  int n, p0, qh, kvh, max_ctx;
-};
 // ---- integer Q4 GEMV of the fixed-point path (q4d_int.hip) ------------------
 int launch_gemv_q26(const q4d_matrix_t* w, const int32_t* x, int64_t* y_q26, int32_t* y_q12, int32_t* saturated,
                     hipStream_t st);
 int launch_argmax_q26(const int64_t* scores, int n, int32_t* tok, int64_t* score, hipStream_t st);
 
-int launch_prefill_rope(const PrefillArgs& a, hipStream_t st);
+// ---- prefill (many tokens of one sequence) ---------------------------------------
 int launch_prefill_attention(const PrefillArgs& a, hipStream_t st);
 
 // Prefill workspace: the single-token layout (status, counters, LM-head argmax)
@@ -260,7 +266,6 @@ struct PrefillLayout {
   WsLayout base;
   size_t hidden;  // f32 [n][hidden]
   size_t xh;      // f16 [n][max(hidden, intermediate)]
-  size_t qkv;     // f32 [n][(qh + 2 kvh) * d]
   size_t q16;     // f16 [qh][n][d]
   size_t attn;    // f16 [n][qh * d]
   size_t act;     // f16 [n][intermediate]
@@ -272,12 +277,11 @@ inline PrefillLayout prefill_layout(const q4d_model_t* m, int n) {
   PrefillLayout P{};
   P.base = ws_layout(m, 1);
   const size_t A = 256;
-  const int d = m->head_dim, qh = m->num_q_heads, kvh = m->num_kv_heads;
+  const int d = m->head_dim, qh = m->num_q_heads;
   const int wx = m->hidden_size > m->intermediate_size ? m->hidden_size : m->intermediate_size;
   size_t o = align_up(P.base.total, A);
   P.hidden = o; o = align_up(o + (size_t)n * m->hidden_size * 4, A);
   P.xh = o;     o = align_up(o + (size_t)n * wx * 2, A);
-  P.qkv = o;    o = align_up(o + (size_t)n * (qh + 2 * kvh) * d * 4, A);
   P.q16 = o;    o = align_up(o + (size_t)qh * n * d * 2, A);
   P.attn = o;   o = align_up(o + (size_t)n * qh * d * 2, A);
   P.act = o;    o = align_up(o + (size_t)n * m->intermediate_size * 2, A);

@@ -1,19 +1,12 @@
-// Prefill of many tokens of one sequence (gfx950): the per-token q/k RMSNorm,
-// RoPE and KV-cache append for all tokens, and causal GQA attention on MFMA.
+// Causal GQA attention of a prefill on MFMA (gfx950).
 //
 // The reference's prefill is serial: run_manual_one_token once per prompt
 // token (10_validate_full_run_one_token.py:81-135), each call appending one
 // K/V row and attending over the cache (common.py:231-298).  Here the n new
 // tokens at positions p0 .. p0 + n - 1 go through each layer together; the
-// projections are Q4 GEMMs (q4d_gemm.hip) and this file supplies the rest.
-//
-// prefill_rope_kernel: one wave per (token, row) where the rows of a token
-// are its 16 q heads, 8 k heads and 8 v heads.  Lane l holds dims l and
-// l + 64 (each other's rotate-half partner), so per-head RMSNorm
-// (common.py:258-262) and RoPE (common.py:264-268) are wave-local.  q goes
-// to an fp16 [q_head][token][128] buffer with the softmax scale and log2(e)
-// folded in; k (normed, roped) and v go to the fp16 KV cache at their
-// positions (append_cache, common.py:186-189).
+// projections are Q4 GEMMs (q4d_gemm.hip), whose q|k|v epilogue also applies
+// the per-head q/k RMSNorm and RoPE, appends K/V to the cache and leaves q as
+// fp16 [q_head][token][128] with the softmax scale and log2(e) folded in.
 //
 // prefill_attn_kernel: flash attention forward, causal, one block per
 // (64-query tile, q head), 4 waves of 16 queries.  Per 64-key tile:
@@ -44,47 +37,6 @@ constexpr int kBK = 64;   // keys per tile
 constexpr int kLdk = kD + 8;   // fp16 row stride of the K tile
 constexpr int kLdv = kBK + 4;  // fp16 row stride of the V^T tile (+4 beat +8, +12 and +16 when measured)
 constexpr float kRescale = 8.0f;  // log2 headroom of the lazily moved running max
-
-__device__ __forceinline__ float wave_sum_bcast(float v) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wave_sum_dpp(v)), 63));
-}
-
-__global__ __launch_bounds__(256) void prefill_rope_kernel(const PrefillArgs a) {
-  const int lane = threadIdx.x & 63;
-  const int row = blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int rows_per_tok = a.qh + 2 * a.kvh;
-  const int tok = row / rows_per_tok, r = row % rows_per_tok;
-  if (tok >= a.n) return;
-  const int pos = a.p0 + tok;
-  const float* src = a.qkv + (size_t)tok * rows_per_tok * kD + (size_t)r * kD;
-  const float x0 = src[lane], x1 = src[lane + 64];
-  if (r >= a.qh + a.kvh) {  // v head: fp16 into the cache
-    const int j = r - a.qh - a.kvh;
-    uint16_t* dst = a.vcache + ((size_t)j * a.max_ctx + pos) * kD;
-    dst[lane] = __builtin_bit_cast(uint16_t, (_Float16)x0);
-    dst[lane + 64] = __builtin_bit_cast(uint16_t, (_Float16)x1);
-    return;
-  }
-  const bool isq = r < a.qh;
-  const float* gam = isq ? a.q_gamma : a.k_gamma;
-  const float c = a.rope_cos[(size_t)pos * (kD / 2) + lane];
-  const float sn = a.rope_sin[(size_t)pos * (kD / 2) + lane];
-  const float ss = wave_sum_bcast(fmaf(x0, x0, x1 * x1));
-  const float inv = 1.0f / sqrtf(ss / (float)kD + a.eps);
-  const float n0 = (x0 * inv) * gam[lane], n1 = (x1 * inv) * gam[lane + 64];
-  // rotate_half: dim d < 64 takes -x[d + 64], dim d >= 64 takes x[d - 64]
-  const float r0 = n0 * c + (-n1) * sn;
-  const float r1 = n1 * c + n0 * sn;
-  if (isq) {
-    _Float16* dst = a.q16 + ((size_t)r * a.n + tok) * kD;
-    dst[lane] = (_Float16)(r0 * a.qscale);
-    dst[lane + 64] = (_Float16)(r1 * a.qscale);
-  } else {
-    uint16_t* dst = a.kcache + ((size_t)(r - a.qh) * a.max_ctx + pos) * kD;
-    dst[lane] = __builtin_bit_cast(uint16_t, (_Float16)r0);
-    dst[lane + 64] = __builtin_bit_cast(uint16_t, (_Float16)r1);
-  }
-}
 
 // Global loads of one K/V tile.  K: thread (kr = t >> 4, kc = t & 15) holds dims
 // 8kc .. 8kc+7 of keys kr + 16b, so 16 lanes store one whole 256-byte K row and the
@@ -263,12 +215,6 @@ __global__ __launch_bounds__(256) void prefill_attn_kernel(const PrefillArgs a) 
 }
 
 }  // namespace
-
-int launch_prefill_rope(const PrefillArgs& a, hipStream_t st) {
-  const int rows = a.n * (a.qh + 2 * a.kvh);
-  hipLaunchKernelGGL(prefill_rope_kernel, dim3((rows + 3) / 4), dim3(256), 0, st, a);
-  return check_launch();
-}
 
 int launch_prefill_attention(const PrefillArgs& a, hipStream_t st) {
   hipLaunchKernelGGL(prefill_attn_kernel, dim3((a.n + kBQ - 1) / kBQ, a.qh), dim3(256), 0, st, a);
