@@ -288,6 +288,38 @@ def run_decode(fmodel, prompt, gen_steps, per_graph, torch, desc=None):
     return out
 
 
+def decode_launch_floor(torch, fmodel, tokens=15, replays=20):
+    """A decode step's 141 launches with their grids, each kernel reduced to one dependent
+    read of the previous launch's 4 KB output (q4d_diag_launch_chain), graph-replayed:
+    what the launches of a token cost without their work.  Grids (blocks x threads) of the
+    step's kernels, as the kernel trace of this leg shows them: q|k|v 512 x 256, attention
+    ceil(max_ctx / 64) x kv_heads blocks of 256, o_proj 128 x 512, gate/up 384 x 256,
+    down 256 x 384, LM head 238 x 1024."""
+    from llm_accelerator_amd import _lib
+    lib = _lib.load()
+    cfg = fmodel.config
+    layer = [(512, 1, 256), ((fmodel.max_ctx + 63) // 64, cfg.num_key_value_heads, 256), (128, 1, 512),
+             (384, 1, 256), (256, 1, 384)]
+    shapes = layer * cfg.num_hidden_layers + [(238, 1, 1024)]
+    n = len(shapes)
+    gx = (ctypes.c_int32 * n)(*[x for x, _, _ in shapes])
+    gy = (ctypes.c_int32 * n)(*[y for _, y, _ in shapes])
+    bl = (ctypes.c_int32 * n)(*[b for _, _, b in shapes])
+    buf = torch.zeros(2048, dtype=torch.float32, device=fmodel.device)
+
+    def chain(i):
+        rc = lib.q4d_diag_launch_chain(ctypes.cast(gx, ctypes.c_void_p), ctypes.cast(gy, ctypes.c_void_p),
+                                       ctypes.cast(bl, ctypes.c_void_p), n, buf.data_ptr(),
+                                       torch.cuda.current_stream().cuda_stream)
+        if rc:
+            raise RuntimeError(f"q4d_diag_launch_chain: {rc}")
+    g = graph_of(chain, tokens, torch)
+    time_graph(g, 2, torch)
+    us = time_graph(g, replays, torch) / tokens * 1e3
+    return {"us_per_token": round(us, 2), "launches_per_token": n,
+            "us_per_launch": round(us / n, 3)}
+
+
 def leg_decode(args, torch, np, fmodel):
     from llm_accelerator_amd import model as M
     fcfg = fmodel.config
@@ -296,6 +328,7 @@ def leg_decode(args, torch, np, fmodel):
     per_graph = max(d for d in range(1, 17) if steps % d == 0)
     flushed = run_decode(fmodel, prompt, steps, per_graph, torch)
     resident = run_decode(fmodel, prompt, steps, per_graph, torch, desc=aliased_descriptor(fmodel))
+    floor = decode_launch_floor(torch, fmodel, tokens=per_graph)
     # step p feeds position p and attends p + 1 positions
     tok_bytes = sum(M.batched_step_bytes(fcfg, 1, p + 1) for p in range(PROMPT, PROMPT + steps)) / steps
     wb = fmodel.weight_bytes()
@@ -309,6 +342,9 @@ def leg_decode(args, torch, np, fmodel):
            "roofline_frac": round(tok_bytes * tok_s / 1e9 / HBM_PEAK_GBPS, 4),
            "generated": flushed["generated"], "status": flushed["status"],
            "launches_per_token": 5 * fcfg.num_hidden_layers + 1,
+           "launch_floor": dict(floor, note="the same 141 launches with their grids, each kernel only one "
+                                            "dependent 4 KB read and write (q4d_diag_launch_chain)",
+                                share=round(floor["us_per_token"] / flushed["us_per_token"], 3)),
            "resident": {"note": "every layer aliased to layer 0's weights: 91 MB per token, inside the 256 MB cache",
                         "tok_s": round(1e6 / resident["us_per_token"], 1),
                         "us_per_token": round(resident["us_per_token"], 2),

@@ -568,6 +568,16 @@ int q4d_session_fixed_runner(void* runner_context, uint32_t input_token_id, uint
 int q4d_quantize_q4(const void* weight, int32_t dtype, int64_t ld, int32_t rows, int32_t cols, uint8_t* packed,
                     uint16_t* scale, int32_t* status, void* stream);
 
+/* ---- diagnostics --------------------------------------------------------------
+ * No counterpart in the reference; for measurement.  Launches n dependent kernels on
+ * `stream`, kernel i with grid (grid_x[i], grid_y[i]) of block[i] threads (a multiple of
+ * 64, at most 1024), each doing one global read of the previous kernel's 4 KB output and
+ * (block 0) writing its own: the launch floor of a chain of kernels with those grids.
+ * grid_x, grid_y, block: host arrays of n (1..4096); buf: device, 2048 floats, 16-byte
+ * aligned. */
+int q4d_diag_launch_chain(const int32_t* grid_x, const int32_t* grid_y, const int32_t* block, int32_t n,
+                          float* buf, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -151,6 +151,7 @@ SIGNATURES = {
                                     c_int32, _P, c_size_t, _P], c_int32),
     "q4d_run_one_token_noalloc": ([POINTER(Q4dModel), _P, _P, POINTER(Q4dKVCache), _P, _P, _P, _P, _P], c_int32),
     "q4d_apply_rope": ([_P, _P, _P, _P, c_int32, c_int32, c_int32, _P], c_int32),
+    "q4d_diag_launch_chain": ([_P, _P, _P, c_int32, _P, _P], c_int32),
     "q4d_advance": ([_P, _P, _P, _P, _P, _P, _P, c_int32, _P], c_int32),
     "q4d_advance_session": ([_P, _P, _P, _P, _P, _P, _P, c_int32, _P, _P], c_int32),
     "q4d_prefill_workspace_bytes": ([POINTER(Q4dModel), c_int32], c_size_t),

@@ -869,4 +869,16 @@ int q4d_apply_rope(const float* x, float* y, const float* cos, const float* sin,
   return launch_apply_rope(x, y, cos, sin, batch, heads, head_dim, as_stream(stream));
 }
 
+int q4d_diag_launch_chain(const int32_t* grid_x, const int32_t* grid_y, const int32_t* block, int32_t n,
+                          float* buf, void* stream) {
+  if (!grid_x || !grid_y || !block || !buf) return Q4D_ERR_NULL;
+  if (n <= 0 || n > 4096) return Q4D_ERR_SHAPE;
+  if (!aligned(buf, 16)) return Q4D_ERR_BAD_ADDR;
+  for (int i = 0; i < n; ++i)
+    if (grid_x[i] < 1 || grid_x[i] > 65535 || grid_y[i] < 1 || grid_y[i] > 65535 || block[i] < 64 ||
+        block[i] > 1024 || block[i] % 64)
+      return Q4D_ERR_SHAPE;
+  return launch_chain(grid_x, grid_y, block, n, buf, as_stream(stream));
+}
+
 }  // extern "C"

@@ -291,6 +291,8 @@ inline PrefillLayout prefill_layout(const q4d_model_t* m, int n) {
 }
 
 int launch_fill_i32(int32_t* p, int32_t v, size_t n, hipStream_t stream);
+int launch_chain(const int32_t* grid_x, const int32_t* grid_y, const int32_t* block, int n, float* buf,
+                 hipStream_t stream);
 int launch_advance_session(int32_t* tokens, int32_t* positions, const int32_t* next_token, const float* score,
                            int32_t* hist_tokens, float* hist_scores, int32_t* hist_count, int32_t hist_capacity,
                            int32_t* stop, hipStream_t stream);

@@ -142,6 +142,30 @@ int launch_fill_i32(int32_t* p, int32_t v, size_t n, hipStream_t stream) {
   return check_launch();
 }
 
+// Launch-floor probe: a kernel that only reads the previous launch's 4 KB output (one
+// dependent global load per thread) and, in block 0, writes its own (in + 1).  A chain
+// of these with the grids of a decode step measures what the launches cost without
+// their work.
+__global__ void chain_kernel(const float* __restrict__ in, float* __restrict__ out) {
+  const int t = threadIdx.x;
+  if (blockIdx.x == 0 && blockIdx.y == 0) {
+    for (int i = t; i < 1024; i += blockDim.x) out[i] = in[i] + 1.0f;
+  } else {
+    const float v = in[t & 1023];
+    if (v != v) out[t & 1023] = v;  // never taken for finite data; keeps the read
+  }
+}
+
+int launch_chain(const int32_t* grid_x, const int32_t* grid_y, const int32_t* block, int n, float* buf,
+                 hipStream_t stream) {
+  for (int i = 0; i < n; ++i) {
+    const float* in = buf + (i & 1) * 1024;
+    float* out = buf + ((i + 1) & 1) * 1024;
+    hipLaunchKernelGGL(chain_kernel, dim3(grid_x[i], grid_y[i]), dim3(block[i]), 0, stream, in, out);
+  }
+  return check_launch();
+}
+
 __global__ void advance_kernel(int32_t* tokens, int32_t* positions, const int32_t* next_token,
                                const float* score, int32_t* hist_tokens, float* hist_scores,
                                int32_t* hist_count, int32_t hist_capacity) {

@@ -240,3 +240,30 @@ def test_feedback_step_validates_on_host(lib):
     assert call(ht=FAKE, hc=FAKE, cap=-1) == -7
     assert call(kvd=Q4dKVCache(FAKE, 1, 2, 8, 512, 128)) == -9
     assert call(wsb=ws_bytes - 1) == -9
+
+
+def test_launch_chain_validates_on_host(lib):
+    """q4d_diag_launch_chain (the launch-floor probe) rejects a missing array or buffer,
+    a chain length outside 1..4096, a grid outside 1..65535, a block that is not a
+    multiple of 64 up to 1024, and an unaligned buffer, before any launch."""
+    f = lib.q4d_diag_launch_chain
+
+    def arr(*v):
+        a = (ctypes.c_int32 * len(v))(*v)
+        return ctypes.cast(a, ctypes.c_void_p), a
+
+    gx, _kx = arr(4, 4)
+    gy, _ky = arr(1, 1)
+    bl, _kb = arr(256, 256)
+    assert f(None, gy, bl, 2, FAKE, None) == -7
+    assert f(gx, gy, bl, 2, None, None) == -7
+    assert f(gx, gy, bl, 0, FAKE, None) == -11
+    assert f(gx, gy, bl, 4097, FAKE, None) == -11
+    assert f(gx, gy, bl, 2, FAKE + 4, None) == -4
+    for bad_gx, bad_gy, bad_bl in (((0, 4), (1, 1), (256, 256)), ((4, 65536), (1, 1), (256, 256)),
+                                   ((4, 4), (1, 0), (256, 256)), ((4, 4), (1, 1), (256, 96)),
+                                   ((4, 4), (1, 1), (2048, 256))):
+        x, _a = arr(*bad_gx)
+        y, _b = arr(*bad_gy)
+        b, _c = arr(*bad_bl)
+        assert f(x, y, b, 2, FAKE, None) == -11, (bad_gx, bad_gy, bad_bl)
