@@ -82,7 +82,12 @@ enum {
 /* Device status word bits (q4d_read_status). */
 enum {
   Q4D_STATUS_BAD_TOKEN = 1,
-  Q4D_STATUS_BAD_POSITION = 2
+  Q4D_STATUS_BAD_POSITION = 2,
+  /* XCD-split decode layer only (no reference counterpart): the workgroups of one kv
+   * head (blockIdx % 8 equal) did not all run on one XCD, or an exchange between them
+   * did not complete within 20 ms (the results of that call are not valid). */
+  Q4D_STATUS_XCD_MAP = 4,
+  Q4D_STATUS_SYNC_TIMEOUT = 8
 };
 
 enum { Q4D_F16 = 0, Q4D_F32 = 1, Q4D_BF16 = 2 };
@@ -142,6 +147,16 @@ int q4d_workspace_init(void* ws, size_t ws_bytes, const q4d_model_t* model, int3
  * enters as an fp16 hi + fp16 lo pair (~22 significant bits); 1 = rounded to
  * fp16.  Process-wide; set it before launching work. */
 int q4d_set_activation_precision(int32_t mode);
+/* Kernel plan of the batch-1 decode layer (q4d_decoder_layer, q4d_run_one_token*; no
+ * reference counterpart, the arithmetic is the same): Q4D_DECODE_XCD (default) runs a
+ * layer as two launches split over the GPU's eight XCDs, one kv head per XCD, with the
+ * XCD's workgroups exchanging data through its L2; Q4D_DECODE_STAGED runs the five
+ * per-stage launches of q4d_layer_stage.  XCD applies to the Qwen3-0.6B shape (hidden
+ * 1024, 16/8 heads of 128, intermediate 3072), max_ctx <= 4096 and activation
+ * precision 2; other models run staged.  Process-wide; set it before capturing graphs.
+ * Returns the previous plan. */
+enum { Q4D_DECODE_XCD = 0, Q4D_DECODE_STAGED = 1 };
+int q4d_set_decode_plan(int32_t plan);
 /* Copy the device status word into *out (synchronises `stream`). */
 int q4d_read_status(const void* ws, size_t ws_bytes, const q4d_model_t* model, int32_t batch,
                     int32_t* out, void* stream);
@@ -265,7 +280,7 @@ int q4d_run_one_token_feedback(const q4d_model_t* model, int32_t* tokens, int32_
  * hipMalloc).  No counterpart in the reference.  Its scratch is a 4 MiB device array
  * inside the library, one per GPU, held until the process ends; the call allocates
  * nothing.  Models whose batch-1 workspace (q4d_workspace_bytes(model, 1)) exceeds
- * 4 MiB are rejected with Q4D_ERR_CAPACITY (Qwen3-0.6B shapes: max_ctx <= 30208).
+ * 4 MiB are rejected with Q4D_ERR_CAPACITY (Qwen3-0.6B shapes: max_ctx <= 27328).
  * status: device int32[1], caller-owned and caller-cleared; the step ORs its
  * Q4D_STATUS_* bits into it.  All calls on one GPU share that GPU's scratch, so calls
  * that overlap on one GPU (two streams, two threads) race; serialise them.  Results

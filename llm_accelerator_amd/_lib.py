@@ -125,6 +125,7 @@ SIGNATURES = {
     "q4d_workspace_bytes": ([POINTER(Q4dModel), c_int32], c_size_t),
     "q4d_workspace_init": ([_P, c_size_t, POINTER(Q4dModel), c_int32, _P], c_int32),
     "q4d_set_activation_precision": ([c_int32], c_int32),
+    "q4d_set_decode_plan": ([c_int32], c_int32),
     "q4d_read_status": ([_P, c_size_t, POINTER(Q4dModel), c_int32, POINTER(c_int32), _P], c_int32),
     "q4d_linear": ([POINTER(Q4dMatrix), _P, c_int32, _P, c_int32, c_int32, _P], c_int32),
     "q4d_rms_norm": ([_P, _P, c_float, c_int32, c_int32, _P, c_int32, _P], c_int32),

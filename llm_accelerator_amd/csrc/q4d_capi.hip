@@ -22,6 +22,7 @@ namespace {
 // Activation precision inside the fused decode: 2 = fp32 activations enter
 // each GEMV as hi+lo fp16 halves (about 22 significant bits), 1 = rounded to fp16.
 int g_act_precision = 2;
+int g_decode_plan = Q4D_DECODE_XCD;
 
 inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 
@@ -106,6 +107,11 @@ struct Feedback {
   int32_t hist_capacity;
 };
 
+bool xcd_eligible(const q4d_model_t* m);
+int run_layer_xcd(const q4d_model_t* m, int l, int in_mode, const float* hin, const int32_t* emb_tokens,
+                  float* hout, const q4d_kv_cache_t* kv, const int32_t* positions, void* ws, const WsLayout& W,
+                  int32_t* status, hipStream_t st);
+
 // One decoder layer, batch 1 (common.py:231-298), five launches; `only`
 // selects a single stage (Q4D_STAGE_*) or -1 for all.  With `emb_tokens` the
 // layer's input is the embedding row of emb_tokens[0], built in the q|k|v
@@ -114,6 +120,11 @@ struct Feedback {
 int run_layer(const q4d_model_t* m, int l, const float* hin, float* hout, const q4d_kv_cache_t* kv,
               const int32_t* positions, void* ws, const WsLayout& W, hipStream_t st, int only = -1,
               int32_t* status = nullptr, const int32_t* emb_tokens = nullptr) {
+  if (only < 0 && xcd_eligible(m)) {
+    int32_t* stw = status ? status : ws_ptr<int32_t>(ws, W.status);
+    return emb_tokens ? run_layer_xcd(m, l, 2, nullptr, emb_tokens, hout, kv, positions, ws, W, stw, st)
+                      : run_layer_xcd(m, l, 1, hin, nullptr, hout, kv, positions, ws, W, stw, st);
+  }
   const q4d_layer_t& L = m->layers[l];
   const int xp = g_act_precision;
   float* qkv = ws_ptr<float>(ws, W.qkv);
@@ -221,6 +232,73 @@ int run_layer(const q4d_model_t* m, int l, const float* hin, float* hout, const 
   return Q4D_OK;
 }
 
+// The XCD-split layer (q4d_xcd.hip) covers the Qwen3-0.6B shape at activation precision 2.
+bool xcd_eligible(const q4d_model_t* m) {
+  return g_decode_plan == Q4D_DECODE_XCD && g_act_precision == 2 && m->hidden_size == 1024 &&
+         m->intermediate_size == kXcdInter && m->num_q_heads == 2 * kXcdGroups && m->num_kv_heads == kXcdGroups &&
+         m->head_dim == 128 && xcd_npt(m->max_ctx) > 0;
+}
+
+XcdBufs xcd_bufs(void* ws, const WsLayout& W, int32_t* status) {
+  XcdBufs x;
+  x.flags = ws_ptr<uint32_t>(ws, W.xflags);
+  x.qkv = ws_ptr<float>(ws, W.xqkv);
+  x.ap = ws_ptr<float>(ws, W.xap);
+  x.ac = ws_ptr<float>(ws, W.xac);
+  x.po = ws_ptr<float>(ws, W.xpo);
+  x.pd = ws_ptr<float>(ws, W.xpd);
+  x.hx = ws_ptr<float>(ws, W.xhx);
+  x.hx2 = ws_ptr<float>(ws, W.xhx2);
+  x.status = status;
+  return x;
+}
+
+// One decoder layer, batch 1, as the two XCD-split launches.  Input: in_mode 1 = hin,
+// 2 = the embedding row of emb_tokens[0], 0 = the previous layer of the same step
+// (its post-attention state and down partials in the workspace).  With hout set, the
+// layer output is also formed there (otherwise the next layer's launch A forms it).
+int run_layer_xcd(const q4d_model_t* m, int l, int in_mode, const float* hin, const int32_t* emb_tokens,
+                  float* hout, const q4d_kv_cache_t* kv, const int32_t* positions, void* ws, const WsLayout& W,
+                  int32_t* status, hipStream_t st) {
+  const q4d_layer_t& L = m->layers[l];
+  const XcdBufs xb = xcd_bufs(ws, W, status);
+  XcdAttnArgs a;
+  memset(&a, 0, sizeof(a));
+  a.qw = L.q_proj.w; a.qs = L.q_proj.s;
+  a.kw = L.k_proj.w; a.ks = L.k_proj.s;
+  a.vw = L.v_proj.w; a.vs = L.v_proj.s;
+  a.ow = L.o_proj.w; a.os = L.o_proj.s;
+  a.in_gamma = L.input_layernorm;
+  a.q_gamma = L.q_norm;
+  a.k_gamma = L.k_norm;
+  a.eps = m->rms_norm_eps;
+  a.qscale = m->attn_scaling * 1.4426950408889634f;
+  a.rope_cos = m->rope_cos;
+  a.rope_sin = m->rope_sin;
+  kv_planes(kv, l, &a.kcache, &a.vcache);
+  a.positions = positions;
+  a.max_ctx = m->max_ctx;
+  a.in_mode = in_mode;
+  a.hin = hin;
+  a.emb_token = emb_tokens;
+  a.emb_w = m->embed_tokens.w;
+  a.emb_s = m->embed_tokens.s;
+  a.emb_vocab = m->embed_tokens.rows;
+  a.x = xb;
+  int rc = launch_xcd_attn(a, st);
+  if (rc) return rc;
+  XcdMlpArgs b;
+  memset(&b, 0, sizeof(b));
+  b.gw = L.gate_proj.w; b.gs = L.gate_proj.s;
+  b.uw = L.up_proj.w;   b.us = L.up_proj.s;
+  b.dw = L.down_proj.w; b.ds = L.down_proj.s;
+  b.post_gamma = L.post_attention_layernorm;
+  b.eps = m->rms_norm_eps;
+  b.x = xb;
+  if ((rc = launch_xcd_mlp(b, st))) return rc;
+  return hout ? launch_xcd_finalize(xb, hout, st) : Q4D_OK;
+}
+
 int run_lm_head(const q4d_model_t* m, const float* hidden, int32_t* tok, float* score, float* logits,
                 void* ws, const WsLayout& W, hipStream_t st, const Feedback* fb = nullptr) {
   GemvArgs a = one_matrix(&m->embed_tokens, 1);
@@ -252,6 +330,15 @@ int run_token(const q4d_model_t* m, const int32_t* tokens, const int32_t* positi
               hipStream_t st, const Feedback* fb = nullptr) {
   float* hidden = ws_ptr<float>(ws, W.hidden);
   int rc;
+  if (xcd_eligible(m)) {
+    // layer l > 0 takes its input from the previous layer's launches directly; the
+    // last layer's output is formed in `hidden` for the LM head
+    for (int l = 0; l < m->num_layers; ++l)
+      if ((rc = run_layer_xcd(m, l, l == 0 ? 2 : 0, nullptr, tokens, l == m->num_layers - 1 ? hidden : nullptr, kv,
+                              positions, ws, W, status, st)))
+        return rc;
+    return run_lm_head(m, hidden, next_token, score, logits, ws, W, st, fb);
+  }
   for (int l = 0; l < m->num_layers; ++l)
     if ((rc = run_layer(m, l, hidden, hidden, kv, positions, ws, W, st, -1, status, l == 0 ? tokens : nullptr)))
       return rc;
@@ -307,6 +394,13 @@ const char* q4d_status_string(int code) {
     case Q4D_ERR_DTYPE: return "unsupported dtype";
     default: return "unknown status";
   }
+}
+
+int q4d_set_decode_plan(int32_t plan) {
+  if (plan != Q4D_DECODE_XCD && plan != Q4D_DECODE_STAGED) return Q4D_ERR_SHAPE;
+  const int prev = g_decode_plan;
+  g_decode_plan = plan;
+  return prev;
 }
 
 int q4d_set_activation_precision(int32_t mode) {

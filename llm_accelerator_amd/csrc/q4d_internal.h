@@ -16,6 +16,12 @@ constexpr int kAttnChunk = 64;
 constexpr int kAttnChunkLong = 128;
 // Upper bound on the LM-head grid (one partial argmax per block).
 constexpr int kLmMaxBlocks = 2048;
+// XCD-split batch-1 layer (q4d_xcd.hip): one kv head per XCD, 32 workgroups per XCD,
+// attention chunk records of (max, sum, 2 pad, o[128]) floats.
+constexpr int kXcdGroups = 8;
+constexpr int kXcdBlocks = 32;
+constexpr int kXcdApRec = 132;
+constexpr int kXcdInter = 3072;
 
 inline size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
@@ -24,6 +30,7 @@ struct WsLayout {
   size_t status;     // int32[64]: [0] = status bits
   size_t counters;   // int32[batch * kv_heads] attention split counters, then 1 LM counter
   size_t lm_key;     // u64 packed (score, index) running LM-head argmax (zeroed with the counters)
+  size_t xflags;     // u32 [8][32] exchange flags of the XCD-split layer (zeroed with the counters)
   size_t hidden;     // f32 [batch, hidden]          residual stream
   size_t qkv;        // f32 [batch, (qh + 2 kvh) * d] raw q|k|v projections
   size_t qrope;      // f32 [batch, qh * d]          q after norm + RoPE (primitive path)
@@ -36,6 +43,14 @@ struct WsLayout {
   size_t row_idx;    // i32 [batch, vocab/128]
   size_t gemm_part;  // f32 [8][batch][max(q|k|v rows, 2 x intermediate)] split-K partial tiles
   size_t gemm_part_floats;
+  // XCD-split batch-1 layer (q4d_xcd.hip)
+  size_t xqkv;       // f32 [8][512]      each XCD's raw q|k|v rows
+  size_t xap;        // f32 [8][32][2][kXcdApRec] attention chunk partials
+  size_t xac;        // f32 [8][384]      each XCD's SwiGLU activations
+  size_t xpo;        // f32 [8][hidden]   o_proj split-K partials
+  size_t xpd;        // f32 [8][hidden]   down split-K partials
+  size_t xhx;        // f32 [hidden]      layer input (residual base of launch B)
+  size_t xhx2;       // f32 [hidden]      post-attention state (residual base of the next layer)
   size_t total;
   int nsplit_max;
   int lm_counter_index;  // index into counters
@@ -51,6 +66,7 @@ inline WsLayout ws_layout(const q4d_model_t* m, int batch) {
   L.counters = o; o = align_up(o + (size_t)(batch * kvh + 1) * 4, A);
   L.lm_counter_index = batch * kvh;
   L.lm_key = o;   o = align_up(o + 8, A);
+  L.xflags = o;   o = align_up(o + (size_t)kXcdGroups * kXcdBlocks * 4, A);
   L.hidden = o;   o = align_up(o + (size_t)batch * m->hidden_size * 4, A);
   L.qkv = o;      o = align_up(o + (size_t)batch * (qh + 2 * kvh) * d * 4, A);
   L.qrope = o;    o = align_up(o + (size_t)batch * qh * d * 4, A);
@@ -69,6 +85,16 @@ inline WsLayout ws_layout(const q4d_model_t* m, int batch) {
     const size_t w1 = (size_t)(qh + 2 * kvh) * d, w2 = 2 * (size_t)m->intermediate_size;
     L.gemm_part_floats = 8 * (size_t)batch * (w1 > w2 ? w1 : w2);
     L.gemm_part = o; o = align_up(o + L.gemm_part_floats * 4, A);
+  }
+  {
+    const size_t hs = (size_t)m->hidden_size * 4;
+    L.xqkv = o; o = align_up(o + (size_t)kXcdGroups * 4 * d * 4, A);
+    L.xap = o;  o = align_up(o + (size_t)kXcdGroups * kXcdBlocks * 2 * kXcdApRec * 4, A);
+    L.xac = o;  o = align_up(o + (size_t)m->intermediate_size * 4, A);
+    L.xpo = o;  o = align_up(o + kXcdGroups * hs, A);
+    L.xpd = o;  o = align_up(o + kXcdGroups * hs, A);
+    L.xhx = o;  o = align_up(o + hs, A);
+    L.xhx2 = o; o = align_up(o + hs, A);
   }
   L.total = o;
   return L;
@@ -188,6 +214,56 @@ struct AttnArgs {
   int32_t* status;
 };
 int launch_attention(const AttnArgs& a, hipStream_t stream);
+
+// ---- XCD-split batch-1 decoder layer (q4d_xcd.hip) -----------------------------
+struct XcdBufs {
+  uint32_t* flags;  // [8][32]
+  float* qkv;       // [8][512]
+  float* ap;        // [8][32][2][kXcdApRec]
+  float* ac;        // [8][384]
+  float* po;        // [8][1024]
+  float* pd;        // [8][1024]
+  float* hx;        // [1024] layer input
+  float* hx2;       // [1024] post-attention state
+  int32_t* status;
+};
+struct XcdAttnArgs {
+  const uint8_t *qw, *kw, *vw, *ow;
+  const uint16_t *qs, *ks, *vs, *os;
+  const float* in_gamma;
+  const float* q_gamma;
+  const float* k_gamma;
+  float eps;
+  float qscale;            // attention scaling * log2(e)
+  const float* rope_cos;   // [max_ctx][64]
+  const float* rope_sin;
+  uint16_t* kcache;        // the layer's K plane [kv_heads][max_ctx][128] (one sequence)
+  uint16_t* vcache;
+  const int32_t* positions;
+  int max_ctx;
+  // layer input: 0 = hx2 + the 8 down partials of the previous layer, 1 = hin,
+  // 2 = the embedding row of emb_token[0]
+  int in_mode;
+  const float* hin;
+  const int32_t* emb_token;
+  const uint8_t* emb_w;
+  const uint16_t* emb_s;
+  int emb_vocab;
+  XcdBufs x;
+};
+struct XcdMlpArgs {
+  const uint8_t *gw, *uw, *dw;
+  const uint16_t *gs, *us, *ds;
+  const float* post_gamma;
+  float eps;
+  XcdBufs x;
+};
+// 16-position groups per thread of launch A for a KV capacity (0: unsupported, > 4096).
+int xcd_npt(int max_ctx);
+int launch_xcd_attn(const XcdAttnArgs& a, hipStream_t st);
+int launch_xcd_mlp(const XcdMlpArgs& a, hipStream_t st);
+// out = hx2 + sum of the 8 down partials.
+int launch_xcd_finalize(const XcdBufs& x, float* out, hipStream_t st);
 
 // ---- Q4 GEMM on MFMA (prefill / batched decode) ------------------------------
 // Prefill's per-head work on the q|k|v projections (q/k RMSNorm, RoPE, K/V append)

@@ -208,16 +208,16 @@ def test_activation_precision_setter(lib):
 def test_noalloc_step_rejects_models_beyond_its_scratch(lib):
     """q4d_run_one_token_noalloc validates on the host before it touches the device:
     a model whose batch-1 workspace exceeds the 4 MiB scratch (Qwen3-0.6B shapes past
-    30208 positions) is refused with Q4D_ERR_CAPACITY; missing pointers with NULL."""
+    27328 positions) is refused with Q4D_ERR_CAPACITY; missing pointers with NULL."""
     arr = _layers()
-    big = _model(arr, max_ctx=30209)
+    big = _model(arr, max_ctx=27329)
     assert lib.q4d_workspace_bytes(ctypes.byref(big), 1) > 4 << 20
-    kv = Q4dKVCache(FAKE, 1, 1, 8, 30209, 128)
+    kv = Q4dKVCache(FAKE, 1, 1, 8, 27329, 128)
     assert lib.q4d_run_one_token_noalloc(ctypes.byref(big), FAKE, FAKE, ctypes.byref(kv), FAKE, FAKE, None, FAKE,
                                          None) == -9
-    ok = _model(arr, max_ctx=30208)
+    ok = _model(arr, max_ctx=27328)
     assert lib.q4d_workspace_bytes(ctypes.byref(ok), 1) <= 4 << 20
-    kv2 = Q4dKVCache(FAKE, 1, 1, 8, 30208, 128)
+    kv2 = Q4dKVCache(FAKE, 1, 1, 8, 27328, 128)
     assert lib.q4d_run_one_token_noalloc(ctypes.byref(ok), FAKE, FAKE, ctypes.byref(kv2), FAKE, FAKE, None, None,
                                          None) == -7
 

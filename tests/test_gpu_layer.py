@@ -70,10 +70,18 @@ def _oracle_layer(om, kv_k, kv_v, hidden, kv_store):
                                          kv_store_dtype=kv_store)
 
 
-@pytest.mark.parametrize("precision,tol", [(2, 1e-4), (1, 3e-3)])
-def test_decoder_layer_config2(dev, layer_setup, precision, tol):
+@pytest.mark.parametrize("precision,tol,plan", [(2, 1e-4, 0), (2, 1e-4, 1), (1, 3e-3, 1)],
+                         ids=["xcd", "staged", "staged-fp16"])
+def test_decoder_layer_config2(dev, layer_setup, precision, tol, plan):
+    """One decoder layer at context 512 (config 2) for both kernel plans (the XCD-split
+    layer needs activation precision 2; precision 1 runs staged)."""
     cfg, model, om64, om32, kv_k, kv_v, hidden = layer_setup
-    out, knew, vnew = _run_gpu_layer(cfg, model, kv_k, kv_v, hidden, precision, dev)
+    lib = _lib.load()
+    prev = lib.q4d_set_decode_plan(plan)
+    try:
+        out, knew, vnew = _run_gpu_layer(cfg, model, kv_k, kv_v, hidden, precision, dev)
+    finally:
+        lib.q4d_set_decode_plan(prev)
     ref, kc, vc = _oracle_layer(om64, kv_k, kv_v, hidden, np.float16)
     mx, rel = report(f"layer mode{precision} vs fp16-KV oracle", out, ref)
     assert rel <= tol
@@ -216,14 +224,20 @@ def test_attention_context_lengths_and_batch(dev, lengths):
         assert mx <= 2e-6 * max(1.0, float(np.abs(ref).max())) + 1e-6, (n, mx)
 
 
+@pytest.mark.parametrize("plan,max_ctx", [(0, 4096), (0, 2048), (1, 4097)], ids=["xcd-4096", "xcd-2048", "staged-4097"])
 @pytest.mark.parametrize("position", [1024, 1151, 2047, 4095])
-def test_decoder_layer_long_context(dev, layer_setup, position):
-    """Batch-1 decode layer past 1024 cached positions, where the o_proj prologue
-    merges more than eight 128-position attention chunks (its loop over further
-    batches of eight), against the fp16-KV oracle at the layer-test bar."""
+def test_decoder_layer_long_context(dev, layer_setup, position, plan, max_ctx):
+    """Batch-1 decode layer past 1024 cached positions against the fp16-KV oracle at
+    the layer-test bar, for both kernel plans: the XCD-split layer at a capacity of
+    4096 / 2048 positions (each of the 32 attention workgroups of an XCD takes 8 / 4
+    groups of 16 positions), and the five staged launches past 4096 positions (the
+    o_proj prologue merges more than eight 128-position chunks, its loop over further
+    batches of eight)."""
     from llm_accelerator_amd.model import with_context
     cfg, model, om64, _, _, _, hidden = layer_setup
-    m = with_context(model, 4097)
+    if position >= max_ctx:
+        pytest.skip("position beyond the capacity")
+    m = with_context(model, max_ctx)
     rng = np.random.default_rng(position)
     kv_k = rng.normal(size=(1, 8, position, 128)).astype(np.float16)
     kv_v = rng.normal(size=(1, 8, position, 128)).astype(np.float16)
@@ -237,9 +251,13 @@ def test_decoder_layer_long_context(dev, layer_setup, position):
     h = torch.from_numpy(hidden.reshape(1, 1024)).to(dev)
     out = torch.empty_like(h)
     pos = torch.tensor([position], dtype=torch.int32, device=dev)
-    print(f"[layer long ctx] position={position}", flush=True)
-    check(lib.q4d_decoder_layer(ctypes.byref(desc), 0, h.data_ptr(), out.data_ptr(), ctypes.byref(kvd),
-                                pos.data_ptr(), ws.data_ptr(), ws.numel(), current_stream()), "q4d_decoder_layer")
+    print(f"[layer long ctx] plan={plan} max_ctx={max_ctx} position={position}", flush=True)
+    prev = lib.q4d_set_decode_plan(plan)
+    try:
+        check(lib.q4d_decoder_layer(ctypes.byref(desc), 0, h.data_ptr(), out.data_ptr(), ctypes.byref(kvd),
+                                    pos.data_ptr(), ws.data_ptr(), ws.numel(), current_stream()), "q4d_decoder_layer")
+    finally:
+        lib.q4d_set_decode_plan(prev)
     st = ctypes.c_int32(0)
     check(lib.q4d_read_status(ws.data_ptr(), ws.numel(), ctypes.byref(desc), 1, ctypes.byref(st), current_stream()),
           "q4d_read_status")
