@@ -24,7 +24,9 @@ steps, and its HBM roofline fraction (Q4 weights + the tied table + fp16 K/V
 of every attended position, averaged over the steps, over 8 TB/s).  The
 model's 306 MB of weights exceed the 256 MB cache; ``resident`` repeats the
 loop with every layer aliased to layer 0's weights (91 MB working set) for the
-cache-resident figure.
+cache-resident figure.  The layer runs as two launches split over the eight XCDs
+(one kv head per XCD); ``staged`` repeats the loop with the five-launch layer, and
+``launch_floor`` times the step's launches with their grids and no work.
 
 ``lm_head``: final RMSNorm + 151936 x 1024 Q4 GEMV + argmax alone, flushed
 (rotating over 4 copies of the table, 331 MB) and repeated.
@@ -235,6 +237,8 @@ def leg_layer(args, lib, torch, dev, st):
     stage_bytes = M.stage_bytes_layer(M.Qwen3Config(), ctx)
     out = {"workload": f"one Qwen3-0.6B decoder layer, one decode step at ctx {ctx}, weights rotated over "
                        f"{copies} distinct layers (flushed) or one layer repeated (resident)",
+           "plan": "q4d_decoder_layer: the XCD-split layer (launch A, launch B, output sum); "
+                   "stage_us_flushed: the five staged launches of q4d_layer_stage",
            "bytes_per_step": step_bytes, "flushed_us": round(fl_us, 3),
            "flushed_GBps": round(step_bytes / fl_us / 1e3, 1), "resident_us": round(res_us, 3),
            "resident_GBps": round(step_bytes / res_us / 1e3, 1),
@@ -288,19 +292,24 @@ def run_decode(fmodel, prompt, gen_steps, per_graph, torch, desc=None):
     return out
 
 
-def decode_launch_floor(torch, fmodel, tokens=15, replays=20):
-    """A decode step's 141 launches with their grids, each kernel reduced to one dependent
+def decode_launch_floor(torch, fmodel, tokens=15, replays=20, staged=False):
+    """A decode step's launches with their grids, each kernel reduced to one dependent
     read of the previous launch's 4 KB output (q4d_diag_launch_chain), graph-replayed:
-    what the launches of a token cost without their work.  Grids (blocks x threads) of the
-    step's kernels, as the kernel trace of this leg shows them: q|k|v 512 x 256, attention
+    what the launches of a token cost without their work.  Grids (blocks x threads) of
+    the step's kernels, as the kernel trace of this leg shows them.  XCD-split plan:
+    per layer launch A and launch B, 256 x 320 each, then the last layer's output sum
+    1 x 256 and the LM head 238 x 1024.  Staged plan: q|k|v 512 x 256, attention
     ceil(max_ctx / 64) x kv_heads blocks of 256, o_proj 128 x 512, gate/up 384 x 256,
     down 256 x 384, LM head 238 x 1024."""
     from llm_accelerator_amd import _lib
     lib = _lib.load()
     cfg = fmodel.config
-    layer = [(512, 1, 256), ((fmodel.max_ctx + 63) // 64, cfg.num_key_value_heads, 256), (128, 1, 512),
-             (384, 1, 256), (256, 1, 384)]
-    shapes = layer * cfg.num_hidden_layers + [(238, 1, 1024)]
+    if staged:
+        layer = [(512, 1, 256), ((fmodel.max_ctx + 63) // 64, cfg.num_key_value_heads, 256), (128, 1, 512),
+                 (384, 1, 256), (256, 1, 384)]
+        shapes = layer * cfg.num_hidden_layers + [(238, 1, 1024)]
+    else:
+        shapes = [(256, 1, 320), (256, 1, 320)] * cfg.num_hidden_layers + [(1, 1, 256), (238, 1, 1024)]
     n = len(shapes)
     gx = (ctypes.c_int32 * n)(*[x for x, _, _ in shapes])
     gy = (ctypes.c_int32 * n)(*[y for _, y, _ in shapes])
@@ -326,9 +335,18 @@ def leg_decode(args, torch, np, fmodel):
     prompt = np.random.default_rng(1).integers(0, fcfg.vocab_size, PROMPT).tolist()
     steps = args.decode_gen - 1                     # token 0 comes from the last prompt step
     per_graph = max(d for d in range(1, 17) if steps % d == 0)
+    from llm_accelerator_amd import _lib
+    lib = _lib.load()
     flushed = run_decode(fmodel, prompt, steps, per_graph, torch)
     resident = run_decode(fmodel, prompt, steps, per_graph, torch, desc=aliased_descriptor(fmodel))
     floor = decode_launch_floor(torch, fmodel, tokens=per_graph)
+    # the staged five-launch layer (q4d_set_decode_plan), for comparison
+    prev = lib.q4d_set_decode_plan(1)
+    try:
+        staged = run_decode(fmodel, prompt, steps, per_graph, torch)
+    finally:
+        lib.q4d_set_decode_plan(prev)
+    staged_floor = decode_launch_floor(torch, fmodel, tokens=per_graph, staged=True)
     # step p feeds position p and attends p + 1 positions
     tok_bytes = sum(M.batched_step_bytes(fcfg, 1, p + 1) for p in range(PROMPT, PROMPT + steps)) / steps
     wb = fmodel.weight_bytes()
@@ -341,10 +359,17 @@ def leg_decode(args, torch, np, fmodel):
            "bytes_per_token": int(tok_bytes), "GBps": round(tok_bytes * tok_s / 1e9, 1),
            "roofline_frac": round(tok_bytes * tok_s / 1e9 / HBM_PEAK_GBPS, 4),
            "generated": flushed["generated"], "status": flushed["status"],
-           "launches_per_token": 5 * fcfg.num_hidden_layers + 1,
-           "launch_floor": dict(floor, note="the same 141 launches with their grids, each kernel only one "
-                                            "dependent 4 KB read and write (q4d_diag_launch_chain)",
+           "plan": "XCD-split layer: 2 launches per layer (one kv head per XCD), last-layer sum, LM head",
+           "launches_per_token": floor["launches_per_token"],
+           "launch_floor": dict(floor, note=f"the same {floor['launches_per_token']} launches with their grids, "
+                                            "each kernel only one dependent 4 KB read and write "
+                                            "(q4d_diag_launch_chain)",
                                 share=round(floor["us_per_token"] / flushed["us_per_token"], 3)),
+           "staged": {"note": "the five-launch layer of q4d_layer_stage (q4d_set_decode_plan(1))",
+                      "tok_s": round(1e6 / staged["us_per_token"], 1),
+                      "us_per_token": round(staged["us_per_token"], 2), "status": staged["status"],
+                      "launches_per_token": staged_floor["launches_per_token"],
+                      "launch_floor_us_per_token": staged_floor["us_per_token"]},
            "resident": {"note": "every layer aliased to layer 0's weights: 91 MB per token, inside the 256 MB cache",
                         "tok_s": round(1e6 / resident["us_per_token"], 1),
                         "us_per_token": round(resident["us_per_token"], 2),
