@@ -297,8 +297,8 @@ def decode_launch_floor(torch, fmodel, tokens=15, replays=20, staged=False):
     read of the previous launch's 4 KB output (q4d_diag_launch_chain), graph-replayed:
     what the launches of a token cost without their work.  Grids (blocks x threads) of
     the step's kernels, as the kernel trace of this leg shows them.  XCD-split plan:
-    per layer launch A and launch B, 256 x 320 each, then the last layer's output sum
-    1 x 256 and the LM head 238 x 1024.  Staged plan: q|k|v 512 x 256, attention
+    per layer launch A and launch B, 256 x 320 each, then the LM head 238 x 1024 (which
+    forms the last layer's output in its prologue).  Staged plan: q|k|v 512 x 256, attention
     ceil(max_ctx / 64) x kv_heads blocks of 256, o_proj 128 x 512, gate/up 384 x 256,
     down 256 x 384, LM head 238 x 1024."""
     from llm_accelerator_amd import _lib
@@ -309,7 +309,7 @@ def decode_launch_floor(torch, fmodel, tokens=15, replays=20, staged=False):
                  (384, 1, 256), (256, 1, 384)]
         shapes = layer * cfg.num_hidden_layers + [(238, 1, 1024)]
     else:
-        shapes = [(256, 1, 320), (256, 1, 320)] * cfg.num_hidden_layers + [(1, 1, 256), (238, 1, 1024)]
+        shapes = [(256, 1, 320), (256, 1, 320)] * cfg.num_hidden_layers + [(238, 1, 1024)]
     n = len(shapes)
     gx = (ctypes.c_int32 * n)(*[x for x, _, _ in shapes])
     gy = (ctypes.c_int32 * n)(*[y for _, y, _ in shapes])
@@ -359,7 +359,7 @@ def leg_decode(args, torch, np, fmodel):
            "bytes_per_token": int(tok_bytes), "GBps": round(tok_bytes * tok_s / 1e9, 1),
            "roofline_frac": round(tok_bytes * tok_s / 1e9 / HBM_PEAK_GBPS, 4),
            "generated": flushed["generated"], "status": flushed["status"],
-           "plan": "XCD-split layer: 2 launches per layer (one kv head per XCD), last-layer sum, LM head",
+           "plan": "XCD-split layer: 2 launches per layer (one kv head per XCD), LM head (forms the last layer's output)",
            "launches_per_token": floor["launches_per_token"],
            "launch_floor": dict(floor, note=f"the same {floor['launches_per_token']} launches with their grids, "
                                             "each kernel only one dependent 4 KB read and write "

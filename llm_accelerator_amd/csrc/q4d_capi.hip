@@ -299,10 +299,15 @@ int run_layer_xcd(const q4d_model_t* m, int l, int in_mode, const float* hin, co
   return hout ? launch_xcd_finalize(xb, hout, st) : Q4D_OK;
 }
 
+// With parts set, the LM head's input is hidden + parts[0] + ... + parts[7] (the
+// XCD-split layer's output), which it also stores to hidden_out when that is set.
 int run_lm_head(const q4d_model_t* m, const float* hidden, int32_t* tok, float* score, float* logits,
-                void* ws, const WsLayout& W, hipStream_t st, const Feedback* fb = nullptr) {
+                void* ws, const WsLayout& W, hipStream_t st, const Feedback* fb = nullptr,
+                const float* parts = nullptr, float* hidden_out = nullptr) {
   GemvArgs a = one_matrix(&m->embed_tokens, 1);
   a.x = hidden;
+  a.x_parts = parts;
+  a.x_out = hidden_out;
   a.gamma = m->final_norm;
   a.eps = m->rms_norm_eps;
   a.logits = logits;
@@ -331,13 +336,13 @@ int run_token(const q4d_model_t* m, const int32_t* tokens, const int32_t* positi
   float* hidden = ws_ptr<float>(ws, W.hidden);
   int rc;
   if (xcd_eligible(m)) {
-    // layer l > 0 takes its input from the previous layer's launches directly; the
-    // last layer's output is formed in `hidden` for the LM head
+    // layer l > 0 takes its input from the previous layer's launches directly; the LM
+    // head's prologue forms the last layer's output (stored in `hidden` as well)
     for (int l = 0; l < m->num_layers; ++l)
-      if ((rc = run_layer_xcd(m, l, l == 0 ? 2 : 0, nullptr, tokens, l == m->num_layers - 1 ? hidden : nullptr, kv,
-                              positions, ws, W, status, st)))
+      if ((rc = run_layer_xcd(m, l, l == 0 ? 2 : 0, nullptr, tokens, nullptr, kv, positions, ws, W, status, st)))
         return rc;
-    return run_lm_head(m, hidden, next_token, score, logits, ws, W, st, fb);
+    const XcdBufs xb = xcd_bufs(ws, W, status);
+    return run_lm_head(m, xb.hx2, next_token, score, logits, ws, W, st, fb, xb.pd, hidden);
   }
   for (int l = 0; l < m->num_layers; ++l)
     if ((rc = run_layer(m, l, hidden, hidden, kv, positions, ws, W, st, -1, status, l == 0 ? tokens : nullptr)))

@@ -392,7 +392,7 @@ __device__ __forceinline__ float chunk_scaled(const u32x4 w, const XChunk& h, co
   return code * fmaf(fmaf(a, 16.f, b), 64.f, -s8);
 }
 
-template <int XP, int U, int NWB>
+template <int XP, int U, int NWB, bool PARTS>
 __global__ __launch_bounds__(NWB * 64) void lm_kernel(const GemvArgs a) {
   constexpr int K = 1024;
   const int lane = threadIdx.x & 63;
@@ -406,6 +406,14 @@ __global__ __launch_bounds__(NWB * 64) void lm_kernel(const GemvArgs a) {
 
   ActRegs<K, NWB, X_RMS, XP> ar;
   act_load(a, 0, ar);
+  static_assert(ActRegs<K, NWB, X_RMS, XP>::XPT == 1, "one activation vector per thread");
+  f32x4 pp[PARTS ? kXcdGroups : 1];
+  if constexpr (PARTS) {
+    if (threadIdx.x < K / 4) {
+#pragma unroll
+      for (int g = 0; g < kXcdGroups; ++g) pp[g] = reinterpret_cast<const f32x4*>(a.x_parts + g * K)[threadIdx.x];
+    }
+  }
 
   const Rsrc rw = make_rsrc(a.w[0], (uint32_t)R * (K / 2));
   const Rsrc rsc = make_rsrc(a.s[0], (uint32_t)R * (K / 32));
@@ -431,6 +439,15 @@ __global__ __launch_bounds__(NWB * 64) void lm_kernel(const GemvArgs a) {
   Tile4 A[U], B[U];
 #pragma unroll
   for (int u = 0; u < U; ++u) A[u] = load4(base + u * step);
+  if constexpr (PARTS) {
+    if (threadIdx.x < K / 4) {
+      f32x4 v = ar.x[0];
+#pragma unroll
+      for (int g = 0; g < kXcdGroups; ++g) v = v + pp[g];
+      ar.x[0] = v;
+      if (blockIdx.x == 0 && a.x_out) reinterpret_cast<f32x4*>(a.x_out)[threadIdx.x] = v;
+    }
+  }
   // stage 1 goes out after the activation prologue: issued with stage 0 the
   // grid's 15 MB of weight requests queue the activation loads behind them
   // (measured ~1 µs later prologue).  It is unconditional (clamped): a
@@ -561,13 +578,16 @@ int launch_lm(const GemvArgs& a, hipStream_t stream) {
   const int NT4 = (a.rows + 3) / 4;
   // stages per wave over the resident grid (at least 2), then the smallest
   // grid covering the matrix in that many stages (few clamped tail tiles)
-  const int res = resident_blocks(lm_kernel<XP, U, NWB>, NWB * 64);
+  const int res = resident_blocks(lm_kernel<XP, U, NWB, false>, NWB * 64);
   const long per_stage = (long)res * NWB * U;
   int S = (int)((NT4 + per_stage - 1) / per_stage);
   if (S < 2) S = 2;
   int blocks = (int)((NT4 + (long)NWB * U * S - 1) / ((long)NWB * U * S));
   if (blocks < 1) blocks = 1;
-  hipLaunchKernelGGL((lm_kernel<XP, U, NWB>), dim3(blocks), dim3(NWB * 64), 0, stream, a);
+  if (a.x_parts)
+    hipLaunchKernelGGL((lm_kernel<XP, U, NWB, true>), dim3(blocks), dim3(NWB * 64), 0, stream, a);
+  else
+    hipLaunchKernelGGL((lm_kernel<XP, U, NWB, false>), dim3(blocks), dim3(NWB * 64), 0, stream, a);
   return check_launch();
 }
 
@@ -674,6 +694,8 @@ int launch_gemv_xp(const GemvArgs& a, int xm, int xp, int ep, bool pair, hipStre
   if (ep == EP_ARGMAX && (!a.lm_key || !a.counter || !a.out_token || !a.out_score || a.batch != 1))
     return Q4D_ERR_NULL;
   if (ep == EP_ARGMAX && (!aligned(a.lm_key, 8) || a.nseg != 1)) return Q4D_ERR_BAD_ADDR;
+  if ((a.x_parts || a.x_out) && (ep != EP_ARGMAX || xm != X_RMS || a.cols != 1024 || !a.x_parts)) return Q4D_ERR_SHAPE;
+  if ((a.x_parts && !aligned(a.x_parts, 16)) || (a.x_out && !aligned(a.x_out, 16))) return Q4D_ERR_BAD_ADDR;
   if (xm == X_F16 && xp != 1) return Q4D_ERR_DTYPE;
   // unused segments: empty ranges on segment 0's memory, never selected
   GemvArgs b = a;

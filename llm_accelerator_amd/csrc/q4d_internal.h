@@ -134,6 +134,11 @@ struct GemvArgs {
   int cols;         // K
   // Activations.
   const void* x;        // X_F16: fp16 [batch, K]; X_F32 / X_RMS: fp32 [batch, K]
+  // X_RMS in the streaming LM head only: x is x + x_parts[0] + ... + x_parts[7]
+  // (fp32 [8][K], summed in this order, as the XCD-split layer forms its output);
+  // block 0 stores that sum to x_out when x_out is set.
+  const float* x_parts;
+  float* x_out;
   const float* gamma;   // X_RMS
   float eps;            // X_RMS
   // Epilogue.

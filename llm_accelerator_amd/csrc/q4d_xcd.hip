@@ -111,6 +111,8 @@ __device__ __forceinline__ f32x4 sum_partials(const float* base, const float* pa
   return v;
 }
 
+__device__ __forceinline__ void prep_vals(float (&v)[4], int q, uint32_t* ph, uint32_t* pl, float2* sm);
+
 // fp16 hi/lo pairs in dequant order (see act_prepare in q4d_gemv_dev.h) for work
 // item q (< K / 4) of a K-vector in LDS: chunk c = q / 8 holds columns 32c..32c+31,
 // and the 8 items of a chunk are 8 consecutive lanes, which sum the chunk.
@@ -126,6 +128,13 @@ __device__ __forceinline__ void prep_item(const float* sx, int q, bool norm, flo
     v[2] = (v[2] * inv) * g4[2];
     v[3] = (v[3] * inv) * g4[3];
   }
+  prep_vals(v, q, ph, pl, sm);
+}
+
+// The conversion of prep_item for the values v = {x[ea], x[eb], x[ea + 1], x[eb + 1]}
+// of work item q.
+__device__ __forceinline__ void prep_vals(float (&v)[4], int q, uint32_t* ph, uint32_t* pl, float2* sm) {
+  const int c = q >> 3, m = (q & 7) >> 1, i0 = (q & 1) * 2;
   _Float16 h[4], l[4];
 #pragma unroll
   for (int k = 0; k < 4; ++k) {
@@ -218,20 +227,6 @@ __device__ __forceinline__ void attn_split(int T, int& nA, int& chunk) {
   chunk = (T + nA - 1) / nA;
 }
 
-// Sum over lanes l, l ^ 16, l ^ 32, l ^ 48 (v_permlane32_swap / v_permlane16_swap
-// with both operands the same register give the two halves / row pairs).
-__device__ __forceinline__ float rows_sum(float v) {
-  const uint32_t a = __builtin_bit_cast(uint32_t, v);
-  const auto r = __builtin_amdgcn_permlane32_swap(a, a, false, false);
-  const uint32_t r0 = r[0], r1 = r[1];
-  const float u = __builtin_bit_cast(float, r0) + __builtin_bit_cast(float, r1);
-  const uint32_t b = __builtin_bit_cast(uint32_t, u);
-  const auto q = __builtin_amdgcn_permlane16_swap(b, b, false, false);
-  const uint32_t q0 = q[0], q1 = q[1];
-  return __builtin_bit_cast(float, q0) + __builtin_bit_cast(float, q1);
-}
-constexpr int kDppRowRor4 = 0x124, kDppRowRor8 = 0x128;
-
 // Max / sum over each 32-lane half, in every lane of the half.
 __device__ __forceinline__ float half_max(float v) {
   v = row16_max_f(v);
@@ -323,7 +318,6 @@ __global__ __launch_bounds__(kXThreads) void xcd_attn_kernel(const XcdAttnArgs a
   __shared__ alignas(16) float sqkv[4 * D];
   __shared__ alignas(16) float sq[2][D];
   __shared__ alignas(16) uint16_t snew[2][D];
-  __shared__ alignas(16) float sattn[2 * D];
   __shared__ float swt[2][kXcdBlocks];
   __shared__ alignas(16) float spart[4][2 * D];
   __shared__ alignas(16) uint32_t ph2[2 * D / 2];
@@ -339,10 +333,12 @@ __global__ __launch_bounds__(kXThreads) void xcd_attn_kernel(const XcdAttnArgs a
   WChunk wq[2], wo;
   f32x4 g4 = {0.f, 0.f, 0.f, 0.f};
   float nx0 = 0.f, nx1 = 0.f, rc = 0.f, rs = 0.f;
-  // attention waves (0, 1: q head 2g + wid): lane = 4 p + quarter; position p of a
-  // 16-position group, dims 32 quarter .. +31 of K and V
+  // attention waves (0, 1: q head 2g + wid): for K, lane = 4 p + quarter (position p of
+  // a 16-position group, dims 32 quarter .. +31); for V, lane holds dims 2 lane, 2 lane + 1
+  // of each of the group's 16 positions, so P.V needs no sum across lanes
   const int ap = lane >> 2, aq = lane & 3;
-  u32x4 kr[4], vr[4];
+  u32x4 kr[4];
+  uint32_t vv[16];
   const uint16_t* kb = a.kcache + (size_t)g * a.max_ctx * D;
   const uint16_t* vb = a.vcache + (size_t)g * a.max_ctx * D;
   const int plast = pos > 0 ? pos - 1 : 0;
@@ -392,9 +388,11 @@ __global__ __launch_bounds__(kXThreads) void xcd_attn_kernel(const XcdAttnArgs a
       int p = cstart + ap;
       p = p < pos ? p : plast;
 #pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        kr[k] = *reinterpret_cast<const u32x4*>(kb + (size_t)p * D + 32 * aq + 8 * k);
-        vr[k] = *reinterpret_cast<const u32x4*>(vb + (size_t)p * D + 32 * aq + 8 * k);
+      for (int k = 0; k < 4; ++k) kr[k] = *reinterpret_cast<const u32x4*>(kb + (size_t)p * D + 32 * aq + 8 * k);
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int pv = cstart + i < pos ? cstart + i : plast;
+        vv[i] = *reinterpret_cast<const uint32_t*>(vb + (size_t)pv * D + 2 * lane);
       }
     }
   }
@@ -483,7 +481,7 @@ __global__ __launch_bounds__(kXThreads) void xcd_attn_kernel(const XcdAttnArgs a
 
   // ---- attention of q head 2g + wid over this workgroup's chunk, one wave per head:
   // scores over the 4 quarter lanes of a position, an online softmax over the
-  // 16-position groups, P.V per lane, summed over positions at the end ----
+  // 16-position groups, P.V with each lane owning two dims of the head ----
   if (wid < 2 && attn_active) {
     float q[32];
 #pragma unroll
@@ -491,28 +489,26 @@ __global__ __launch_bounds__(kXThreads) void xcd_attn_kernel(const XcdAttnArgs a
       const f32x4 v = *reinterpret_cast<const f32x4*>(&sq[wid][32 * aq + 4 * k]);
       q[4 * k] = v[0]; q[4 * k + 1] = v[1]; q[4 * k + 2] = v[2]; q[4 * k + 3] = v[3];
     }
-    float M = -INFINITY, L = 0.f;
-    float o[32];
-#pragma unroll
-    for (int k = 0; k < 32; ++k) o[k] = 0.f;
+    float M = -INFINITY, L = 0.f, o0 = 0.f, o1 = 0.f;
     for (int i = 0; i < NPT; ++i) {
       const int pl_ = 16 * i + ap;  // position within the chunk
+      const int gb = cstart + 16 * i;  // first position of the group
       if (i > 0) {
         int p = cstart + pl_;
         p = p < pos ? p : plast;
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-          kr[k] = *reinterpret_cast<const u32x4*>(kb + (size_t)p * D + 32 * aq + 8 * k);
-          vr[k] = *reinterpret_cast<const u32x4*>(vb + (size_t)p * D + 32 * aq + 8 * k);
+        for (int k = 0; k < 4; ++k) kr[k] = *reinterpret_cast<const u32x4*>(kb + (size_t)p * D + 32 * aq + 8 * k);
+#pragma unroll
+        for (int ii = 0; ii < 16; ++ii) {
+          const int pv = gb + ii < pos ? gb + ii : plast;
+          vv[ii] = *reinterpret_cast<const uint32_t*>(vb + (size_t)pv * D + 2 * lane);
         }
       }
       if (cstart + pl_ == pos) {
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-          kr[k] = *reinterpret_cast<const u32x4*>(&snew[0][32 * aq + 8 * k]);
-          vr[k] = *reinterpret_cast<const u32x4*>(&snew[1][32 * aq + 8 * k]);
-        }
+        for (int k = 0; k < 4; ++k) kr[k] = *reinterpret_cast<const u32x4*>(&snew[0][32 * aq + 8 * k]);
       }
+      if (gb <= pos && pos < gb + 16) vv[pos - gb] = *reinterpret_cast<const uint32_t*>(&snew[1][2 * lane]);
       float sc = 0.f;
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
@@ -528,32 +524,21 @@ __global__ __launch_bounds__(kXThreads) void xcd_attn_kernel(const XcdAttnArgs a
       const float mg = wave_max_bcast(sc);
       const float Mn = fmaxf(M, mg);
       const float so = M == -INFINITY ? 0.f : exp2f(M - Mn);
-      const float e = valid ? exp2f(sc - Mn) : 0.f;
+      const float e = valid ? exp2f(sc - Mn) : 0.f;  // the same in the 4 lanes of a position
       L = L * so + wave_sum_bcast(aq == 0 ? e : 0.f);
+      o0 *= so;
+      o1 *= so;
 #pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        float vf[8];
-        unpack8h(vr[k], vf);
-#pragma unroll
-        for (int ee = 0; ee < 8; ++ee) o[8 * k + ee] = fmaf(e, vf[ee], o[8 * k + ee] * so);
+      for (int ii = 0; ii < 16; ++ii) {
+        const float ei = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, e), 4 * ii));
+        const h2 v = __builtin_bit_cast(h2, vv[ii]);
+        o0 = fmaf(ei, (float)v.x, o0);
+        o1 = fmaf(ei, (float)v.y, o1);
       }
       M = Mn;
     }
-    // sum over the 16 positions of the wave: the 4 lanes of a row with this quarter,
-    // then the 4 rows
     float* rec = X.ap + (size_t)((g * kXcdBlocks + j) * 2 + wid) * kXcdApRec;
-#pragma unroll
-    for (int k = 0; k < 32; ++k) {
-      float v = o[k];
-      v += dpp_f<kDppRowRor4>(v);
-      v += dpp_f<kDppRowRor8>(v);
-      o[k] = rows_sum(v);
-    }
-    if (lane < 4) {
-#pragma unroll
-      for (int k = 0; k < 8; ++k)
-        *reinterpret_cast<f32x4*>(rec + 4 + 32 * lane + 4 * k) = f32x4{o[4 * k], o[4 * k + 1], o[4 * k + 2], o[4 * k + 3]};
-    }
+    *reinterpret_cast<float2*>(rec + 4 + 2 * lane) = make_float2(o0, o1);
     if (lane == 0) *reinterpret_cast<f32x4*>(rec) = f32x4{M, L, 0.f, 0.f};
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // acknowledged before the exchange wave's flag
   }
@@ -600,15 +585,17 @@ __global__ __launch_bounds__(kXThreads) void xcd_attn_kernel(const XcdAttnArgs a
       *reinterpret_cast<f32x4*>(&spart[rg][4 * v]) = acc;
     }
     block_sync_lds();
-    if (t < 64) {
-      f32x4 o = *reinterpret_cast<const f32x4*>(&spart[0][4 * t]);
+    // the merged 256-dim output is the sum of the 4 rows of spart, in row order
+    if (wid == 0) {
+      float v[4];
+      const int c = lane >> 3, m = (lane & 7) >> 1, i0 = (lane & 1) * 2;
+      const int ea = c * 32 + m * 8 + i0, eb = ea + 4;
+      const int ix[4] = {ea, eb, ea + 1, eb + 1};
 #pragma unroll
-      for (int r = 1; r < 4; ++r) o += *reinterpret_cast<const f32x4*>(&spart[r][4 * t]);
-      *reinterpret_cast<f32x4*>(&sattn[4 * t]) = o;
+      for (int k = 0; k < 4; ++k) v[k] = ((spart[0][ix[k]] + spart[1][ix[k]]) + spart[2][ix[k]]) + spart[3][ix[k]];
+      prep_vals(v, lane, ph2, pl2, sm2);
     }
   }
-  block_sync_lds();
-  if (wid == 0) prep_item(sattn, lane, false, 1.f, g4, ph2, pl2, sm2);
   block_sync_lds();
 
   // ---- o_proj split-K partial: rows 32j + t/8, the XCD's 256 columns ----
