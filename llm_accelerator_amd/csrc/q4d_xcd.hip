@@ -287,16 +287,44 @@ __device__ __forceinline__ f32x4 xin_value(int mode, const XIn& r, bool ok) {
   return v;
 }
 
+// The argument blocks' fields, loaded as one batch of scalar loads at kernel entry
+// (left to itself the compiler loads fields where the control flow first needs them:
+// the argument pointer of the position, the position, then the rest, three dependent
+// scalar round trips before the first load of the layer input).
+__device__ __forceinline__ void xcd_bufs_preload(const XcdBufs& x) {
+  asm volatile("" ::"s"(x.flags), "s"(x.qkv), "s"(x.ap), "s"(x.ac), "s"(x.po), "s"(x.pd), "s"(x.hx), "s"(x.hx2),
+               "s"(x.status));
+}
+__device__ __forceinline__ void xcd_attn_preload(const XcdAttnArgs& a) {
+  asm volatile("" ::"s"(a.qw), "s"(a.kw), "s"(a.vw), "s"(a.ow), "s"(a.qs), "s"(a.ks), "s"(a.vs), "s"(a.os),
+               "s"(a.in_gamma), "s"(a.q_gamma), "s"(a.k_gamma), "s"(a.eps), "s"(a.qscale), "s"(a.rope_cos),
+               "s"(a.rope_sin), "s"(a.kcache), "s"(a.vcache), "s"(a.positions), "s"(a.max_ctx), "s"(a.in_mode),
+               "s"(a.hin), "s"(a.emb_token), "s"(a.emb_w), "s"(a.emb_s), "s"(a.emb_vocab));
+  xcd_bufs_preload(a.x);
+}
+__device__ __forceinline__ void xcd_mlp_preload(const XcdMlpArgs& a) {
+  asm volatile("" ::"s"(a.gw), "s"(a.uw), "s"(a.dw), "s"(a.gs), "s"(a.us), "s"(a.ds), "s"(a.post_gamma),
+               "s"(a.eps));
+  xcd_bufs_preload(a.x);
+}
+
 // ---------------------------------------------------------------------------
 // Launch A: input, q|k|v, attention, o_proj partial.  NPT = 16-position groups of a
 // workgroup's chunk (chunk <= 16 * NPT).
 template <int NPT>
 __global__ __launch_bounds__(kXThreads) void xcd_attn_kernel(const XcdAttnArgs a) {
   constexpr int D = kD;
+  xcd_attn_preload(a);
   const int b = blockIdx.x, g = b & (kXcdGroups - 1), j = b >> 3;
   const int t = threadIdx.x, lane = t & 63;
   const int wid = __builtin_amdgcn_readfirstlane(t >> 6);
   const XcdBufs& X = a.x;
+
+  // the layer input does not depend on the position: its loads go out first
+  XIn xin;
+  bool tok_ok = true;
+  if (wid < 4)
+    xin_issue(a.in_mode, X.hx2, X.pd, a.hin, a.emb_token, a.emb_w, a.emb_s, a.emb_vocab, 4 * t, xin, tok_ok);
 
   const int pos = a.positions[0];
   if (pos < 0 || pos >= a.max_ctx) {
@@ -328,8 +356,6 @@ __global__ __launch_bounds__(kXThreads) void xcd_attn_kernel(const XcdAttnArgs a
   uint32_t e0 = 0, xcc = 0, fl = 0;
 
   // compute-wave registers, loaded at entry
-  XIn xin;
-  bool tok_ok = true;
   WChunk wq[2], wo;
   f32x4 g4 = {0.f, 0.f, 0.f, 0.f};
   float nx0 = 0.f, nx1 = 0.f, rc = 0.f, rs = 0.f;
@@ -347,9 +373,8 @@ __global__ __launch_bounds__(kXThreads) void xcd_attn_kernel(const XcdAttnArgs a
     xcc = xcc_id();
     fl = ld_sc1_u32(flags + j);
   } else {
-    // ---- every load of the launch goes out now: the input first, then the small
-    // ones, then the weights (vector loads retire in issue order) ----
-    xin_issue(a.in_mode, X.hx2, X.pd, a.hin, a.emb_token, a.emb_w, a.emb_s, a.emb_vocab, 4 * t, xin, tok_ok);
+    // ---- every other load of the launch goes out now: the small ones, then the
+    // weights (vector loads retire in issue order) ----
     g4 = prep_gamma(a.in_gamma, t);
     {
       const float* gam = wid < 2 ? a.q_gamma : a.k_gamma;
@@ -613,6 +638,7 @@ __global__ __launch_bounds__(kXThreads) void xcd_attn_kernel(const XcdAttnArgs a
 // ---------------------------------------------------------------------------
 // Launch B: x' = x + o_proj partials, post-attention RMSNorm, gate/up, SwiGLU, down partial.
 __global__ __launch_bounds__(kXThreads) void xcd_mlp_kernel(const XcdMlpArgs a) {
+  xcd_mlp_preload(a);
   const int b = blockIdx.x, g = b & (kXcdGroups - 1), j = b >> 3;
   const int t = threadIdx.x, lane = t & 63;
   const int wid = __builtin_amdgcn_readfirstlane(t >> 6);
