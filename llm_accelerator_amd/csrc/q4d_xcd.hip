@@ -310,8 +310,10 @@ __device__ __forceinline__ void xcd_mlp_preload(const XcdMlpArgs& a) {
 
 // ---------------------------------------------------------------------------
 // Launch A: input, q|k|v, attention, o_proj partial.  NPT = 16-position groups of a
-// workgroup's chunk (chunk <= 16 * NPT).
-template <int NPT>
+// workgroup's chunk (chunk <= 16 * NPT); MODE = the input mode (XcdAttnArgs::in_mode),
+// a template parameter so that every compute wave issues the same loads in the same
+// order whatever the mode: the wait for the input then covers the input loads only.
+template <int NPT, int MODE>
 __global__ __launch_bounds__(kXThreads) void xcd_attn_kernel(const XcdAttnArgs a) {
   constexpr int D = kD;
   xcd_attn_preload(a);
@@ -320,13 +322,50 @@ __global__ __launch_bounds__(kXThreads) void xcd_attn_kernel(const XcdAttnArgs a
   const int wid = __builtin_amdgcn_readfirstlane(t >> 6);
   const XcdBufs& X = a.x;
 
-  // the layer input does not depend on the position: its loads go out first
+  // ---- the loads that do not depend on the position go out first: the layer input,
+  // then the weights (vector loads retire in issue order).  Every wave issues the same
+  // loads, the exchange wave with wave 0's addresses (tc, wc) and without using them:
+  // loads issued under a wave condition make the compiler's wait for the input cover
+  // the loads issued after it as well. ----
+  const int tc = t & 255, wc = wid & 3;
   XIn xin;
   bool tok_ok = true;
-  if (wid < 4)
-    xin_issue(a.in_mode, X.hx2, X.pd, a.hin, a.emb_token, a.emb_w, a.emb_s, a.emb_vocab, 4 * t, xin, tok_ok);
+  WChunk wq[2], wo;
+  f32x4 g4;
+  {
+    xin_issue(MODE, X.hx2, X.pd, a.hin, a.emb_token, a.emb_w, a.emb_s, a.emb_vocab, 4 * tc, xin, tok_ok);
+    g4 = prep_gamma(a.in_gamma, tc);
+    // q|k|v rows 16j .. 16j+15 of the XCD's 512 (one matrix per workgroup)
+    const int R0 = 16 * j;
+    const uint8_t* wm;
+    const uint16_t* sm_;
+    int rb;
+    if (R0 < 2 * D) {
+      wm = a.qw; sm_ = a.qs; rb = 2 * D * g + R0;
+    } else if (R0 < 3 * D) {
+      wm = a.kw; sm_ = a.ks; rb = D * g + R0 - 2 * D;
+    } else {
+      wm = a.vw; sm_ = a.vs; rb = D * g + R0 - 3 * D;
+    }
+    const int c = lane & 31, hf = lane >> 5;
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+      const int row = rb + 4 * wc + 2 * p + hf;
+      wq[p] = load_w(wm, (size_t)row * (kH / 2) + 16 * c, sm_, (size_t)row * (kH / 64) + (c >> 1));
+    }
+    // o_proj rows 32j + t/8, columns 256g + 32 (t % 8) .. +31
+    {
+      const int ro = 32 * j + (tc >> 3), c8 = tc & 7;
+      wo = load_w(a.ow, (size_t)ro * (2 * kH / 2) + 128 * g + 16 * c8, a.os,
+                  (size_t)ro * (2 * kH / 64) + 4 * g + (c8 >> 1));
+    }
+  }
 
-  const int pos = a.positions[0];
+  // the position, by a scalar load whose wait does not cover the vector loads above
+  // (as an ordinary load the compiler made it a vector load behind them and waited
+  // for all of them before issuing anything that depends on it)
+  int pos;
+  asm volatile("s_load_dword %0, %1, 0x0\n\ts_waitcnt lgkmcnt(0)" : "=s"(pos) : "s"(a.positions) : "memory");
   if (pos < 0 || pos >= a.max_ctx) {
     if (b == 0 && t == 0) atomicOr(X.status, Q4D_STATUS_BAD_POSITION);
     return;  // uniform over the grid: no workgroup enters an exchange
@@ -355,9 +394,6 @@ __global__ __launch_bounds__(kXThreads) void xcd_attn_kernel(const XcdAttnArgs a
   uint32_t* flags = X.flags + g * kXcdBlocks;
   uint32_t e0 = 0, xcc = 0, fl = 0;
 
-  // compute-wave registers, loaded at entry
-  WChunk wq[2], wo;
-  f32x4 g4 = {0.f, 0.f, 0.f, 0.f};
   float nx0 = 0.f, nx1 = 0.f, rc = 0.f, rs = 0.f;
   // attention waves (0, 1: q head 2g + wid): for K, lane = 4 p + quarter (position p of
   // a 16-position group, dims 32 quarter .. +31); for V, lane holds dims 2 lane, 2 lane + 1
@@ -369,47 +405,19 @@ __global__ __launch_bounds__(kXThreads) void xcd_attn_kernel(const XcdAttnArgs a
   const uint16_t* vb = a.vcache + (size_t)g * a.max_ctx * D;
   const int plast = pos > 0 ? pos - 1 : 0;
 
-  if (wid == 4) {
-    xcc = xcc_id();
-    fl = ld_sc1_u32(flags + j);
-  } else {
-    // ---- every other load of the launch goes out now: the small ones, then the
-    // weights (vector loads retire in issue order) ----
-    g4 = prep_gamma(a.in_gamma, t);
+  {
     {
-      const float* gam = wid < 2 ? a.q_gamma : a.k_gamma;
+      const float* gam = wc < 2 ? a.q_gamma : a.k_gamma;
       nx0 = gam[lane];
       nx1 = gam[lane + 64];
       rc = a.rope_cos[(size_t)pos * (D / 2) + lane];
       rs = a.rope_sin[(size_t)pos * (D / 2) + lane];
     }
-    // q|k|v rows 16j .. 16j+15 of the XCD's 512 (one matrix per workgroup)
-    const int R0 = 16 * j;
-    const uint8_t* wm;
-    const uint16_t* sm_;
-    int rb;
-    if (R0 < 2 * D) {
-      wm = a.qw; sm_ = a.qs; rb = 2 * D * g + R0;
-    } else if (R0 < 3 * D) {
-      wm = a.kw; sm_ = a.ks; rb = D * g + R0 - 2 * D;
-    } else {
-      wm = a.vw; sm_ = a.vs; rb = D * g + R0 - 3 * D;
-    }
-    const int c = lane & 31, hf = lane >> 5;
-#pragma unroll
-    for (int p = 0; p < 2; ++p) {
-      const int row = rb + 4 * wid + 2 * p + hf;
-      wq[p] = load_w(wm, (size_t)row * (kH / 2) + 16 * c, sm_, (size_t)row * (kH / 64) + (c >> 1));
-    }
-    // o_proj rows 32j + t/8, columns 256g + 32 (t % 8) .. +31
-    {
-      const int ro = 32 * j + (t >> 3), c8 = t & 7;
-      wo = load_w(a.ow, (size_t)ro * (2 * kH / 2) + 128 * g + 16 * c8, a.os,
-                  (size_t)ro * (2 * kH / 64) + 4 * g + (c8 >> 1));
-    }
     // the first 16 positions of the chunk (rows at or past pos load the last cached
-    // row; pos itself is replaced from LDS and rows past the chunk are masked)
-    if (wid < 2) {
+    // row; pos itself is replaced from LDS and rows past the chunk are masked).  Waves
+    // 2 and 3 issue the same loads and do not use them: with the loads issued under
+    // a wave condition, the compiler's wait for the input would cover them as well.
+    {
       int p = cstart + ap;
       p = p < pos ? p : plast;
 #pragma unroll
@@ -425,20 +433,23 @@ __global__ __launch_bounds__(kXThreads) void xcd_attn_kernel(const XcdAttnArgs a
   // ---- the layer input: every workgroup forms all of it (XCD 0, workgroup 0 keeps
   // it as the residual base of launch B) ----
   if (wid < 4) {
-    const f32x4 xv = xin_value(a.in_mode, xin, tok_ok);
+    const f32x4 xv = xin_value(MODE, xin, tok_ok);
     *reinterpret_cast<f32x4*>(&sx[4 * t]) = xv;
     if (b == 0) *reinterpret_cast<f32x4*>(X.hx + 4 * t) = xv;
-    if (a.in_mode == 2 && !tok_ok && b == 0 && t == 0) atomicOr(X.status, Q4D_STATUS_BAD_TOKEN);
+    if (MODE == 2 && !tok_ok && b == 0 && t == 0) atomicOr(X.status, Q4D_STATUS_BAD_TOKEN);
     float ss = fmaf(xv[0], xv[0], fmaf(xv[1], xv[1], fmaf(xv[2], xv[2], xv[3] * xv[3])));
     ss = wave_sum_bcast(ss);
     if (lane == 0) sred[wid] = ss;
   }
   block_sync_lds();
 
-  // ---- input RMSNorm -> hi/lo pairs ----
+  // ---- input RMSNorm -> hi/lo pairs; the exchange wave reads its flag ----
   if (wid < 4) {
     const float inv = 1.0f / sqrtf(((sred[0] + sred[1]) + (sred[2] + sred[3])) / (float)kH + a.eps);
     prep_item(sx, t, true, inv, g4, ph, pl, sm);
+  } else {
+    xcc = xcc_id();
+    fl = ld_sc1_u32(flags + j);
   }
   block_sync_lds();
 
@@ -761,13 +772,23 @@ int xcd_npt(int max_ctx) {
   return n <= 1 ? 1 : n <= 2 ? 2 : n <= 4 ? 4 : n <= 8 ? 8 : 0;
 }
 
-int launch_xcd_attn(const XcdAttnArgs& a, hipStream_t st) {
+template <int NPT>
+void launch_xcd_attn_npt(const XcdAttnArgs& a, hipStream_t st) {
   const dim3 grid(kXcdGroups * kXcdBlocks), block(kXThreads);
+  switch (a.in_mode) {
+    case 0: hipLaunchKernelGGL((xcd_attn_kernel<NPT, 0>), grid, block, 0, st, a); break;
+    case 1: hipLaunchKernelGGL((xcd_attn_kernel<NPT, 1>), grid, block, 0, st, a); break;
+    default: hipLaunchKernelGGL((xcd_attn_kernel<NPT, 2>), grid, block, 0, st, a); break;
+  }
+}
+
+int launch_xcd_attn(const XcdAttnArgs& a, hipStream_t st) {
+  if (a.in_mode < 0 || a.in_mode > 2) return Q4D_ERR_SHAPE;
   switch (xcd_npt(a.max_ctx)) {
-    case 1: hipLaunchKernelGGL(xcd_attn_kernel<1>, grid, block, 0, st, a); break;
-    case 2: hipLaunchKernelGGL(xcd_attn_kernel<2>, grid, block, 0, st, a); break;
-    case 4: hipLaunchKernelGGL(xcd_attn_kernel<4>, grid, block, 0, st, a); break;
-    case 8: hipLaunchKernelGGL(xcd_attn_kernel<8>, grid, block, 0, st, a); break;
+    case 1: launch_xcd_attn_npt<1>(a, st); break;
+    case 2: launch_xcd_attn_npt<2>(a, st); break;
+    case 4: launch_xcd_attn_npt<4>(a, st); break;
+    case 8: launch_xcd_attn_npt<8>(a, st); break;
     default: return Q4D_ERR_CAPACITY;
   }
   return check_launch();
