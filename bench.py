@@ -297,19 +297,19 @@ def decode_launch_floor(torch, fmodel, tokens=15, replays=20, staged=False):
     read of the previous launch's 4 KB output (q4d_diag_launch_chain), graph-replayed:
     what the launches of a token cost without their work.  Grids (blocks x threads) of
     the step's kernels, as the kernel trace of this leg shows them.  XCD-split plan:
-    per layer launch A and launch B, 256 x 320 each, then the LM head 238 x 1024 (which
+    per layer launch A and launch B, 256 x 320 each, then the LM head 256 x 1024 (which
     forms the last layer's output in its prologue).  Staged plan: q|k|v 512 x 256, attention
     ceil(max_ctx / 64) x kv_heads blocks of 256, o_proj 128 x 512, gate/up 384 x 256,
-    down 256 x 384, LM head 238 x 1024."""
+    down 256 x 384, LM head 256 x 1024."""
     from llm_accelerator_amd import _lib
     lib = _lib.load()
     cfg = fmodel.config
     if staged:
         layer = [(512, 1, 256), ((fmodel.max_ctx + 63) // 64, cfg.num_key_value_heads, 256), (128, 1, 512),
                  (384, 1, 256), (256, 1, 384)]
-        shapes = layer * cfg.num_hidden_layers + [(238, 1, 1024)]
+        shapes = layer * cfg.num_hidden_layers + [(256, 1, 1024)]
     else:
-        shapes = [(256, 1, 320), (256, 1, 320)] * cfg.num_hidden_layers + [(238, 1, 1024)]
+        shapes = [(256, 1, 320), (256, 1, 320)] * cfg.num_hidden_layers + [(256, 1, 1024)]
     n = len(shapes)
     gx = (ctypes.c_int32 * n)(*[x for x, _, _ in shapes])
     gy = (ctypes.c_int32 * n)(*[y for _, y, _ in shapes])

@@ -434,7 +434,9 @@ __global__ __launch_bounds__(NWB * 64) void lm_kernel(const GemvArgs a) {
     return d;
   };
 
-  const int base = blockIdx.x * NWB + wid;
+  // waves are numbered wave-major (wave w of every block, then wave w + 1), so the waves
+  // that take one tile more than the others are spread about one per SIMD
+  const int base = wid * gridDim.x + blockIdx.x;
   const int step = gridDim.x * NWB;
   Tile4 A[U], B[U];
 #pragma unroll
@@ -490,10 +492,10 @@ __global__ __launch_bounds__(NWB * 64) void lm_kernel(const GemvArgs a) {
       }
     }
   };
-  // S stages of U tiles per wave (uniform over the grid; the host sizes the
-  // grid so that S >= 2 wherever the matrix allows).  Steady state: both
-  // reloads are unconditional, so each consume waits only for its own stage.
-  const int S = (NT4 + U * step - 1) / (U * step);
+  // S stages of U tiles for this wave (the host sizes the grid so that S >= 2
+  // wherever the matrix allows; tiles past the matrix are masked).  Steady state:
+  // both reloads are unconditional, so each consume waits only for its own stage.
+  const int S = base < NT4 ? (NT4 - base + U * step - 1) / (U * step) : 0;
   auto reload = [&](Tile4 (&D)[U], int st) {
 #pragma unroll
     for (int u = 0; u < U; ++u) D[u] = load4(base + (st * U + u) * step);
@@ -576,13 +578,10 @@ int launch_lm(const GemvArgs& a, hipStream_t stream) {
   constexpr int U = kLmStage, NWB = kLmWaves;
   if (a.rows < 4) return Q4D_ERR_SHAPE;
   const int NT4 = (a.rows + 3) / 4;
-  // stages per wave over the resident grid (at least 2), then the smallest
-  // grid covering the matrix in that many stages (few clamped tail tiles)
+  // the resident grid, or fewer blocks where that leaves every wave two stages
   const int res = resident_blocks(lm_kernel<XP, U, NWB, false>, NWB * 64);
-  const long per_stage = (long)res * NWB * U;
-  int S = (int)((NT4 + per_stage - 1) / per_stage);
-  if (S < 2) S = 2;
-  int blocks = (int)((NT4 + (long)NWB * U * S - 1) / ((long)NWB * U * S));
+  int blocks = (int)((long)NT4 / ((long)NWB * U * 2));
+  if (blocks > res) blocks = res;
   if (blocks < 1) blocks = 1;
   if (a.x_parts)
     hipLaunchKernelGGL((lm_kernel<XP, U, NWB, true>), dim3(blocks), dim3(NWB * 64), 0, stream, a);
