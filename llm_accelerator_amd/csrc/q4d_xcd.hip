@@ -328,6 +328,9 @@ __global__ __launch_bounds__(kXThreads) void xcd_attn_kernel(const XcdAttnArgs a
   // loads issued under a wave condition make the compiler's wait for the input cover
   // the loads issued after it as well. ----
   const int tc = t & 255, wc = wid & 3;
+  // the position through the constant address space: a scalar load issued here, whose
+  // wait the compiler places at the first use (after the input is formed)
+  const int pos = *(const __attribute__((address_space(4))) int32_t*)(a.positions);
   XIn xin;
   bool tok_ok = true;
   WChunk wq[2], wo;
@@ -361,15 +364,6 @@ __global__ __launch_bounds__(kXThreads) void xcd_attn_kernel(const XcdAttnArgs a
     }
   }
 
-  // the position, by a scalar load whose wait does not cover the vector loads above
-  // (as an ordinary load the compiler made it a vector load behind them and waited
-  // for all of them before issuing anything that depends on it)
-  int pos;
-  asm volatile("s_load_dword %0, %1, 0x0\n\ts_waitcnt lgkmcnt(0)" : "=s"(pos) : "s"(a.positions) : "memory");
-  if (pos < 0 || pos >= a.max_ctx) {
-    if (b == 0 && t == 0) atomicOr(X.status, Q4D_STATUS_BAD_POSITION);
-    return;  // uniform over the grid: no workgroup enters an exchange
-  }
   const int T = pos + 1;
   int nA, chunk;
   attn_split(T, nA, chunk);
@@ -394,6 +388,25 @@ __global__ __launch_bounds__(kXThreads) void xcd_attn_kernel(const XcdAttnArgs a
   uint32_t* flags = X.flags + g * kXcdBlocks;
   uint32_t e0 = 0, xcc = 0, fl = 0;
 
+  // ---- the layer input: every workgroup forms all of it (XCD 0, workgroup 0 keeps
+  // it as the residual base of launch B) ----
+  if (wid < 4) {
+    const f32x4 xv = xin_value(MODE, xin, tok_ok);
+    *reinterpret_cast<f32x4*>(&sx[4 * t]) = xv;
+    if (b == 0) *reinterpret_cast<f32x4*>(X.hx + 4 * t) = xv;
+    if (MODE == 2 && !tok_ok && b == 0 && t == 0) atomicOr(X.status, Q4D_STATUS_BAD_TOKEN);
+    float ss = fmaf(xv[0], xv[0], fmaf(xv[1], xv[1], fmaf(xv[2], xv[2], xv[3] * xv[3])));
+    ss = wave_sum_bcast(ss);
+    if (lane == 0) sred[wid] = ss;
+  }
+  block_sync_lds();
+
+  // ---- the position (checked here: every load before this is independent of it),
+  // then the RoPE rows and the K/V rows of the chunk ----
+  if (pos < 0 || pos >= a.max_ctx) {
+    if (b == 0 && t == 0) atomicOr(X.status, Q4D_STATUS_BAD_POSITION);
+    return;  // uniform over the grid: no workgroup enters an exchange
+  }
   float nx0 = 0.f, nx1 = 0.f, rc = 0.f, rs = 0.f;
   // attention waves (0, 1: q head 2g + wid): for K, lane = 4 p + quarter (position p of
   // a 16-position group, dims 32 quarter .. +31); for V, lane holds dims 2 lane, 2 lane + 1
@@ -414,9 +427,9 @@ __global__ __launch_bounds__(kXThreads) void xcd_attn_kernel(const XcdAttnArgs a
       rs = a.rope_sin[(size_t)pos * (D / 2) + lane];
     }
     // the first 16 positions of the chunk (rows at or past pos load the last cached
-    // row; pos itself is replaced from LDS and rows past the chunk are masked).  Waves
-    // 2 and 3 issue the same loads and do not use them: with the loads issued under
-    // a wave condition, the compiler's wait for the input would cover them as well.
+    // row; pos itself is replaced from LDS and rows past the chunk are masked).  Every
+    // wave issues them and only waves 0 and 1 use them: issued under a wave condition,
+    // the compiler's waits for the weights loaded before them would cover them as well.
     {
       int p = cstart + ap;
       p = p < pos ? p : plast;
@@ -430,26 +443,16 @@ __global__ __launch_bounds__(kXThreads) void xcd_attn_kernel(const XcdAttnArgs a
     }
   }
 
-  // ---- the layer input: every workgroup forms all of it (XCD 0, workgroup 0 keeps
-  // it as the residual base of launch B) ----
-  if (wid < 4) {
-    const f32x4 xv = xin_value(MODE, xin, tok_ok);
-    *reinterpret_cast<f32x4*>(&sx[4 * t]) = xv;
-    if (b == 0) *reinterpret_cast<f32x4*>(X.hx + 4 * t) = xv;
-    if (MODE == 2 && !tok_ok && b == 0 && t == 0) atomicOr(X.status, Q4D_STATUS_BAD_TOKEN);
-    float ss = fmaf(xv[0], xv[0], fmaf(xv[1], xv[1], fmaf(xv[2], xv[2], xv[3] * xv[3])));
-    ss = wave_sum_bcast(ss);
-    if (lane == 0) sred[wid] = ss;
-  }
-  block_sync_lds();
+  // the exchange flag, read by every wave (the exchange wave uses it): a load issued by
+  // one wave only shared a register with the compute waves' code and made them wait
+  // for every load before the RMSNorm
+  xcc = xcc_id();
+  fl = ld_sc1_u32(flags + j);
 
-  // ---- input RMSNorm -> hi/lo pairs; the exchange wave reads its flag ----
+  // ---- input RMSNorm -> hi/lo pairs ----
   if (wid < 4) {
     const float inv = 1.0f / sqrtf(((sred[0] + sred[1]) + (sred[2] + sred[3])) / (float)kH + a.eps);
     prep_item(sx, t, true, inv, g4, ph, pl, sm);
-  } else {
-    xcc = xcc_id();
-    fl = ld_sc1_u32(flags + j);
   }
   block_sync_lds();
 
