@@ -16,7 +16,8 @@
 //   launch B: x' = x + sum of the 8 o_proj partials -> post-attention RMSNorm -> the
 //             XCD's 384 gate and 384 up rows -> SwiGLU -> down over the XCD's 384 input
 //             columns: a split-K partial, pd[xcd].
-// The next layer's launch A (or xcd_finalize after the last layer) forms
+// The next layer's launch A (after the last layer: the LM head's prologue in a
+// one-token step, xcd_finalize for a single layer call) forms
 // x'' = x' + sum of the 8 down partials, summed in XCD order so every XCD gets the
 // same bits.
 //
