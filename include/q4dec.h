@@ -141,7 +141,10 @@ int q4d_version(void);
 const char* q4d_status_string(int code);
 /* Bytes of workspace needed by the fused entry points for `batch` sequences. */
 size_t q4d_workspace_bytes(const q4d_model_t* model, int32_t batch);
-/* Zero the workspace counters and status word (call once after allocation). */
+/* Zero the workspace counters, exchange flags and status word (call once after
+ * allocation, and again to clear a status word that reported an error).  With batch 1
+ * it also runs the XCD-split plan's one-time device check (q4d_set_decode_plan), which
+ * synchronises `stream` the first time on each device. */
 int q4d_workspace_init(void* ws, size_t ws_bytes, const q4d_model_t* model, int32_t batch, void* stream);
 /* Precision of fp32 activations inside the GEMVs: 2 (default) = each value
  * enters as an fp16 hi + fp16 lo pair (~22 significant bits); 1 = rounded to
@@ -153,10 +156,24 @@ int q4d_set_activation_precision(int32_t mode);
  * XCD's workgroups exchanging data through its L2; Q4D_DECODE_STAGED runs the five
  * per-stage launches of q4d_layer_stage.  XCD applies to the Qwen3-0.6B shape (hidden
  * 1024, 16/8 heads of 128, intermediate 3072), max_ctx <= 4096 and activation
- * precision 2; other models run staged.  Process-wide; set it before capturing graphs.
- * Returns the previous plan. */
+ * precision 2, on a device that passes a one-time check (at least 256 CUs, one 320-thread
+ * workgroup of each XCD-split kernel fits on a CU, and a probe launch of 256 workgroups
+ * places workgroups b, b + 8, b + 16, ... on one XCD and the eight residues on eight
+ * XCDs, as an unpartitioned MI355X does); other models and devices run staged.  The
+ * check runs in q4d_workspace_init (batch 1) or at the first decode call, synchronises
+ * the stream once, and is skipped (staged plan, not cached) while the stream is being
+ * captured into a graph.  Process-wide; set it before capturing graphs.  Returns the
+ * previous plan. */
 enum { Q4D_DECODE_XCD = 0, Q4D_DECODE_STAGED = 1 };
 int q4d_set_decode_plan(int32_t plan);
+/* The plan a batch-1 decode call with `model` runs on the current device now
+ * (Q4D_DECODE_XCD or Q4D_DECODE_STAGED); runs the device check if it has not run yet.
+ * No reference counterpart. */
+int q4d_decode_plan_active(const q4d_model_t* model, void* stream);
+/* Test hook of the device check (no reference counterpart): mode 1 reports every device
+ * as unsuitable, so the staged plan runs; mode 0 (default) restores the check.  Returns
+ * the previous mode. */
+int q4d_diag_set_xcd_check(int32_t mode);
 /* Copy the device status word into *out (synchronises `stream`). */
 int q4d_read_status(const void* ws, size_t ws_bytes, const q4d_model_t* model, int32_t batch,
                     int32_t* out, void* stream);
@@ -178,6 +195,28 @@ int q4d_qk_norm_rope(const float* x, float* y, const float* gamma, float eps, in
  * x, y: fp32 [batch, heads, head_dim]; cos, sin: fp32 [batch, head_dim] (full width). */
 int q4d_apply_rope(const float* x, float* y, const float* cos, const float* sin, int32_t batch,
                    int32_t heads, int32_t head_dim, void* stream);
+/* manual_apply_rope over a sequence (common.py:173-183, as 04_validate_qk_norm_rope.py:59-60
+ * calls it for a whole prompt): y[b,h,s,:] = x*cos[b,s] + rotate_half(x)*sin[b,s].
+ * x, y: fp32 [batch, heads, seq, head_dim] (y must not alias x); cos, sin: fp32
+ * [batch, seq, head_dim].  q4d_apply_rope is the seq = 1 case. */
+int q4d_apply_rope_seq(const float* x, float* y, const float* cos, const float* sin, int32_t batch,
+                       int32_t heads, int32_t seq, int32_t head_dim, void* stream);
+/* manual_rotate_half (common.py:148-152): y = cat(-x[..., d/2:], x[..., :d/2]) per row.
+ * x, y: fp32 [rows, head_dim], not aliased. */
+int q4d_rotate_half(const float* x, float* y, int64_t rows, int32_t head_dim, void* stream);
+/* manual_causal_attention (common.py:201-216; called by 06_validate_attention.py:71):
+ * out = softmax(q k^T * scaling + causal mask) v per head, GQA with q head h reading kv head
+ * h / (q_heads / kv_heads) (manual_repeat_kv, common.py:192-198, without the copy).
+ * q, out: fp32 [batch, q_heads, seq, head_dim]; k, v: fp32 [batch, kv_heads, seq,
+ * head_dim]; head_dim 128; 16-byte aligned.  The operands are rounded to fp16 (q with
+ * scaling folded in) for the MFMA flash-attention kernel of q4d_prefill, which keeps
+ * the probabilities in fp16 and accumulates in fp32; the softmax weights are not
+ * materialised.  ws: q4d_causal_attention_workspace_bytes(batch, q_heads, kv_heads, seq)
+ * bytes, 256-byte aligned. */
+size_t q4d_causal_attention_workspace_bytes(int32_t batch, int32_t q_heads, int32_t kv_heads, int32_t seq);
+int q4d_causal_attention(const float* q, const float* k, const float* v, float* out, int32_t batch,
+                         int32_t q_heads, int32_t kv_heads, int32_t seq, int32_t head_dim, float scaling,
+                         void* ws, size_t ws_bytes, void* stream);
 /* Write k, v (fp32 [batch, kv_heads, head_dim]) into layer `layer` of the cache at positions[b];
  * either of k / v may be NULL to leave that plane untouched. */
 int q4d_kv_append(const q4d_kv_cache_t* kv, int32_t layer, const float* k, const float* v,

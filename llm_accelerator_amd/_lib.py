@@ -18,6 +18,12 @@ Q4D_F32 = 1
 Q4D_BF16 = 2
 STATUS_BAD_TOKEN = 1
 STATUS_BAD_POSITION = 2
+STATUS_XCD_MAP = 4
+STATUS_SYNC_TIMEOUT = 8
+STATUS_NAMES = {STATUS_BAD_TOKEN: "BAD_TOKEN", STATUS_BAD_POSITION: "BAD_POSITION", STATUS_XCD_MAP: "XCD_MAP",
+                STATUS_SYNC_TIMEOUT: "SYNC_TIMEOUT"}
+DECODE_XCD = 0
+DECODE_STAGED = 1
 
 # Status codes (include/q4dec.h); 0..-10 mirror QOT_ERR_* of
 # FPGA_Project/software/qmap_one_token_runtime/qmap_one_token_runtime.h:17-29.
@@ -126,6 +132,8 @@ SIGNATURES = {
     "q4d_workspace_init": ([_P, c_size_t, POINTER(Q4dModel), c_int32, _P], c_int32),
     "q4d_set_activation_precision": ([c_int32], c_int32),
     "q4d_set_decode_plan": ([c_int32], c_int32),
+    "q4d_decode_plan_active": ([POINTER(Q4dModel), _P], c_int32),
+    "q4d_diag_set_xcd_check": ([c_int32], c_int32),
     "q4d_read_status": ([_P, c_size_t, POINTER(Q4dModel), c_int32, POINTER(c_int32), _P], c_int32),
     "q4d_linear": ([POINTER(Q4dMatrix), _P, c_int32, _P, c_int32, c_int32, _P], c_int32),
     "q4d_rms_norm": ([_P, _P, c_float, c_int32, c_int32, _P, c_int32, _P], c_int32),
@@ -152,6 +160,11 @@ SIGNATURES = {
                                     c_int32, _P, c_size_t, _P], c_int32),
     "q4d_run_one_token_noalloc": ([POINTER(Q4dModel), _P, _P, POINTER(Q4dKVCache), _P, _P, _P, _P, _P], c_int32),
     "q4d_apply_rope": ([_P, _P, _P, _P, c_int32, c_int32, c_int32, _P], c_int32),
+    "q4d_apply_rope_seq": ([_P, _P, _P, _P, c_int32, c_int32, c_int32, c_int32, _P], c_int32),
+    "q4d_rotate_half": ([_P, _P, ctypes.c_int64, c_int32, _P], c_int32),
+    "q4d_causal_attention_workspace_bytes": ([c_int32, c_int32, c_int32, c_int32], c_size_t),
+    "q4d_causal_attention": ([_P, _P, _P, _P, c_int32, c_int32, c_int32, c_int32, c_int32, c_float, _P, c_size_t,
+                              _P], c_int32),
     "q4d_diag_launch_chain": ([_P, _P, _P, c_int32, _P, _P], c_int32),
     "q4d_advance": ([_P, _P, _P, _P, _P, _P, _P, c_int32, _P], c_int32),
     "q4d_advance_session": ([_P, _P, _P, _P, _P, _P, _P, c_int32, _P, _P], c_int32),
@@ -211,3 +224,19 @@ def load(path: Path | str | None = None) -> ctypes.CDLL:
 def check(rc: int, what: str) -> None:
     if rc != 0:
         raise Q4DecError(rc, what)
+
+
+def status_names(status: int) -> list[str]:
+    """Names of the Q4D_STATUS_* bits set in a device status word."""
+    return [n for bit, n in STATUS_NAMES.items() if status & bit] + (["UNKNOWN"] if status & ~0xF else [])
+
+
+def check_status(status: int, what: str) -> None:
+    """Raise Q4DecError(Q4D_ERR_STATUS) if the device status word has any bit set:
+    the results of the calls that set it are not valid (q4d_read_status)."""
+    if status:
+        err = Q4DecError(-6, what)
+        err.status = status
+        err.args = (f"{what}: device status {status:#x} ({', '.join(status_names(status))}); "
+                    "the results are not valid",)
+        raise err

@@ -12,8 +12,9 @@ What changes is only the types:
   reallocation); ``append_cache(None, v)`` allocates a standalone cache;
 * ``manual_repeat_kv`` returns a :class:`RepeatedKV` marker instead of a
   copy: the attention kernel maps q head ``h`` to kv head ``h // repeat``;
-* ``manual_cached_attention`` returns ``(output, None)``: the softmax weights
-  are never materialised.
+* ``manual_cached_attention`` returns ``(output, None)`` and
+  ``manual_causal_attention`` ``(output, AttentionWeights)`` (shape only): the
+  softmax weights are never materialised.
 
 Errors: a failing entry point raises :class:`~llm_accelerator_amd._lib.Q4DecError`
 (a ``RuntimeError``, as the reference's ``require_*``/``finish`` raise).
@@ -88,20 +89,36 @@ def manual_rope_cos_sin(rotary_emb: Any, x: torch.Tensor, position_ids: torch.Te
     return torch.cat((c, c), dim=-1), torch.cat((s, s), dim=-1)
 
 
+def manual_rotate_half(x: torch.Tensor) -> torch.Tensor:
+    """``cat(-x[..., D/2:], x[..., :D/2])`` over the last dim (common.py:148-152); fp32."""
+    xf = _dev_f32(x, "x")
+    d = xf.shape[-1]
+    y = torch.empty_like(xf)
+    if xf.numel():
+        check(_lib.load().q4d_rotate_half(xf.data_ptr(), y.data_ptr(), xf.numel() // d, d, current_stream()),
+              "q4d_rotate_half")
+    return y
+
+
 def manual_apply_rope(q: torch.Tensor, k: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor):
-    """``x*cos + rotate_half(x)*sin`` for q [B,H,1,D] and k [B,KVH,1,D]
-    with cos/sin [B,1,D] (common.py:173-183)."""
+    """``x*cos + rotate_half(x)*sin`` (common.py:173-183) for q [B,H,S,D] and
+    k [B,KVH,S,D] with cos/sin [B,S,D] (a batch of 1 broadcasts over B), for one
+    decode position or a whole prompt (04_validate_qk_norm_rope.py:59-60)."""
     lib = _lib.load()
+    if q.dim() != 4 or k.dim() != 4 or q.shape[0] != k.shape[0] or q.shape[2:] != k.shape[2:]:
+        raise ValueError("q and k must be [B, heads, S, D] with the same B, S, D")
+    b, _, seq, d = q.shape
+    if cos.shape[-2:] != (seq, d) or sin.shape != cos.shape or cos.dim() != 3 or cos.shape[0] not in (1, b):
+        raise ValueError(f"cos/sin must be [B, {seq}, {d}] (or [1, {seq}, {d}])")
+    c = _dev_f32(cos.expand(b, seq, d), "cos")
+    s = _dev_f32(sin.expand(b, seq, d), "sin")
     out = []
-    c = _dev_f32(cos, "cos").reshape(cos.shape[0], -1)
-    s = _dev_f32(sin, "sin").reshape(sin.shape[0], -1)
     for t in (q, k):
         tf = _dev_f32(t, "q/k")
-        if tf.shape[2] != 1:
-            raise ValueError("decode RoPE takes one position per sequence")
         y = torch.empty_like(tf)
-        check(lib.q4d_apply_rope(tf.data_ptr(), y.data_ptr(), c.data_ptr(), s.data_ptr(), tf.shape[0],
-                                 tf.shape[1], tf.shape[3], current_stream()), "q4d_apply_rope")
+        if tf.numel():
+            check(lib.q4d_apply_rope_seq(tf.data_ptr(), y.data_ptr(), c.data_ptr(), s.data_ptr(), b, tf.shape[1],
+                                         seq, d, current_stream()), "q4d_apply_rope_seq")
         out.append(y)
     return out[0], out[1]
 
@@ -122,10 +139,28 @@ class KVLayerView:
 
 
 class RepeatedKV:
-    """``manual_repeat_kv`` result: the cache plus the GQA repeat factor."""
+    """``manual_repeat_kv`` result: the cache view (or the K/V tensor) plus the GQA
+    repeat factor; ``shape`` is the shape the reference's repeated copy would have."""
 
-    def __init__(self, view: KVLayerView, repeat: int):
+    def __init__(self, view, repeat: int):
         self.view, self.repeat = view, repeat
+
+    @property
+    def shape(self):
+        b, kvh, t, d = tuple(self.view.shape)
+        return torch.Size((b, kvh * self.repeat, t, d))
+
+
+class AttentionWeights:
+    """Stand-in for the softmax weights ``manual_causal_attention`` returns
+    (common.py:213-216): the flash-attention kernel never materialises them, so
+    only their shape [B, H, S, S] and dtype are given."""
+
+    def __init__(self, shape, dtype=torch.float32):
+        self.shape, self.dtype = torch.Size(shape), dtype
+
+    def __repr__(self) -> str:
+        return f"AttentionWeights(shape={list(self.shape)}, not materialised)"
 
 
 def layer_views(cache: KVCache, length: int = 0) -> tuple[list, list]:
@@ -158,9 +193,44 @@ def append_cache(old_cache: KVLayerView | None, current_value: torch.Tensor) -> 
     return KVLayerView(c, view.layer, view.kind, view.length + 1)
 
 
-def manual_repeat_kv(x: KVLayerView, repeat_count: int) -> RepeatedKV:
-    """GQA repeat as a marker (common.py:192-198)."""
+def manual_repeat_kv(x, repeat_count: int) -> RepeatedKV:
+    """GQA repeat as a marker (common.py:192-198) over a cache view or a
+    [B, KVH, S, D] tensor: q head h reads kv head h // repeat_count."""
+    if isinstance(x, RepeatedKV):
+        return RepeatedKV(x.view, x.repeat * repeat_count)
     return RepeatedKV(x, repeat_count)
+
+
+def manual_causal_attention(q: torch.Tensor, k, v, scaling: float):
+    """``softmax(q k^T * scaling, causal) v`` (common.py:201-216), the prompt
+    attention 06_validate_attention.py:71 calls.  q [B,H,S,D]; k, v: the
+    :func:`manual_repeat_kv` markers of [B,KVH,S,D] tensors or [B,H,S,D] tensors.
+    Returns ``(output [B,H,S,D] fp32, AttentionWeights)``: MFMA flash attention
+    over fp16-rounded operands (q4d_causal_attention), no weights materialised."""
+    def unwrap(x, name):
+        if isinstance(x, RepeatedKV):
+            if not isinstance(x.view, torch.Tensor):
+                raise TypeError(f"{name}: causal attention takes tensors (cache views go to manual_cached_attention)")
+            return x.view, x.repeat
+        return x, 1
+    kt, kr = unwrap(k, "k")
+    vt, vr = unwrap(v, "v")
+    if q.dim() != 4 or kt.dim() != 4 or vt.shape != kt.shape or kr != vr:
+        raise ValueError("q [B,H,S,D]; k and v of one shape [B,KVH,S,D] with one repeat factor")
+    b, h, s, d = q.shape
+    kvh = kt.shape[1]
+    if kt.shape[0] != b or kt.shape[2:] != (s, d) or kvh * kr != h:
+        raise ValueError(f"k/v {tuple(kt.shape)} x repeat {kr} do not match q {tuple(q.shape)}")
+    lib = _lib.load()
+    qf, kf, vf = _dev_f32(q, "q"), _dev_f32(kt, "k"), _dev_f32(vt, "v")
+    out = torch.empty_like(qf)
+    if qf.numel():
+        nbytes = int(lib.q4d_causal_attention_workspace_bytes(b, h, kvh, s))
+        ws = torch.empty(nbytes, dtype=torch.uint8, device=qf.device)
+        check(lib.q4d_causal_attention(qf.data_ptr(), kf.data_ptr(), vf.data_ptr(), out.data_ptr(), b, h, kvh, s, d,
+                                       float(scaling), ws.data_ptr(), nbytes, current_stream()),
+              "q4d_causal_attention")
+    return out, AttentionWeights((b, h, s, s))
 
 
 _model_registry: dict[int, tuple] = {}
@@ -189,6 +259,8 @@ def manual_cached_attention(q_current: torch.Tensor, k_cache_repeated: RepeatedK
     """``softmax(q k^T * scaling) v`` over the cached positions
     (common.py:219-228); q [B,H,1,D] fp32 -> ([B,H,1,D], None)."""
     kv = k_cache_repeated.view
+    if not isinstance(kv, KVLayerView) or not isinstance(v_cache_repeated.view, KVLayerView):
+        raise TypeError("cached attention reads KVLayerView caches (prompt tensors go to manual_causal_attention)")
     if v_cache_repeated.view.cache is not kv.cache or v_cache_repeated.view.layer != kv.layer:
         raise ValueError("k and v views must come from the same cache layer")
     cache = kv.cache
@@ -259,6 +331,9 @@ def manual_decoder_layer_cached(hidden: torch.Tensor, layer: Any, rotary_emb: An
     check(_lib.load().q4d_decoder_layer(ctypes.byref(desc), li, h_in.data_ptr(), h_out.data_ptr(),
                                         ctypes.byref(kvd), rt.pos.data_ptr(), rt.ws.ptr, rt.ws.nbytes,
                                         current_stream()), "q4d_decoder_layer")
+    # synchronous like the reference function: a device-side failure (an exchange of the
+    # XCD-split layer that timed out or ran off its XCD) raises here
+    rt.ws.raise_for_status("q4d_decoder_layer")
     return (h_out.view(1, 1, cfg.hidden_size), KVLayerView(k_cache.cache, li, 0, position + 1),
             KVLayerView(v_cache.cache, li, 1, position + 1))
 
@@ -291,6 +366,7 @@ def run_manual_one_token(current_token_ids: torch.Tensor, position: int, embeddi
                                         rt.next_tok.data_ptr(), rt.score.data_ptr(),
                                         logits.data_ptr() if logits is not None else None, rt.ws.ptr,
                                         rt.ws.nbytes, current_stream()), "q4d_run_one_token")
+    rt.ws.raise_for_status("q4d_run_one_token")
     for i in range(len(manual_k_caches)):
         manual_k_caches[i] = KVLayerView(k0.cache, i, 0, position + 1)
         manual_v_caches[i] = KVLayerView(k0.cache, i, 1, position + 1)
@@ -298,6 +374,7 @@ def run_manual_one_token(current_token_ids: torch.Tensor, position: int, embeddi
 
 
 __all__ = ["get_rms_norm_eps", "manual_rms_norm", "manual_linear_from_weight", "manual_rope_cos_sin",
-           "manual_apply_rope", "append_cache", "manual_repeat_kv", "manual_cached_attention",
+           "manual_rotate_half", "manual_apply_rope", "append_cache", "manual_repeat_kv",
+           "manual_causal_attention", "manual_cached_attention", "AttentionWeights",
            "manual_decoder_layer_cached", "run_manual_one_token", "KVLayerView", "RepeatedKV", "layer_views",
            "runtime", "Q4D_F16"]

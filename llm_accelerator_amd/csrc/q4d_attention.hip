@@ -292,8 +292,11 @@ __global__ __launch_bounds__(256) void attn_kernel(const AttnArgs a) {
     const int p = pr + 16 * i;
     const float e0 = p < n ? ssc[0][p] : 0.f;
     const float e1 = p < n ? ssc[1][p] : 0.f;
+    // rows past the chunk stand in for absent positions: zero them rather than weight an
+    // Inf or NaN bit pattern of a row not yet written by 0
+    const u32x4 vq = p < n ? vr[i] : u32x4{0u, 0u, 0u, 0u};
     float vf[8];
-    unpack8(vr[i], vf);
+    unpack8(vq, vf);
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       o0[e] = fmaf(e0, vf[e], o0[e]);
@@ -567,8 +570,9 @@ __global__ __launch_bounds__(256) void attn_span_kernel(const AttnArgs a, int sp
       const int p = pr + 16 * i;
       const float e0 = p < n ? ssc[0][p] : 0.f;
       const float e1 = p < n ? ssc[1][p] : 0.f;
+      const u32x4 vq = p < n ? vr[i] : u32x4{0u, 0u, 0u, 0u};  // as in attn_kernel
       float vf[8];
-      unpack8(vr[i], vf);
+      unpack8(vq, vf);
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         o0[e] = fmaf(e0, vf[e], o0[e]);

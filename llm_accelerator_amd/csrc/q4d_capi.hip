@@ -107,7 +107,7 @@ struct Feedback {
   int32_t hist_capacity;
 };
 
-bool xcd_eligible(const q4d_model_t* m);
+bool xcd_eligible(const q4d_model_t* m, hipStream_t st);
 int run_layer_xcd(const q4d_model_t* m, int l, int in_mode, const float* hin, const int32_t* emb_tokens,
                   float* hout, const q4d_kv_cache_t* kv, const int32_t* positions, void* ws, const WsLayout& W,
                   int32_t* status, hipStream_t st);
@@ -120,7 +120,7 @@ int run_layer_xcd(const q4d_model_t* m, int l, int in_mode, const float* hin, co
 int run_layer(const q4d_model_t* m, int l, const float* hin, float* hout, const q4d_kv_cache_t* kv,
               const int32_t* positions, void* ws, const WsLayout& W, hipStream_t st, int only = -1,
               int32_t* status = nullptr, const int32_t* emb_tokens = nullptr) {
-  if (only < 0 && xcd_eligible(m)) {
+  if (only < 0 && xcd_eligible(m, st)) {
     int32_t* stw = status ? status : ws_ptr<int32_t>(ws, W.status);
     return emb_tokens ? run_layer_xcd(m, l, 2, nullptr, emb_tokens, hout, kv, positions, ws, W, stw, st)
                       : run_layer_xcd(m, l, 1, hin, nullptr, hout, kv, positions, ws, W, stw, st);
@@ -232,11 +232,12 @@ int run_layer(const q4d_model_t* m, int l, const float* hin, float* hout, const 
   return Q4D_OK;
 }
 
-// The XCD-split layer (q4d_xcd.hip) covers the Qwen3-0.6B shape at activation precision 2.
-bool xcd_eligible(const q4d_model_t* m) {
+// The XCD-split layer (q4d_xcd.hip) covers the Qwen3-0.6B shape at activation precision 2,
+// on a device that passes its placement check (xcd_device_ok); anything else runs staged.
+bool xcd_eligible(const q4d_model_t* m, hipStream_t st) {
   return g_decode_plan == Q4D_DECODE_XCD && g_act_precision == 2 && m->hidden_size == 1024 &&
          m->intermediate_size == kXcdInter && m->num_q_heads == 2 * kXcdGroups && m->num_kv_heads == kXcdGroups &&
-         m->head_dim == 128 && xcd_npt(m->max_ctx) > 0;
+         m->head_dim == 128 && xcd_npt(m->max_ctx) > 0 && xcd_device_ok(st);
 }
 
 XcdBufs xcd_bufs(void* ws, const WsLayout& W, int32_t* status) {
@@ -335,7 +336,7 @@ int run_token(const q4d_model_t* m, const int32_t* tokens, const int32_t* positi
               hipStream_t st, const Feedback* fb = nullptr) {
   float* hidden = ws_ptr<float>(ws, W.hidden);
   int rc;
-  if (xcd_eligible(m)) {
+  if (xcd_eligible(m, st)) {
     // layer l > 0 takes its input from the previous layer's launches directly; the LM
     // head's prologue forms the last layer's output (stored in `hidden` as well)
     for (int l = 0; l < m->num_layers; ++l)
@@ -424,8 +425,21 @@ int q4d_workspace_init(void* ws, size_t ws_bytes, const q4d_model_t* model, int3
   int rc = check_ws(ws, ws_bytes, model, batch);
   if (rc) return rc;
   const WsLayout W = ws_layout(model, batch);
+  // the XCD-split plan's one-time device check runs here, before any decode call
+  // (and before a caller captures decode steps into a graph)
+  if (batch == 1) xcd_device_ok(as_stream(stream));
   // status block and counters are contiguous at the start of the workspace
   return launch_fill_i32(ws_ptr<int32_t>(ws, 0), 0, W.hidden / 4, as_stream(stream));
+}
+
+int q4d_decode_plan_active(const q4d_model_t* model, void* stream) {
+  if (!model) return Q4D_ERR_NULL;
+  return xcd_eligible(model, as_stream(stream)) ? Q4D_DECODE_XCD : Q4D_DECODE_STAGED;
+}
+
+int q4d_diag_set_xcd_check(int32_t mode) {
+  if (mode != 0 && mode != 1) return Q4D_ERR_SHAPE;
+  return xcd_set_check_mode(mode);
 }
 
 int q4d_read_status(const void* ws, size_t ws_bytes, const q4d_model_t* model, int32_t batch, int32_t* out,
@@ -963,9 +977,39 @@ int q4d_advance_session(int32_t* tokens, int32_t* positions, const int32_t* next
 
 int q4d_apply_rope(const float* x, float* y, const float* cos, const float* sin, int32_t batch, int32_t heads,
                    int32_t head_dim, void* stream) {
+  return q4d_apply_rope_seq(x, y, cos, sin, batch, heads, 1, head_dim, stream);
+}
+
+int q4d_apply_rope_seq(const float* x, float* y, const float* cos, const float* sin, int32_t batch, int32_t heads,
+                       int32_t seq, int32_t head_dim, void* stream) {
   if (!x || !y || !cos || !sin) return Q4D_ERR_NULL;
-  if (batch <= 0 || heads <= 0 || head_dim <= 0 || (head_dim & 1)) return Q4D_ERR_SHAPE;
-  return launch_apply_rope(x, y, cos, sin, batch, heads, head_dim, as_stream(stream));
+  if (batch <= 0 || heads <= 0 || seq <= 0 || head_dim <= 0 || (head_dim & 1)) return Q4D_ERR_SHAPE;
+  return launch_apply_rope(x, y, cos, sin, batch, heads, seq, head_dim, as_stream(stream));
+}
+
+int q4d_rotate_half(const float* x, float* y, int64_t rows, int32_t head_dim, void* stream) {
+  if (!x || !y) return Q4D_ERR_NULL;
+  if (rows <= 0 || head_dim <= 0 || (head_dim & 1) || rows > (int64_t(1) << 40) / head_dim) return Q4D_ERR_SHAPE;
+  return launch_rotate_half(x, y, rows, head_dim, as_stream(stream));
+}
+
+size_t q4d_causal_attention_workspace_bytes(int32_t batch, int32_t q_heads, int32_t kv_heads, int32_t seq) {
+  if (batch <= 0 || q_heads <= 0 || kv_heads <= 0 || seq <= 0) return 0;
+  return causal_attention_ws_bytes(batch, q_heads, kv_heads, seq);
+}
+
+int q4d_causal_attention(const float* q, const float* k, const float* v, float* out, int32_t batch,
+                         int32_t q_heads, int32_t kv_heads, int32_t seq, int32_t head_dim, float scaling, void* ws,
+                         size_t ws_bytes, void* stream) {
+  if (!q || !k || !v || !out || !ws) return Q4D_ERR_NULL;
+  if (batch <= 0 || q_heads <= 0 || kv_heads <= 0 || seq <= 0 || q_heads % kv_heads || q_heads > 65535)
+    return Q4D_ERR_SHAPE;
+  if (head_dim != 128) return Q4D_ERR_SHAPE;
+  if ((long long)batch * q_heads * seq * head_dim > (1LL << 40)) return Q4D_ERR_SHAPE;
+  if (!aligned(q, 16) || !aligned(k, 16) || !aligned(v, 16) || !aligned(out, 16) || !aligned(ws, 256))
+    return Q4D_ERR_BAD_ADDR;
+  if (ws_bytes < causal_attention_ws_bytes(batch, q_heads, kv_heads, seq)) return Q4D_ERR_CAPACITY;
+  return launch_causal_attention(q, k, v, out, batch, q_heads, kv_heads, seq, scaling, ws, as_stream(stream));
 }
 
 int q4d_diag_launch_chain(const int32_t* grid_x, const int32_t* grid_y, const int32_t* block, int32_t n,

@@ -265,6 +265,11 @@ struct XcdMlpArgs {
 };
 // 16-position groups per thread of launch A for a KV capacity (0: unsupported, > 4096).
 int xcd_npt(int max_ctx);
+// Whether the current device suits the XCD-split launches (checked once per device;
+// see q4d_decode_plan_active).  xcd_set_check_mode(1) reports every device as
+// unsuitable, 0 restores the check (q4d_diag_set_xcd_check); returns the previous mode.
+bool xcd_device_ok(hipStream_t st);
+int xcd_set_check_mode(int mode);
 int launch_xcd_attn(const XcdAttnArgs& a, hipStream_t st);
 int launch_xcd_mlp(const XcdMlpArgs& a, hipStream_t st);
 // out = hx2 + sum of the 8 down partials.
@@ -381,6 +386,13 @@ int launch_advance(int32_t* tokens, int32_t* positions, const int32_t* next_toke
                    int32_t* hist_tokens, float* hist_scores, int32_t* hist_count, int32_t hist_capacity,
                    hipStream_t stream);
 int launch_apply_rope(const float* x, float* y, const float* cosv, const float* sinv, int batch, int heads,
-                      int head_dim, hipStream_t stream);
+                      int seq, int head_dim, hipStream_t stream);
+int launch_rotate_half(const float* x, float* y, long long rows, int head_dim, hipStream_t stream);
+// Causal GQA attention over fp32 q [batch, qh, seq, 128], k / v [batch, kvh, seq, 128]
+// -> fp32 out [batch, qh, seq, 128] through prefill_attn_kernel (q4d_prefill.hip);
+// ws holds the fp16 operands (causal_attention_ws_bytes).
+size_t causal_attention_ws_bytes(int batch, int qh, int kvh, int seq);
+int launch_causal_attention(const float* q, const float* k, const float* v, float* out, int batch, int qh,
+                            int kvh, int seq, float scaling, void* ws, hipStream_t st);
 
 }  // namespace q4d

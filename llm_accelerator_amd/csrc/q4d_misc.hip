@@ -235,22 +235,45 @@ int launch_advance(int32_t* tokens, int32_t* positions, const int32_t* next_toke
   return check_launch();
 }
 
-// y = x * cos + rotate_half(x) * sin (common.py:148-152, 173-183); one block per (batch, head).
+// y = x * cos + rotate_half(x) * sin (common.py:148-152, 173-183) for x [batch, heads,
+// seq, head_dim] and cos / sin [batch, seq, head_dim]; one block per (batch, head, position).
 __global__ __launch_bounds__(128) void apply_rope_kernel(const float* x, float* y, const float* cosv,
-                                                         const float* sinv, int heads, int head_dim) {
-  const int bh = blockIdx.x, b = bh / heads, half = head_dim / 2;
-  const float* xr = x + (size_t)bh * head_dim;
+                                                         const float* sinv, int heads, int seq, int head_dim) {
+  const int r = blockIdx.x, sp = r % seq, b = r / seq / heads, half = head_dim / 2;
+  const float* xr = x + (size_t)r * head_dim;
+  const float* cr = cosv + ((size_t)b * seq + sp) * head_dim;
+  const float* sr = sinv + ((size_t)b * seq + sp) * head_dim;
   for (int d = threadIdx.x; d < head_dim; d += blockDim.x) {
     const float rot = d < half ? -xr[d + half] : xr[d - half];
-    y[(size_t)bh * head_dim + d] = xr[d] * cosv[(size_t)b * head_dim + d] + rot * sinv[(size_t)b * head_dim + d];
+    y[(size_t)r * head_dim + d] = xr[d] * cr[d] + rot * sr[d];
   }
 }
 
 int launch_apply_rope(const float* x, float* y, const float* cosv, const float* sinv, int batch, int heads,
-                      int head_dim, hipStream_t stream) {
+                      int seq, int head_dim, hipStream_t stream) {
   if (x == y) return Q4D_ERR_SHAPE;  // rotate_half reads the other half of the row
-  hipLaunchKernelGGL(apply_rope_kernel, dim3(batch * heads), dim3(128), 0, stream, x, y, cosv, sinv, heads,
+  const long long rows = (long long)batch * heads * seq;
+  if (rows > 0x7fffffffLL) return Q4D_ERR_SHAPE;
+  hipLaunchKernelGGL(apply_rope_kernel, dim3((unsigned)rows), dim3(128), 0, stream, x, y, cosv, sinv, heads, seq,
                      head_dim);
+  return check_launch();
+}
+
+// y = cat(-x[..., half:], x[..., :half]) per row of head_dim (common.py:148-152).
+__global__ __launch_bounds__(256) void rotate_half_kernel(const float* x, float* y, long long n, int head_dim) {
+  const int half = head_dim / 2;
+  for (long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (long long)gridDim.x * blockDim.x) {
+    const int d = (int)(i % head_dim);
+    y[i] = d < half ? -x[i + half] : x[i - half];
+  }
+}
+
+int launch_rotate_half(const float* x, float* y, long long rows, int head_dim, hipStream_t stream) {
+  if (x == y) return Q4D_ERR_SHAPE;
+  const long long n = rows * head_dim;
+  const long long blocks = (n + 255) / 256;
+  hipLaunchKernelGGL(rotate_half_kernel, dim3((unsigned)(blocks < 8192 ? blocks : 8192)), dim3(256), 0, stream,
+                     x, y, n, head_dim);
   return check_launch();
 }
 

@@ -20,6 +20,7 @@
 // Row strides of the LDS tiles: 136 and 68 fp16 (measured best of the 16-byte /
 // 8-byte aligned choices; SQ_LDS_BANK_CONFLICT fell with the row-contiguous K stores).
 #include <math.h>
+#include <string.h>
 
 #include "q4d_device.h"
 #include "q4d_internal.h"
@@ -241,6 +242,88 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
 int launch_prefill_attention(const PrefillArgs& a, hipStream_t st) {
   hipLaunchKernelGGL(prefill_attn_kernel, dim3((a.n + kBQ - 1) / kBQ, a.qh), dim3(256), 0, st, a);
   return check_launch();
+}
+
+// ---- the causal-attention primitive (manual_causal_attention, common.py:201-216) -----
+// The fp32 operands are rounded to the fp16 layouts prefill_attn_kernel reads (q with
+// the softmax scale and log2(e) folded in, as the prefill's q|k|v epilogue leaves it;
+// k / v as a cache plane of max_ctx = seq positions), and its fp16 output
+// [seq][qh][128] is widened back to fp32 [qh][seq][128].
+namespace {
+
+__global__ __launch_bounds__(256) void to_f16_kernel(const float* x, _Float16* y, long long n4, float mul) {
+  for (long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x; i < n4; i += (long long)gridDim.x * blockDim.x) {
+    const f32x4 v = reinterpret_cast<const f32x4*>(x)[i];
+    h4 h;
+    h[0] = (_Float16)(v[0] * mul);
+    h[1] = (_Float16)(v[1] * mul);
+    h[2] = (_Float16)(v[2] * mul);
+    h[3] = (_Float16)(v[3] * mul);
+    reinterpret_cast<h4*>(y)[i] = h;
+  }
+}
+
+// out[h][s][d] = o16[s][h][d] for one sequence
+__global__ __launch_bounds__(256) void attn_out_kernel(const _Float16* o16, float* out, int seq, int qh) {
+  const long long n4 = (long long)qh * seq * (kD / 4);
+  for (long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x; i < n4; i += (long long)gridDim.x * blockDim.x) {
+    const int d4 = (int)(i % (kD / 4));
+    const long long hs = i / (kD / 4);
+    const int sp = (int)(hs % seq), h = (int)(hs / seq);
+    const h4 v = *reinterpret_cast<const h4*>(o16 + ((size_t)sp * qh + h) * kD + 4 * d4);
+    reinterpret_cast<f32x4*>(out)[i] = f32x4{(float)v[0], (float)v[1], (float)v[2], (float)v[3]};
+  }
+}
+
+inline unsigned grid_for(long long n4) {
+  const long long b = (n4 + 255) / 256;
+  return (unsigned)(b < 16384 ? b : 16384);
+}
+
+}  // namespace
+
+size_t causal_attention_ws_bytes(int batch, int qh, int kvh, int seq) {
+  const size_t A = 256;
+  const size_t q = align_up((size_t)batch * qh * seq * kD * 2, A);
+  const size_t kv = align_up((size_t)batch * kvh * seq * kD * 2, A);
+  const size_t o = align_up((size_t)seq * qh * kD * 2, A);
+  return q + 2 * kv + o;
+}
+
+int launch_causal_attention(const float* q, const float* k, const float* v, float* out, int batch, int qh,
+                            int kvh, int seq, float scaling, void* ws, hipStream_t st) {
+  const size_t A = 256;
+  const size_t qn = (size_t)batch * qh * seq * kD, kvn = (size_t)batch * kvh * seq * kD;
+  char* base = static_cast<char*>(ws);
+  _Float16* q16 = reinterpret_cast<_Float16*>(base);
+  _Float16* k16 = reinterpret_cast<_Float16*>(base + align_up(qn * 2, A));
+  _Float16* v16 = reinterpret_cast<_Float16*>(reinterpret_cast<char*>(k16) + align_up(kvn * 2, A));
+  _Float16* o16 = reinterpret_cast<_Float16*>(reinterpret_cast<char*>(v16) + align_up(kvn * 2, A));
+  hipLaunchKernelGGL(to_f16_kernel, dim3(grid_for(qn / 4)), dim3(256), 0, st, q, q16, (long long)(qn / 4),
+                     scaling * 1.4426950408889634f);
+  hipLaunchKernelGGL(to_f16_kernel, dim3(grid_for(kvn / 4)), dim3(256), 0, st, k, k16, (long long)(kvn / 4), 1.0f);
+  hipLaunchKernelGGL(to_f16_kernel, dim3(grid_for(kvn / 4)), dim3(256), 0, st, v, v16, (long long)(kvn / 4), 1.0f);
+  int rc = check_launch();
+  if (rc) return rc;
+  for (int b = 0; b < batch; ++b) {
+    PrefillArgs a;
+    memset(&a, 0, sizeof(a));
+    a.q16 = q16 + (size_t)b * qh * seq * kD;
+    a.kcache = reinterpret_cast<uint16_t*>(k16 + (size_t)b * kvh * seq * kD);
+    a.vcache = reinterpret_cast<uint16_t*>(v16 + (size_t)b * kvh * seq * kD);
+    a.out = o16;
+    a.n = seq;
+    a.p0 = 0;
+    a.qh = qh;
+    a.kvh = kvh;
+    a.max_ctx = seq;
+    if ((rc = launch_prefill_attention(a, st))) return rc;
+    const long long n4 = (long long)qh * seq * (kD / 4);
+    hipLaunchKernelGGL(attn_out_kernel, dim3(grid_for(n4)), dim3(256), 0, st, o16, out + (size_t)b * qh * seq * kD,
+                       seq, qh);
+    if ((rc = check_launch())) return rc;
+  }
+  return Q4D_OK;
 }
 
 }  // namespace q4d

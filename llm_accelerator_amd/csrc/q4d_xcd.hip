@@ -44,6 +44,8 @@
 // weight loads (vector loads retire in issue order).
 #include <math.h>
 
+#include <mutex>
+
 #include "q4d_device.h"
 #include "q4d_gemv_dev.h"
 #include "q4d_internal.h"
@@ -571,7 +573,9 @@ __global__ __launch_bounds__(kXThreads) void xcd_attn_kernel(const XcdAttnArgs a
 #pragma unroll
       for (int ii = 0; ii < 16; ++ii) {
         const float ei = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, e), 4 * ii));
-        const h2 v = __builtin_bit_cast(h2, vv[ii]);
+        // rows past pos stand in for absent positions (at pos 0 a row not yet written):
+        // their zero weight must not meet an Inf or NaN bit pattern
+        const h2 v = __builtin_bit_cast(h2, gb + ii <= pos ? vv[ii] : 0u);
         o0 = fmaf(ei, (float)v.x, o0);
         o1 = fmaf(ei, (float)v.y, o1);
       }
@@ -768,7 +772,89 @@ __global__ __launch_bounds__(256) void xcd_finalize_kernel(const float* hx2, con
   *reinterpret_cast<f32x4*>(out + e) = sum_partials(hx2, pd, e);
 }
 
+// Placement probe of the device check: workgroup b of a grid shaped like the XCD-split
+// launches writes 0x100 | the XCC_ID register of the XCD it ran on.  No waits.
+constexpr int kProbeBlocks = kXcdGroups * kXcdBlocks;
+__device__ uint32_t g_xcc_probe[kProbeBlocks];
+
+__global__ __launch_bounds__(64) void xcc_probe_kernel(uint32_t* out) {
+  if (threadIdx.x == 0) out[blockIdx.x] = 0x100u | xcc_id();
+}
+
+template <int NPT>
+bool attn_kernels_fit(int dev) {
+  const void* fns[3] = {reinterpret_cast<const void*>(&xcd_attn_kernel<NPT, 0>),
+                        reinterpret_cast<const void*>(&xcd_attn_kernel<NPT, 1>),
+                        reinterpret_cast<const void*>(&xcd_attn_kernel<NPT, 2>)};
+  (void)dev;
+  for (const void* f : fns) {
+    int n = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, f, kXThreads, 0) != hipSuccess || n < 1) return false;
+  }
+  return true;
+}
+
+// The device facts the XCD-split launches rely on: at least 8 x 32 CUs, one 320-thread
+// workgroup of every launch fits on a CU, and a 256-workgroup grid deals workgroups
+// b, b + 8, b + 16, ... to one XCD, with the 8 residues on 8 different XCDs.
+bool xcd_device_probe(int dev, hipStream_t st) {
+  int cus = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      cus < kXcdGroups * kXcdBlocks)
+    return false;
+  if (!attn_kernels_fit<1>(dev) || !attn_kernels_fit<2>(dev) || !attn_kernels_fit<4>(dev) ||
+      !attn_kernels_fit<8>(dev))
+    return false;
+  int n = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, reinterpret_cast<const void*>(&xcd_mlp_kernel), kXThreads,
+                                                   0) != hipSuccess ||
+      n < 1)
+    return false;
+  void* p = nullptr;
+  if (hipGetSymbolAddress(&p, HIP_SYMBOL(g_xcc_probe)) != hipSuccess || !p) return false;
+  uint32_t* dp = static_cast<uint32_t*>(p);
+  uint32_t h[kProbeBlocks];
+  hipLaunchKernelGGL(xcc_probe_kernel, dim3(kProbeBlocks), dim3(64), 0, st, dp);
+  if (hipGetLastError() != hipSuccess) return false;
+  if (hipMemcpyAsync(h, dp, sizeof(h), hipMemcpyDeviceToHost, st) != hipSuccess) return false;
+  if (hipStreamSynchronize(st) != hipSuccess) return false;
+  unsigned seen = 0;
+  for (int b = 0; b < kProbeBlocks; ++b) {
+    if (!(h[b] & 0x100u) || (h[b] & 0xfu) != (h[b & (kXcdGroups - 1)] & 0xfu)) return false;
+    if (b < kXcdGroups) seen |= 1u << (h[b] & 0xfu);
+  }
+  return __builtin_popcount(seen) == kXcdGroups;
+}
+
 }  // namespace
+
+namespace {
+std::mutex g_check_mu;
+int g_check_mode = 0;                 // 1: report every device as unsuitable
+constexpr int kMaxDevices = 64;
+int8_t g_check_state[kMaxDevices] = {};  // per device: 0 unknown, 1 suitable, -1 not
+}  // namespace
+
+// Per-device answer of xcd_device_probe, found once (not while `st` is being captured
+// into a graph: the probe synchronises; the plan then falls back without caching).
+bool xcd_device_ok(hipStream_t st) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return false;
+  std::lock_guard<std::mutex> lock(g_check_mu);
+  if (g_check_mode == 1) return false;
+  if (g_check_state[dev]) return g_check_state[dev] > 0;
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(st, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) return false;
+  g_check_state[dev] = xcd_device_probe(dev, st) ? 1 : -1;
+  return g_check_state[dev] > 0;
+}
+
+int xcd_set_check_mode(int mode) {
+  std::lock_guard<std::mutex> lock(g_check_mu);
+  const int prev = g_check_mode;
+  g_check_mode = mode;
+  return prev;
+}
 
 int xcd_npt(int max_ctx) {
   const int cm = max(16, (max_ctx + kXcdBlocks - 1) / kXcdBlocks);

@@ -82,6 +82,11 @@ class GreedyDecoder:
         self.hist_count.zero_()
         self.pos.zero_()
         self.position = 0
+        self.ws.reset()
+
+    def plan(self) -> int:
+        """The decode plan the steps run (q4d_decode_plan_active: DECODE_XCD or DECODE_STAGED)."""
+        return int(self._lib.q4d_decode_plan_active(ctypes.byref(self._desc), current_stream()))
 
     def step(self, token: int | None = None, logits: torch.Tensor | None = None, record: bool = True) -> None:
         """One eager step; ``token`` overrides the fed-back id (teacher forcing)."""
@@ -195,14 +200,16 @@ class GreedyDecoder:
         return g
 
     def history(self) -> tuple[list[int], list[float]]:
+        """Generated ids and their logits so far.  Raises Q4DecError(Q4D_ERR_STATUS) when
+        the device status word reports a failed step (the history is then not valid)."""
+        st = self.status()
+        if st:
+            _lib.check_status(st, "GreedyDecoder")
         c = int(self.hist_count.item())
         return self.hist_tok[:c].tolist(), self.hist_score[:c].tolist()
 
     def status(self) -> int:
-        out = ctypes.c_int32(0)
-        check(self._lib.q4d_read_status(self.ws.ptr, self.ws.nbytes, ctypes.byref(self._desc), 1, ctypes.byref(out),
-                                        current_stream()), "q4d_read_status")
-        return out.value
+        return self.ws.status()
 
 
 class Prefill:
@@ -298,7 +305,4 @@ class BatchedDecoder:
         return self.next_tok, self.score
 
     def status(self) -> int:
-        out = ctypes.c_int32(0)
-        check(_lib.load().q4d_read_status(self.ws.ptr, self.ws.nbytes, ctypes.byref(self._desc), self.batch,
-                                          ctypes.byref(out), current_stream()), "q4d_read_status")
-        return out.value
+        return self.ws.status()

@@ -311,12 +311,32 @@ class Workspace:
             raise _lib.Q4DecError(-11, "q4d_workspace_bytes")
         self.buf = torch.empty(self.nbytes, dtype=torch.uint8, device=model.device)
         self.batch = batch
-        _lib.check(lib.q4d_workspace_init(self.buf.data_ptr(), self.nbytes, ctypes.byref(desc), batch,
-                                          current_stream()), "q4d_workspace_init")
+        self._desc = desc
+        self.reset()
 
     @property
     def ptr(self) -> int:
         return self.buf.data_ptr()
+
+    def reset(self) -> None:
+        """Zero the status word, counters and exchange flags (q4d_workspace_init)."""
+        _lib.check(_lib.load().q4d_workspace_init(self.buf.data_ptr(), self.nbytes, ctypes.byref(self._desc),
+                                                  self.batch, current_stream()), "q4d_workspace_init")
+
+    def status(self) -> int:
+        """The device status word (Q4D_STATUS_* bits; synchronises the stream)."""
+        out = ctypes.c_int32(0)
+        _lib.check(_lib.load().q4d_read_status(self.buf.data_ptr(), self.nbytes, ctypes.byref(self._desc),
+                                               self.batch, ctypes.byref(out), current_stream()), "q4d_read_status")
+        return out.value
+
+    def raise_for_status(self, what: str) -> None:
+        """Raise Q4DecError(Q4D_ERR_STATUS) if the status word has a bit set; the
+        workspace is reset first, so the next call starts from a clean state."""
+        st = self.status()
+        if st:
+            self.reset()
+            _lib.check_status(st, what)
 
 
 def current_stream() -> int:

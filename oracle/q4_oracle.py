@@ -29,7 +29,7 @@ __all__ = [
     "lm_head_streamed_argmax_q26",
     "manual_rms_norm", "manual_linear_from_weight", "rope_inv_freq",
     "manual_rope_cos_sin", "manual_rotate_half", "manual_apply_rope",
-    "manual_repeat_kv", "softmax", "silu", "manual_cached_attention",
+    "manual_repeat_kv", "softmax", "silu", "manual_cached_attention", "manual_causal_attention",
     "OracleConfig", "OracleLayer", "OracleModel", "manual_decoder_layer_cached",
     "embed_tokens", "final_logits", "run_manual_one_token", "greedy_decode",
     "serial_prompt_all_at_once",
@@ -323,6 +323,19 @@ def manual_cached_attention(q: np.ndarray, k_rep: np.ndarray, v_rep: np.ndarray,
     dt = q.dtype.type
     scores = (q @ np.swapaxes(k_rep, 2, 3)) * dt(scaling)
     w = softmax(scores.astype(dt), axis=-1).astype(dt)
+    return (w @ v_rep).astype(dt), w
+
+
+def manual_causal_attention(q: np.ndarray, k_rep: np.ndarray, v_rep: np.ndarray, scaling: float):
+    """``softmax(q @ k.T * scaling)`` with keys after the query position filled with
+    the dtype's most negative finite value, then ``@ v`` (``pem/common.py:201-216``).
+    q, k/v: [B, H, S, D] (k/v already repeated); returns ``(output, weights)``."""
+    dt = q.dtype.type
+    scores = (q @ np.swapaxes(k_rep, 2, 3)) * dt(scaling)
+    s = scores.shape[-1]
+    future = np.triu(np.ones((s, s), dtype=bool), k=1)
+    scores = np.where(future[None, None], np.finfo(dt).min, scores).astype(dt)
+    w = softmax(scores, axis=-1).astype(dt)
     return (w @ v_rep).astype(dt), w
 
 
@@ -621,6 +634,8 @@ PINS = {
                                                               "apply_rotary_pos_emb; norm preservation; "
                                                               "relative-position invariance",
     "manual_cached_attention": "torch scaled_dot_product_attention with enable_gqa; brute force",
+    "manual_causal_attention": "torch scaled_dot_product_attention(is_causal=True, enable_gqa); every query row "
+                               "equals manual_cached_attention over keys 0..i; planted off-by-one masks fail",
     "manual_decoder_layer_cached / run_manual_one_token": "transformers Qwen3ForCausalLM (eager, fp32) "
                                                           "loaded with the same dequantised weights",
     "serial_prompt_all_at_once": "the one-token serial loop (run_manual_one_token) on the same prompts, every "

@@ -65,3 +65,26 @@ def report(name, got, ref):
     rel = mx / max(float(np.abs(ref).max()), 1e-30)
     print(f"[{name}] max_abs_err={mx:.3e} rel_err={rel:.3e} max|ref|={float(np.abs(ref).max()):.3e}", flush=True)
     return mx, rel
+
+
+PLANS = [("xcd", 0, 2), ("staged", 1, 2), ("staged-fp16", 1, 1)]   # (id, decode plan, activation precision)
+
+
+class decode_plan:
+    """Run a block under one batch-1 decode plan and activation precision, restoring
+    the previous plan and precision 2 afterwards."""
+
+    def __init__(self, plan: int, precision: int = 2):
+        self.plan, self.precision = plan, precision
+
+    def __enter__(self):
+        lib = _lib.load()
+        self.prev = lib.q4d_set_decode_plan(self.plan)
+        check(lib.q4d_set_activation_precision(self.precision), "q4d_set_activation_precision")
+        return self
+
+    def __exit__(self, *exc):
+        lib = _lib.load()
+        lib.q4d_set_decode_plan(self.prev)
+        check(lib.q4d_set_activation_precision(2), "q4d_set_activation_precision")
+        return False

@@ -17,6 +17,7 @@ import ctypes
 import pytest
 import torch
 
+from gpu_helpers import PLANS, decode_plan
 from llm_accelerator_amd import _lib
 from llm_accelerator_amd._lib import check
 from llm_accelerator_amd.model import (KVCache, Qwen3Config, Workspace, build_model, current_stream,
@@ -25,6 +26,15 @@ from llm_accelerator_amd.model import (KVCache, Qwen3Config, Workspace, build_mo
 pytestmark = pytest.mark.gpu
 
 LAYERS, VOCAB, CTX = 2, 2048, 256
+
+
+@pytest.fixture(params=PLANS, ids=[p[0] for p in PLANS])
+def plan(request):
+    """Each test runs under the XCD-split plan, the staged plan and the staged plan with
+    fp16 activations (the separate launches and the folded step use the same plan)."""
+    _, pl, prec = request.param
+    with decode_plan(pl, prec):
+        yield pl
 
 
 @pytest.fixture(scope="module")
@@ -117,14 +127,14 @@ def _cache(cfg, model, upto, seed, dev):
     return kv.data
 
 
-def test_feedback_step_equals_separate_launches(dev, small):
+def test_feedback_step_equals_separate_launches(dev, small, plan):
     cfg, model = small
     p0, steps = 40, 6
     kv0 = _cache(cfg, model, p0, 11, dev)
     loops = {k: Loop(cfg, model, kv0, 321, p0, cap=3) for k in ("separate", "plain", "feedback")}
     for i in range(steps):
         record = i > 0          # the first step records nothing, then 5 recorded steps into capacity 3
-        print(f"[feedback] step {i} position {p0 + i} record={record}", flush=True)
+        print(f"[feedback] plan {plan} step {i} position {p0 + i} record={record}", flush=True)
         for k, lp in loops.items():
             getattr(lp, k)(record)
         ref = loops["separate"].state()
@@ -139,7 +149,7 @@ def test_feedback_step_equals_separate_launches(dev, small):
         assert lp.status() == 0
 
 
-def test_feedback_bad_token_sets_status_and_zero_embedding(dev, small):
+def test_feedback_bad_token_sets_status_and_zero_embedding(dev, small, plan):
     cfg, model = small
     p0 = 17
     kv0 = _cache(cfg, model, p0, 12, dev)

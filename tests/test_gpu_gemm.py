@@ -400,3 +400,120 @@ def test_decode_batch_64_sequences_4096_positions(dev, batch_long_setup):
         assert not kv.data[:, :, b, :, p + 1:].any(), (b, p)
     print(f"[decode batch long] B={B} max rel logit err={worst:.3e} near_ties={near}", flush=True)
     assert worst < 5e-3
+
+
+FULL_B, FULL_P = 64, 4096   # the batched-decode benchmark: 64 sequences, 4096 cached positions each
+
+
+@pytest.mark.slow
+def test_decode_batch_full_model_64x4096(dev, qwen3_full):
+    """The batched-decode benchmark's workload at full size, under a check: 64
+    sequences, each with a 4096-position fp16 cache of N(0,1) values (the same
+    generator, seed and token draw as the benchmark), one step through all 28 layers
+    and the 151936-row batched LM head with its per-row argmax over 1187 block
+    partials.  Per sequence that is run_manual_one_token
+    (10_validate_full_run_one_token.py:17-56) at position 4096; every sequence's token
+    is the lowest-index argmax of its logits, and 8 sequences spread over the batch are
+    compared with the oracle (logits, token up to a reported near-tie, the K/V rows
+    appended at position 4096 in layers 0, 1, 13 and 27)."""
+    cfg, host, om = qwen3_full
+    L = cfg.num_hidden_layers
+    model = build_model(cfg, host, max_ctx=FULL_P + 1, device=dev)
+    print(f"[decode batch full] {FULL_B} x {FULL_P}: filling 28-layer caches", flush=True)
+    gen = torch.Generator(device=dev).manual_seed(5)
+    kv = KVCache(cfg, L, FULL_B, FULL_P + 1, dev)
+    kv.data[..., :FULL_P, :].normal_(generator=gen)
+    pre_slot = kv.data[..., FULL_P, :].clone()
+    assert not pre_slot.any()
+    tokens = np.random.default_rng(3).integers(0, cfg.vocab_size, FULL_B).astype(np.int32)
+    dec = BatchedDecoder(model, FULL_B, kv)
+    logits = torch.empty((FULL_B, cfg.vocab_size), dtype=torch.float32, device=dev)
+    nt, sc = dec.step(torch.from_numpy(tokens).to(dev), torch.full((FULL_B,), FULL_P, dtype=torch.int32, device=dev),
+                      logits)
+    torch.cuda.synchronize()
+    assert dec.status() == 0
+    nt, sc, lg = nt.cpu().numpy(), sc.cpu().numpy(), logits.cpu().numpy()
+    for b in range(FULL_B):
+        first = int(np.argmax(lg[b]))
+        assert nt[b] == first and sc[b] == lg[b, first], (b, int(nt[b]), first)
+    print("[decode batch full] comparing 8 sequences with the oracle", flush=True)
+    worst, near = 0.0, []
+    for b in range(0, FULL_B, 9):
+        kc = [kv.data[li, 0, b, :, :FULL_P].float().cpu().numpy()[None] for li in range(L)]
+        vc = [kv.data[li, 1, b, :, :FULL_P].float().cpu().numpy()[None] for li in range(L)]
+        rl, rt = o.run_manual_one_token(np.array([[int(tokens[b])]]), FULL_P, om, kc, vc, kv_store_dtype=np.float16)
+        r = rl[0, -1].astype(np.float64)
+        err = np.abs(lg[b].astype(np.float64) - r)
+        rel = float(err.max() / np.abs(r).max())
+        worst = max(worst, rel)
+        if nt[b] != rt[0, 0]:
+            gap = r[rt[0, 0]] - r[nt[b]]
+            assert gap <= err[rt[0, 0]] + err[nt[b]], (b, gap)
+            near.append((b, int(rt[0, 0]), int(nt[b]), float(gap)))
+        for li in (0, 1, 13, 27):
+            for kind, ref_c in ((0, kc[li]), (1, vc[li])):
+                want = ref_c[0, :, FULL_P].astype(np.float64)
+                got = kv.data[li, kind, b, :, FULL_P].float().cpu().numpy()
+                assert np.all(np.abs(got - want) <= 2e-2 * np.abs(want).max(axis=-1, keepdims=True)), (b, li, kind)
+        print(f"[decode batch full] seq {b}: token {int(nt[b])} (oracle {int(rt[0, 0])}), max rel logit err "
+              f"{rel:.3e}", flush=True)
+        del kc, vc
+    print(f"[decode batch full] worst rel logit err={worst:.3e} near_ties={near}", flush=True)
+    assert worst < 5e-3
+    # the step wrote position 4096 of every sequence and layer, and nothing else changed
+    assert kv.data[..., FULL_P, :].abs().amax(dim=-1).gt(0).all()
+
+
+@pytest.mark.slow
+def test_lm_head_batch_full_vocab_64_rows_ties(dev):
+    """The batched LM head at the benchmark's size (151936 rows, 64 sequences): planted
+    winners and exact duplicates of them across the last 128-row blocks, block pairs in
+    the middle and the first/last row resolve to the lower index, and every row's token
+    is the first maximum of its logits (logits against the float64 product of the fp16
+    operands)."""
+    rng = np.random.default_rng(151936)
+    V, H, B = 151936, 1024, 64
+    print(f"[lm head full] {V} x {H}, {B} rows: building the table", flush=True)
+    packed = rng.integers(0, 256, size=(V, H // 2), dtype=np.uint8)
+    scale = rng.integers(100, 400, size=(V, H // 64)).astype(np.uint16)
+    hidden = rng.normal(size=(B, H)).astype(np.float32)
+    gamma = np.ones(H, dtype=np.float32)
+    xn = o.manual_rms_norm(hidden.astype(np.float64), gamma, 1e-6, np.float64)
+    # (winner, duplicate) rows, 128 distinct rows: inside the last 128-row block (1186:
+    # rows 151808..151935), from block 1185 into 1186, across 128-row block edges in the
+    # middle, the first rows against the last ones, and across 64-row tile edges
+    pairs = []
+    for i in range(8):
+        pairs.append((151808 + 4 * i, 151810 + 4 * i))
+    for i in range(8):
+        pairs.append((151680 + 4 * i, 151873 + 4 * i))
+    for i in range(16):
+        k = 500 + 2 * i
+        pairs.append((128 * k + 127, 128 * (k + 1)))
+    for i in range(16):
+        pairs.append((i, 151935 - i))
+    for i in range(16):
+        w = 10000 + 1000 * i + 63
+        pairs.append((w, w + 65))
+    assert len({r for pr in pairs for r in pr}) == 2 * B
+    for b, (wi, di) in enumerate(pairs):
+        sgn = np.sign(xn[b]).astype(np.int64)
+        qrow = np.where(sgn >= 0, 7, -8) * (sgn != 0)
+        packed[wi] = o.pack_signed_int4(qrow[None])[0]
+        scale[wi] = 400
+        packed[di] = packed[wi]
+        scale[di] = scale[wi]
+    tok, score, logits = lm_head_batch(q4(packed, scale), torch.from_numpy(hidden).to(dev),
+                                       torch.from_numpy(gamma).to(dev))
+    for b, (wi, di) in enumerate(pairs):
+        first = int(np.argmax(logits[b]))
+        assert tok[b] == first and score[b] == logits[b, first], (b, tok[b], first)
+        # the planted pair is an exact tie and the lower index wins
+        assert logits[b, wi] == logits[b, di] and tok[b] == wi, (b, int(tok[b]), wi, di)
+    print("[lm head full] float64 reference", flush=True)
+    x16 = xn.astype(np.float16).astype(np.float64)
+    for r0 in range(0, V, 16384):
+        w16 = w16_of(packed[r0:r0 + 16384], scale[r0:r0 + 16384], H).astype(np.float64)
+        ref = x16 @ w16.T
+        bound = np.abs(x16) @ np.abs(o.dequantize_q4(packed[r0:r0 + 16384], scale[r0:r0 + 16384], np.float64)).T
+        assert np.all(np.abs(logits[:, r0:r0 + 16384] - ref) <= 2.0 ** -10 * bound), r0

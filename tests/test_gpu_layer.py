@@ -79,9 +79,16 @@ def test_decoder_layer_config2(dev, layer_setup, precision, tol, plan):
     lib = _lib.load()
     prev = lib.q4d_set_decode_plan(plan)
     try:
+        check(lib.q4d_set_activation_precision(precision), "set precision")
+        active = lib.q4d_decode_plan_active(ctypes.byref(model.descriptor()), current_stream())
+        check(lib.q4d_set_activation_precision(2), "set precision")
         out, knew, vnew = _run_gpu_layer(cfg, model, kv_k, kv_v, hidden, precision, dev)
     finally:
         lib.q4d_set_decode_plan(prev)
+    # an MI355X passes the XCD-split plan's device check, so the xcd case runs that plan
+    assert active == plan, (active, plan)
+    # the drop-in raised on a status bit; read the word explicitly as well
+    assert common.runtime(model).ws.status() == 0
     ref, kc, vc = _oracle_layer(om64, kv_k, kv_v, hidden, np.float16)
     mx, rel = report(f"layer mode{precision} vs fp16-KV oracle", out, ref)
     assert rel <= tol
@@ -224,8 +231,13 @@ def test_attention_context_lengths_and_batch(dev, lengths):
         assert mx <= 2e-6 * max(1.0, float(np.abs(ref).max())) + 1e-6, (n, mx)
 
 
-@pytest.mark.parametrize("plan,max_ctx", [(0, 4096), (0, 2048), (1, 4097)], ids=["xcd-4096", "xcd-2048", "staged-4097"])
-@pytest.mark.parametrize("position", [1024, 1151, 2047, 4095])
+LONG_CASES = [(plan, cap, pos) for plan, cap, name in ((0, 4096, "xcd-4096"), (0, 2048, "xcd-2048"),
+                                                       (1, 4097, "staged-4097"))
+              for pos in (1024, 1151, 2047, 4095) if pos < cap]
+LONG_IDS = [f"{'xcd' if p == 0 else 'staged'}-{c}-{q}" for p, c, q in LONG_CASES]
+
+
+@pytest.mark.parametrize("plan,max_ctx,position", LONG_CASES, ids=LONG_IDS)
 def test_decoder_layer_long_context(dev, layer_setup, position, plan, max_ctx):
     """Batch-1 decode layer past 1024 cached positions against the fp16-KV oracle at
     the layer-test bar, for both kernel plans: the XCD-split layer at a capacity of
@@ -235,8 +247,6 @@ def test_decoder_layer_long_context(dev, layer_setup, position, plan, max_ctx):
     batches of eight)."""
     from llm_accelerator_amd.model import with_context
     cfg, model, om64, _, _, _, hidden = layer_setup
-    if position >= max_ctx:
-        pytest.skip("position beyond the capacity")
     m = with_context(model, max_ctx)
     rng = np.random.default_rng(position)
     kv_k = rng.normal(size=(1, 8, position, 128)).astype(np.float16)
@@ -273,11 +283,16 @@ def test_decoder_layer_long_context(dev, layer_setup, position, plan, max_ctx):
         assert np.all(np.abs(got - want) <= ulp_row), kind
 
 
-@pytest.mark.parametrize("position", [0, 63, 64, 200, 511])
-def test_decoder_layer_64_position_chunks(dev, layer_setup, position):
-    """A context capacity of 512 positions splits batch-1 attention into 64-position
-    chunks (at most 8, merged by the o_proj prologue in one batch of loads); chunk
-    edges and the last slot against the fp16-KV oracle at the layer-test bar."""
+@pytest.mark.parametrize("plan", [0, 1], ids=["xcd", "staged"])
+@pytest.mark.parametrize("position", [0, 1, 63, 64, 200, 511])
+def test_decoder_layer_64_position_chunks(dev, layer_setup, position, plan):
+    """A context capacity of 512 positions: the staged plan splits batch-1 attention
+    into 64-position chunks (at most 8, merged by the o_proj prologue in one batch of
+    loads), the XCD-split plan gives each of an XCD's 32 workgroups one group of 16
+    positions; chunk edges and the last slot against the fp16-KV oracle at the
+    layer-test bar.  The cache rows at and past the position hold NaN bit patterns
+    (rows never written): they stand in for absent positions in the kernels' loads
+    and must not reach the output."""
     from llm_accelerator_amd.model import with_context
     cfg, model, om64, _, _, _, hidden = layer_setup
     m = with_context(model, 512)
@@ -285,6 +300,7 @@ def test_decoder_layer_64_position_chunks(dev, layer_setup, position):
     kv_k = rng.normal(size=(1, 8, position, 128)).astype(np.float16)
     kv_v = rng.normal(size=(1, 8, position, 128)).astype(np.float16)
     kv = KVCache(cfg, 1, 1, m.max_ctx, dev)
+    kv.data.fill_(float("nan"))
     kv.data[0, 0, 0, :, :position] = torch.from_numpy(kv_k[0]).to(dev)
     kv.data[0, 1, 0, :, :position] = torch.from_numpy(kv_v[0]).to(dev)
     lib = _lib.load()
@@ -294,9 +310,19 @@ def test_decoder_layer_64_position_chunks(dev, layer_setup, position):
     h = torch.from_numpy(hidden.reshape(1, 1024)).to(dev)
     out = torch.empty_like(h)
     pos = torch.tensor([position], dtype=torch.int32, device=dev)
-    print(f"[layer 64-position chunks] position={position}", flush=True)
-    check(lib.q4d_decoder_layer(ctypes.byref(desc), 0, h.data_ptr(), out.data_ptr(), ctypes.byref(kvd),
-                                pos.data_ptr(), ws.data_ptr(), ws.numel(), current_stream()), "q4d_decoder_layer")
+    print(f"[layer 64-position chunks] plan={plan} position={position}", flush=True)
+    prev = lib.q4d_set_decode_plan(plan)
+    try:
+        assert lib.q4d_decode_plan_active(ctypes.byref(desc), current_stream()) == plan
+        check(lib.q4d_decoder_layer(ctypes.byref(desc), 0, h.data_ptr(), out.data_ptr(), ctypes.byref(kvd),
+                                    pos.data_ptr(), ws.data_ptr(), ws.numel(), current_stream()), "q4d_decoder_layer")
+    finally:
+        lib.q4d_set_decode_plan(prev)
+    st = ctypes.c_int32(0)
+    check(lib.q4d_read_status(ws.data_ptr(), ws.numel(), ctypes.byref(desc), 1, ctypes.byref(st), current_stream()),
+          "q4d_read_status")
+    assert st.value == 0
+    assert torch.isfinite(out).all()
     ref, kc, vc = o.manual_decoder_layer_cached(hidden.astype(np.float64), om64.layers[0], om64.config, om64.inv_freq,
                                                 np.array([[position]]),
                                                 kv_k.astype(np.float64) if position else None,

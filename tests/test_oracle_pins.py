@@ -175,6 +175,55 @@ def test_attention_matches_torch_sdpa_gqa():
         np.testing.assert_allclose(out2[:, h], single[:, 0], rtol=1e-12, atol=1e-14)
 
 
+def _causal_vs_sdpa(q, k, v, scale):
+    out, w = o.manual_causal_attention(q, o.manual_repeat_kv(k, q.shape[1] // k.shape[1]),
+                                       o.manual_repeat_kv(v, q.shape[1] // k.shape[1]), scale)
+    ref = torch.nn.functional.scaled_dot_product_attention(torch.from_numpy(q), torch.from_numpy(k),
+                                                           torch.from_numpy(v), is_causal=True, scale=scale,
+                                                           enable_gqa=True)
+    return out, w, ref.numpy()
+
+
+def test_causal_attention_matches_sdpa_and_the_cached_prefixes():
+    """manual_causal_attention (common.py:201-216) against torch's causal SDPA with GQA,
+    and row i against manual_cached_attention over keys 0..i (the serial prompt loop
+    sees exactly those keys at step i)."""
+    rng = np.random.default_rng(17)
+    for b, qh, kvh, s in ((1, 16, 8, 37), (2, 4, 1, 5), (1, 2, 2, 1)):
+        q = rng.normal(size=(b, qh, s, 128))
+        k = rng.normal(size=(b, kvh, s, 128))
+        v = rng.normal(size=(b, kvh, s, 128))
+        out, w, ref = _causal_vs_sdpa(q, k, v, 128 ** -0.5)
+        np.testing.assert_allclose(out, ref, rtol=1e-10, atol=1e-12)
+        np.testing.assert_allclose(w.sum(-1), 1.0, rtol=1e-12)
+        assert np.all(np.triu(w[0, 0], k=1) == 0)
+        rep = qh // kvh
+        for i in range(s):
+            cached, _ = o.manual_cached_attention(q[:, :, i:i + 1], o.manual_repeat_kv(k[:, :, :i + 1], rep),
+                                                  o.manual_repeat_kv(v[:, :, :i + 1], rep), 128 ** -0.5)
+            np.testing.assert_allclose(out[:, :, i:i + 1], cached, rtol=1e-10, atol=1e-12)
+
+
+@pytest.mark.parametrize("offset", [0, 2])
+def test_causal_attention_planted_mask_errors_fail(monkeypatch, offset):
+    """A mask that hides the query's own key (offset 0) or shows the next key
+    (offset 2) in the oracle no longer matches the causal SDPA."""
+    import oracle.q4_oracle as qo
+
+    class _Np:
+        def __getattr__(self, name):
+            return getattr(np, name)
+
+        @staticmethod
+        def triu(m, k=0):
+            return np.triu(m, k=offset)
+    monkeypatch.setattr(qo, "np", _Np())
+    rng = np.random.default_rng(18)
+    q, k, v = (rng.normal(size=(1, 2, 9, 128)) for _ in range(3))
+    out, _, ref = _causal_vs_sdpa(q, k, v, 128 ** -0.5)
+    assert not np.allclose(out, ref, rtol=1e-6, atol=1e-8)
+
+
 def _small_q4_model(layers=2, vocab=1024, seed=11):
     from llm_accelerator_amd.model import Qwen3Config, random_host_weights
     cfg = Qwen3Config(num_hidden_layers=layers, vocab_size=vocab)

@@ -14,6 +14,7 @@ import numpy as np
 import pytest
 import torch
 
+from gpu_helpers import PLANS, decode_plan
 from llm_accelerator_amd import _lib
 from llm_accelerator_amd._lib import check
 from llm_accelerator_amd.model import (KVCache, Qwen3Config, Workspace, build_model, current_stream,
@@ -57,17 +58,19 @@ def _filled_cache(cfg, model, upto, seed, dev):
     return kv
 
 
-def test_noalloc_equals_workspace_path_twice(dev, small):
+@pytest.mark.parametrize("plan_id,plan,precision", PLANS, ids=[p[0] for p in PLANS])
+def test_noalloc_equals_workspace_path_twice(dev, small, plan_id, plan, precision):
     cfg, model = small
     lib = _lib.load()
     status = torch.zeros(1, dtype=torch.int32, device=dev)
     for m, position, token, seed in ((model, 700, 1234, 1), (with_context(model, 256), 100, 77, 2)):
-        print(f"[noalloc] max_ctx={m.max_ctx} position={position}", flush=True)
+        print(f"[noalloc] plan {plan_id} max_ctx={m.max_ctx} position={position}", flush=True)
         kv_ref = _filled_cache(cfg, m, position, seed, dev)
         kv_got = KVCache(cfg, 2, 1, m.max_ctx, dev)
         kv_got.data.copy_(kv_ref.data)
-        ref = _step(lib, m, kv_ref, token, position, noalloc=False)
-        got = _step(lib, m, kv_got, token, position, noalloc=True, status=status)
+        with decode_plan(plan, precision):
+            ref = _step(lib, m, kv_ref, token, position, noalloc=False)
+            got = _step(lib, m, kv_got, token, position, noalloc=True, status=status)
         for r, g in zip(ref, got):
             assert torch.equal(r, g)
         assert torch.equal(kv_ref.data, kv_got.data)
