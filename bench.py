@@ -58,6 +58,9 @@ METRIC = "Q4 GEMV HBM GB/s (% peak) + batch-1 decode tok/s, Qwen3-0.6B-Q4"
 HBM_PEAK_GBPS = 8000.0
 MFMA_PEAK_TFLOPS = 2500.0  # dense fp16
 GEMV_ROWS, GEMV_COLS = 3072, 1024
+GEMV_WARM_S = 0.3        # sustained GEMV launches before the timed regions (clock ramp)
+GEMV_TIMED_S = 0.1       # target GPU time of the timed regions together
+GEMV_MIN_REPLAYS = 11    # timed regions of --steps launches at least (median reported)
 PROMPT = 64
 PREFILL_TOKENS = 2048              # prefill of one 2048-token sequence
 BATCH_SEQS, BATCH_CTX = 64, 4096  # batched decode: 64 sequences over 4096 cached positions
@@ -85,13 +88,17 @@ def parse():
     ap.add_argument("--no-extras", action="store_true", help="run the GEMV headline only")
     ap.add_argument("--legs", default="decode,lm,layer,prefill,batch,fx,q4c",
                     help="comma list of the legs beside the GEMV headline: decode (28-layer decode), "
-                         "lm (LM head alone), "
+                         "lm (LM head alone), lmsweep (LM head over 4096..151936 rows, not by default), "
                          "layer (one decoder layer at --ctx), prefill, batch (batched decode), "
                          "fx fixed-point (RTL-exact) layer and token, q4c float -> Q4 conversion of the model")
     ap.add_argument("--extras", dest="legs", default=argparse.SUPPRESS, help="the same as --legs")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--decode-gen", type=int, default=256)
+    ap.add_argument("--gemv-replays", type=int, default=0,
+                    help="timed regions of --steps GEMV launches (0: enough for ~0.1 s, 11..200)")
+    ap.add_argument("--gemv-warm-s", type=float, default=GEMV_WARM_S,
+                    help="seconds of sustained GEMV launches before the timed regions")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run a plain 256 MiB device copy (scales FETCH_SIZE/WRITE_SIZE counters)")
     return ap.parse_args()
@@ -161,20 +168,34 @@ def leg_gemv(args, lib, torch, np, dev, st):
     if g_rest is not None:
         g_rest.replay()
     timed = [g_rot] * full + ([g_rest] if g_rest is not None else [])
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    # the GPU leaves its idle clocks only under sustained load: ~0.3 s of the same launches
+    # first, whatever --warmup asks (a cold start read 18 % slower at --steps 20 --warmup 5)
+    t_w = time.perf_counter()
+    while time.perf_counter() - t_w < args.gemv_warm_s:
+        g_rot.replay()
+        torch.cuda.synchronize()
+    # the K timed steps, as REPLAYS separate timed regions; before each, an untimed full
+    # rotation (200 copies, 336 MB > the 256 MB cache) evicts the copies the region reads
+    # and keeps the GPU busy, so the region starts right after it on a warm device
+    reps = args.gemv_replays or max(GEMV_MIN_REPLAYS, min(200, int(GEMV_TIMED_S * 1e6 / (2.0 * args.steps))))
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    g_rot.replay()                # lead-in, untimed
-    e0.record()
-    for g in timed:
-        g.replay()
-    e1.record()
+    for e0, e1 in ev:
+        g_rot.replay()                # lead-in, untimed
+        e0.record()
+        for g in timed:
+            g.replay()
+        e1.record()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    us = e0.elapsed_time(e1) * 1e3 / args.steps
+    per = sorted(e0.elapsed_time(e1) * 1e3 / args.steps for e0, e1 in ev)
+    us = per[len(per) // 2]
+    spread = {"replays": reps, "min": round(per[0], 3), "p25": round(per[len(per) // 4], 3),
+              "median": round(us, 3), "p75": round(per[(3 * len(per)) // 4], 3), "max": round(per[-1], 3)}
     ok = bool(torch.isfinite(y.float()).all().item())
-    log(f"[bench] GEMV 3072x1024 flushed: {us:.3f} us/launch over {args.steps} launches, "
-        f"{gb / us / 1e3:.1f} GB/s (wall incl. lead-in {wall * 1e3:.2f} ms)")
+    log(f"[bench] GEMV 3072x1024 flushed: {us:.3f} us/launch (median of {reps} timed regions of {args.steps} "
+        f"launches; spread {spread}), {gb / us / 1e3:.1f} GB/s (wall incl. lead-ins {wall * 1e3:.2f} ms)")
 
     g_res = graph_of(lambda i: launch(mats[0]), ncop, torch)
     g_res.replay()
@@ -183,7 +204,7 @@ def leg_gemv(args, lib, torch, np, dev, st):
     g_tiny.replay()
     us_floor = time_graph(g_tiny, max(2, args.steps // ncop), torch) / ncop * 1e3
     log(f"[bench] GEMV resident {us_res:.3f} us, single-launch floor (2x1024) {us_floor:.3f} us")
-    out = {"us": us, "GBps": gb / us / 1e3, "bytes": gb, "wall_s": wall, "finite": ok,
+    out = {"us": us, "GBps": gb / us / 1e3, "bytes": gb, "wall_s": wall, "finite": ok, "spread": spread,
            "resident_us": us_res, "resident_GBps": gb / us_res / 1e3, "floor_us": us_floor}
     del P, S, g_rot, g_rest, g_res, g_tiny, tiny
     torch.cuda.empty_cache()
@@ -245,6 +266,12 @@ def leg_layer(args, lib, torch, dev, st):
            "stage_us_flushed": {k: round(v, 3) for k, v in stage_us.items()},
            "stage_GBps": {k: round(stage_bytes[k] / stage_us[k] / 1e3, 1) for k in stage_names},
            "stage_kernels": STAGE_KERNELS}
+    xj = load_json("decode_xcd_layer_hbm_traffic.json")
+    if xj and ctx == 512 and args.precision == 2:
+        # the plan flushed_us times: counter-measured HBM bytes of its two launches
+        out["traffic_bytes"] = {k: v["total_bytes"] for k, v in xj["launches"].items()}
+        out["traffic_algorithmic_bytes"] = {k: v["algorithmic_bytes"] for k, v in xj["launches"].items()}
+        out["traffic_source"] = xj["source"]
     tj = load_json("decode_layer_ctx512_hbm_traffic.json")
     if tj and ctx == 512 and args.precision == 2:
         out["stage_traffic_bytes"] = {k: v["total_bytes"] for k, v in tj["stages"].items()}
@@ -421,6 +448,61 @@ def leg_lm(lib, torch, dev, st, fmodel):
     del copies, descs, lws, g_fl, g_rp
     torch.cuda.empty_cache()
     return lm
+
+
+def leg_lmsweep(lib, torch, dev, st, fmodel, np):
+    """The LM head (final RMSNorm + Q4 GEMV + argmax) over the first R rows of the
+    table for several R, flushed (rotating over 4 copies), and a least-squares line
+    time = fixed + bytes / rate over R >= 32768: the kernel's marginal streaming rate
+    and its fixed cost (prologue, ramp, tail, argmax hand-off)."""
+    from llm_accelerator_amd import model as M
+    from llm_accelerator_amd._lib import Q4dMatrix, Q4dModel, check
+    fcfg = fmodel.config
+    lw = fmodel.lm_head.weight
+    copies = [lw] + [type(lw)(lw.packed.clone(), lw.scale.clone()) for _ in range(3)]
+    base = fmodel.descriptor()
+    gen = torch.Generator(device=dev).manual_seed(3)
+    hid = torch.randn(1, fcfg.hidden_size, generator=gen, device=dev)
+    tok = torch.zeros(1, dtype=torch.int32, device=dev)
+    score = torch.zeros(1, dtype=torch.float32, device=dev)
+    lws = M.Workspace(fmodel, 1)
+    rows_list = [4096, 8192, 16384, 32768, 65536, 98304, 131072, fcfg.vocab_size]
+    pts = []
+    H = fcfg.hidden_size
+    for R in rows_list:
+        # every disjoint R-row window of the 4 tables (331 MB > the 256 MB cache for each R),
+        # in turn: each launch reads rows no launch has read since they left the cache
+        descs = []
+        for j in range(fcfg.vocab_size // R):
+            for c in copies:
+                d = Q4dModel.from_buffer_copy(base)
+                d.vocab_size = R
+                d.embed_tokens = Q4dMatrix(c.packed.data_ptr() + j * R * (H // 2), c.scale.data_ptr() + j * R * (H // 32),
+                                           R, H)
+                descs.append(d)
+        n = len(descs)
+
+        def lm_head(i, descs=descs):
+            check(lib.q4d_lm_head_argmax(ctypes.byref(descs[i]), hid.data_ptr(), tok.data_ptr(),
+                                         score.data_ptr(), None, lws.ptr, lws.nbytes, st()), "lm_head")
+        g = graph_of(lm_head, n, torch)
+        g.replay()
+        us = time_graph(g, max(2, 80 // n), torch) / n * 1e3
+        nbytes = R * (fcfg.hidden_size // 2 + fcfg.hidden_size // 32) + 4 * fcfg.hidden_size * 2
+        pts.append({"rows": R, "bytes": nbytes, "us": round(us, 3), "GBps": round(nbytes / us / 1e3, 1)})
+        del g, descs
+    big = [p for p in pts if p["rows"] >= 32768]
+    xb = np.array([p["bytes"] for p in big], dtype=np.float64)
+    yt = np.array([p["us"] for p in big], dtype=np.float64)
+    slope, icpt = np.polyfit(xb, yt, 1)
+    out = {"workload": "final RMSNorm + R x 1024 Q4 GEMV + argmax over R-row windows of the table; one graph "
+                       "runs every disjoint R-row window of 4 table copies (331 MB, flushed) in turn",
+           "points": pts,
+           "fit_rows_min": 32768, "marginal_GBps": round(1e-3 / slope, 1), "fixed_us": round(icpt, 3)}
+    log(f"[bench] LM head size sweep: {json.dumps(out)}")
+    del copies, lws
+    torch.cuda.empty_cache()
+    return out
 
 
 # ------------------------------------------------------------------ prefill, batched, fixed point, Q4 conversion
@@ -615,7 +697,7 @@ def main():
     st = lambda: torch.cuda.current_stream().cuda_stream  # noqa: E731
 
     legs = set() if args.no_extras else {x.strip() for x in args.legs.split(",") if x.strip()}
-    known = {"decode", "lm", "layer", "prefill", "batch", "fx", "q4c"}
+    known = {"decode", "lm", "lmsweep", "layer", "prefill", "batch", "fx", "q4c"}
     if legs - known:
         sys.exit(f"unknown legs {sorted(legs - known)}")
 
@@ -626,7 +708,7 @@ def main():
         extras["decoder_layer"] = leg_layer(args, lib, torch, dev, st)
 
     decode = lm = None
-    if legs & {"decode", "lm", "prefill", "batch", "fx"}:
+    if legs & {"decode", "lm", "lmsweep", "prefill", "batch", "fx"}:
         fcfg = M.Qwen3Config()
         t = time.time()
         fhost = M.random_host_weights(fcfg, seed=0)
@@ -640,6 +722,8 @@ def main():
             decode = leg_decode(args, torch, np, M.with_context(fmodel, PROMPT + args.decode_gen + 16))
         if "lm" in legs:
             lm = leg_lm(lib, torch, dev, st, fmodel)
+        if "lmsweep" in legs:
+            extras["lm_head_size_sweep"] = leg_lmsweep(lib, torch, dev, st, fmodel, np)
         if "prefill" in legs:
             extras["prefill_2048"] = leg_prefill(torch, np, dev, fmodel)
         if "batch" in legs:
@@ -679,6 +763,9 @@ def main():
                 "achieved": round(value, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                 "frac": round(value / HBM_PEAK_GBPS, 4), "traffic": None,
                 "bytes_per_launch": gb, "avg_launch_us": round(gemv["us"], 3),
+                "timing": {"method": f"median over {gemv['spread']['replays']} timed regions of exactly "
+                                     f"{args.steps} launches (HIP events), each after an untimed 200-copy rotation",
+                           "us_per_launch": gemv["spread"]},
                 "single_launch_floor_us": round(floor_us, 3),
                 "single_launch_ceiling_GBps": round(gb / (floor_us * 1e3 + gb / HBM_PEAK_GBPS), 1)}
     tj = load_json("gemv_3072x1024_hbm_traffic.json")
