@@ -312,8 +312,7 @@ int run_lm_head(const q4d_model_t* m, const float* hidden, int32_t* tok, float* 
   a.gamma = m->final_norm;
   a.eps = m->rms_norm_eps;
   a.logits = logits;
-  a.lm_key = ws_ptr<unsigned long long>(ws, W.lm_key);
-  a.counter = ws_ptr<int>(ws, W.counters) + W.lm_counter_index;
+  a.lm_hand = ws_ptr<char>(ws, W.lm_hand);
   a.out_token = tok;
   a.out_score = score;
   if (fb) {

@@ -48,13 +48,16 @@
 // (common.py:284,297), SwiGLU over the gate/up pair (common.py:293-295), and
 // LM-head argmax with the lowest-index tie rule
 // (56_export_persistent_multitoken_layer_golden.py:860).  The argmax is
-// finished without fences: each block folds its best (score, index) into one
-// 64-bit key with a device-scope atomicMax, waits for it to complete, then
-// counts in; the last block to count in reads the key back with another
-// atomic, so every read goes to the coherence point.  With greedy feedback the
-// last block also stores the token as the next step's input, advances the
-// position and records the history (what advance_kernel does as a launch of
-// its own).
+// finished without fences, in two levels: each block folds its best (score,
+// index) into the 64-bit key of its group (blocks g, g + 8, ...) with a
+// device-scope atomicMax, waits for it to complete, then counts in on its
+// group's counter; the last block of a group counts in on the top counter, and
+// the last of those reads the eight group keys with device-scope loads (every
+// read goes to the coherence point).  With greedy feedback that block also
+// stores the token as the next step's input, advances the position and
+// records the history (what advance_kernel does as a launch of its own).
+// Weights and scales are read with non-temporal loads, and a wave's issue
+// priority falls as it progresses, so the waves of a SIMD finish together.
 #include <math.h>
 
 #include "q4d_device.h"
@@ -392,6 +395,18 @@ __device__ __forceinline__ float chunk_scaled(const u32x4 w, const XChunk& h, co
   return code * fmaf(fmaf(a, 16.f, b), 64.f, -s8);
 }
 
+// s_setprio with a wave-uniform runtime level (the instruction takes an immediate).
+__device__ __forceinline__ void set_prio(int p) {
+  if (p >= 3)
+    __builtin_amdgcn_s_setprio(3);
+  else if (p == 2)
+    __builtin_amdgcn_s_setprio(2);
+  else if (p == 1)
+    __builtin_amdgcn_s_setprio(1);
+  else
+    __builtin_amdgcn_s_setprio(0);
+}
+
 template <int XP, int U, int NWB, bool PARTS>
 __global__ __launch_bounds__(NWB * 64) void lm_kernel(const GemvArgs a) {
   constexpr int K = 1024;
@@ -428,9 +443,9 @@ __global__ __launch_bounds__(NWB * 64) void lm_kernel(const GemvArgs a) {
     t = t < NT4 ? t : NT4 - 1;
     const int row0 = min(4 * t, R - 4);
     Tile4 d;
-    d.w0 = __builtin_amdgcn_raw_buffer_load_b128(rw, vw, (uint32_t)row0 * (K / 2), 0);
-    d.w1 = __builtin_amdgcn_raw_buffer_load_b128(rw, vw + 256, (uint32_t)row0 * (K / 2), 0);
-    d.s = __builtin_amdgcn_raw_buffer_load_b32(rsc, vs, (uint32_t)row0 * (K / 32), 0);
+    d.w0 = __builtin_amdgcn_raw_buffer_load_b128(rw, vw, (uint32_t)row0 * (K / 2), kLoadNT);
+    d.w1 = __builtin_amdgcn_raw_buffer_load_b128(rw, vw + 256, (uint32_t)row0 * (K / 2), kLoadNT);
+    d.s = __builtin_amdgcn_raw_buffer_load_b32(rsc, vs, (uint32_t)row0 * (K / 32), kLoadNT);
     return d;
   };
 
@@ -500,21 +515,34 @@ __global__ __launch_bounds__(NWB * 64) void lm_kernel(const GemvArgs a) {
 #pragma unroll
     for (int u = 0; u < U; ++u) D[u] = load4(base + (st * U + u) * step);
   };
+  // Issue priority falls as a wave progresses, from 3 to 0 over its S stages, with
+  // the older waves of a SIMD (wid / 4: 0 oldest) given a head start: among equal
+  // priorities the SIMD issues the oldest wave first, which left the youngest slot
+  // 30 % slower per tile and finishing ~3 us after the oldest.
+  const int lead = 2 * (3 - (wid >> 2));
+  auto prio = [&](int k) { set_prio(3 - min(3, (4 * k + lead) / max(S, 1))); };
   int st = 0;
   for (; st + 3 < S; st += 2) {
+    prio(st);
     consume(A, base + st * U * step);
     reload(A, st + 2);
+    prio(st + 1);
     consume(B, base + (st + 1) * U * step);
     reload(B, st + 3);
   }
+  prio(st);
   consume(A, base + st * U * step);
   if (st + 2 < S) {
     reload(A, st + 2);
+    prio(st + 1);
     consume(B, base + (st + 1) * U * step);
+    prio(st + 2);
     consume(A, base + (st + 2) * U * step);
   } else {
+    prio(st + 1);
     consume(B, base + (st + 1) * U * step);  // may lie wholly past the matrix
   }
+  set_prio(0);
 
   unsigned long long key = argmax_key(best, besti);
 #pragma unroll
@@ -524,36 +552,64 @@ __global__ __launch_bounds__(NWB * 64) void lm_kernel(const GemvArgs a) {
   }
   if (lane == 0) s_key[wid] = key;
   __syncthreads();
-  if (threadIdx.x == 0) {
+  if (wid == 0) {
     unsigned long long bk = s_key[0];
 #pragma unroll
     for (int w = 1; w < NWB; ++w) bk = s_key[w] > bk ? s_key[w] : bk;
-    // fold in, wait for the atomic to be performed, then count in
-    const unsigned long long old = __hip_atomic_fetch_max(a.lm_key, bk, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    asm volatile("" ::"v"((uint32_t)old), "v"((uint32_t)(old >> 32)) : "memory");
-    const int done = __hip_atomic_fetch_add(a.counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (done == (int)gridDim.x - 1) {
-      const unsigned long long fin = __hip_atomic_fetch_max(a.lm_key, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      float sc;
-      int ix;
-      argmax_unkey(fin, &sc, &ix);
-      a.out_token[0] = ix;
-      a.out_score[0] = sc;
-      if (a.adv_tokens) {  // greedy feedback, as advance_kernel
-        a.adv_tokens[0] = ix;
-        a.adv_positions[0] += 1;
-        if (a.hist_tokens) {
-          const int32_t c = a.hist_count[0];
-          if (c < a.hist_cap) {
-            a.hist_tokens[c] = ix;
-            if (a.hist_scores) a.hist_scores[c] = sc;
-            a.hist_count[0] = c + 1;
-          }
-        }
+    // two levels (see kLmHandBytes): fold into group key g and wait for the atomic to
+    // be performed, count in on group counter g; the last block of a group counts in
+    // on the top counter, and the last of those reads the group keys (8 lanes, one
+    // load).  With one key and one counter for all 256 blocks, arrivals queued ~1.3 us
+    // at the single address.
+    char* const hb = a.lm_hand;
+    const int G = gridDim.x, ng = G < kLmGroups ? G : kLmGroups, g = blockIdx.x % kLmGroups;
+    int tdone = -1;
+    if (lane == 0) {
+      const unsigned long long old = __hip_atomic_fetch_max(reinterpret_cast<unsigned long long*>(hb + 128 * g), bk,
+                                                            __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      asm volatile("" ::"v"((uint32_t)old), "v"((uint32_t)(old >> 32)) : "memory");
+      const int done = __hip_atomic_fetch_add(reinterpret_cast<int*>(hb + 1024 + 128 * g), 1, __ATOMIC_RELAXED,
+                                              __HIP_MEMORY_SCOPE_AGENT);
+      if (done == (G - g + kLmGroups - 1) / kLmGroups - 1)
+        tdone = __hip_atomic_fetch_add(reinterpret_cast<int*>(hb + 2048), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    tdone = __builtin_amdgcn_readfirstlane(tdone);
+    if (tdone == ng - 1) {
+      const int li = lane < ng ? lane : 0;
+      unsigned long long fin = __hip_atomic_load(reinterpret_cast<unsigned long long*>(hb + 128 * li),
+                                                 __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+      for (int m = kLmGroups / 2; m >= 1; m >>= 1) {
+        const unsigned long long o = __shfl_xor(fin, m, kWave);
+        fin = o > fin ? o : fin;
       }
       // ready for the next launch (stream order makes these visible to it)
-      __hip_atomic_store(a.lm_key, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_store(a.counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (lane < ng) {
+        __hip_atomic_store(reinterpret_cast<unsigned long long*>(hb + 128 * lane), 0ull, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(reinterpret_cast<int*>(hb + 1024 + 128 * lane), 0, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+      }
+      if (lane == 0) {
+        float sc;
+        int ix;
+        argmax_unkey(fin, &sc, &ix);
+        a.out_token[0] = ix;
+        a.out_score[0] = sc;
+        if (a.adv_tokens) {  // greedy feedback, as advance_kernel
+          a.adv_tokens[0] = ix;
+          a.adv_positions[0] += 1;
+          if (a.hist_tokens) {
+            const int32_t c = a.hist_count[0];
+            if (c < a.hist_cap) {
+              a.hist_tokens[c] = ix;
+              if (a.hist_scores) a.hist_scores[c] = sc;
+              a.hist_count[0] = c + 1;
+            }
+          }
+        }
+        __hip_atomic_store(reinterpret_cast<int*>(hb + 2048), 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
     }
   }
 }
@@ -690,9 +746,9 @@ int launch_gemv_xp(const GemvArgs& a, int xm, int xp, int ep, bool pair, hipStre
   if ((xm == X_RMS || xm == X_EMB) && (!a.gamma || !aligned(a.gamma, 16))) return Q4D_ERR_NULL;
   if (a.adv_tokens && (ep != EP_ARGMAX || !a.adv_positions || (a.hist_tokens && !a.hist_count))) return Q4D_ERR_NULL;
   if (ep == EP_RESID && !a.resid) return Q4D_ERR_NULL;
-  if (ep == EP_ARGMAX && (!a.lm_key || !a.counter || !a.out_token || !a.out_score || a.batch != 1))
+  if (ep == EP_ARGMAX && (!a.lm_hand || !a.out_token || !a.out_score || a.batch != 1))
     return Q4D_ERR_NULL;
-  if (ep == EP_ARGMAX && (!aligned(a.lm_key, 8) || a.nseg != 1)) return Q4D_ERR_BAD_ADDR;
+  if (ep == EP_ARGMAX && (!aligned(a.lm_hand, 256) || a.nseg != 1)) return Q4D_ERR_BAD_ADDR;
   if ((a.x_parts || a.x_out) && (ep != EP_ARGMAX || xm != X_RMS || a.cols != 1024 || !a.x_parts)) return Q4D_ERR_SHAPE;
   if ((a.x_parts && !aligned(a.x_parts, 16)) || (a.x_out && !aligned(a.x_out, 16))) return Q4D_ERR_BAD_ADDR;
   if (xm == X_F16 && xp != 1) return Q4D_ERR_DTYPE;

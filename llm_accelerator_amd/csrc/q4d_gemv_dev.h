@@ -48,12 +48,17 @@ __device__ __forceinline__ LaneOff lane_off(int ks, int lane) {
   return o;
 }
 
+// Cache-policy bits of a buffer load: non-temporal.  Weights and their scales are
+// read once per step; as non-temporal loads the 3072 x 1024 GEMV takes 2.38 instead
+// of 2.85 us from HBM (no change when the matrix is cache-resident).
+constexpr int kLoadNT = 2;
+
 // Load tile rows (lrow0, lrow0 + 1) of one matrix (lrow0 uniform).
 template <int K>
 __device__ __forceinline__ TileData load_rows(Rsrc rw, Rsrc rs, int lrow0, const LaneOff& o) {
   TileData d;
-  d.w = __builtin_amdgcn_raw_buffer_load_b128(rw, o.w, (uint32_t)lrow0 * (K / 2), 0);
-  d.s = __builtin_amdgcn_raw_buffer_load_b32(rs, o.s, (uint32_t)lrow0 * (K / 32), 0);
+  d.w = __builtin_amdgcn_raw_buffer_load_b128(rw, o.w, (uint32_t)lrow0 * (K / 2), kLoadNT);
+  d.s = __builtin_amdgcn_raw_buffer_load_b32(rs, o.s, (uint32_t)lrow0 * (K / 32), kLoadNT);
   return d;
 }
 

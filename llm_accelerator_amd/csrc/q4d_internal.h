@@ -25,11 +25,18 @@ constexpr int kXcdInter = 3072;
 
 inline size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
+// The streaming LM head's two-level argmax hand-off: blocks g, g + 8, ... fold their
+// best (score, index) key into group key g (u64 at byte 128 g) and count in on group
+// counter g (int32 at 1024 + 128 g); the last block of each group counts in on the top
+// counter (int32 at 2048).  Each word has a 128-byte line of its own.
+constexpr int kLmGroups = 8;
+constexpr size_t kLmHandBytes = 2048 + 128;
+
 // Byte offsets of the regions of a caller-provided workspace.
 struct WsLayout {
   size_t status;     // int32[64]: [0] = status bits
-  size_t counters;   // int32[batch * kv_heads] attention split counters, then 1 LM counter
-  size_t lm_key;     // u64 packed (score, index) running LM-head argmax (zeroed with the counters)
+  size_t counters;   // int32[batch * kv_heads] attention split counters
+  size_t lm_hand;    // LM-head argmax hand-off, kLmHandBytes (zeroed with the counters)
   size_t xflags;     // u32 [8][32] exchange flags of the XCD-split layer (zeroed with the counters)
   size_t hidden;     // f32 [batch, hidden]          residual stream
   size_t qkv;        // f32 [batch, (qh + 2 kvh) * d] raw q|k|v projections
@@ -53,7 +60,6 @@ struct WsLayout {
   size_t xhx2;       // f32 [hidden]      post-attention state (residual base of the next layer)
   size_t total;
   int nsplit_max;
-  int lm_counter_index;  // index into counters
 };
 
 inline WsLayout ws_layout(const q4d_model_t* m, int batch) {
@@ -63,9 +69,8 @@ inline WsLayout ws_layout(const q4d_model_t* m, int batch) {
   L.nsplit_max = (m->max_ctx + kAttnChunk - 1) / kAttnChunk;
   size_t o = 0;
   L.status = o;   o = align_up(o + 64 * 4, A);
-  L.counters = o; o = align_up(o + (size_t)(batch * kvh + 1) * 4, A);
-  L.lm_counter_index = batch * kvh;
-  L.lm_key = o;   o = align_up(o + 8, A);
+  L.counters = o; o = align_up(o + (size_t)(batch * kvh) * 4, A);
+  L.lm_hand = o;  o = align_up(o + kLmHandBytes, A);
   L.xflags = o;   o = align_up(o + (size_t)kXcdGroups * kXcdBlocks * 4, A);
   L.hidden = o;   o = align_up(o + (size_t)batch * m->hidden_size * 4, A);
   L.qkv = o;      o = align_up(o + (size_t)batch * (qh + 2 * kvh) * d * 4, A);
@@ -146,8 +151,7 @@ struct GemvArgs {
   const float* resid;   // EP_RESID: y = resid + W x
   // EP_ARGMAX.
   float* logits;        // optional
-  unsigned long long* lm_key;  // zero before the first launch; reset by the last block
-  int* counter;
+  char* lm_hand;        // kLmHandBytes, zero before the first launch; reset by the last block
   int* out_token;
   float* out_score;
   int batch;

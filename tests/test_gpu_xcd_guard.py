@@ -24,9 +24,10 @@ from llm_accelerator_amd.model import KVCache, Qwen3Config, Workspace, build_mod
 pytestmark = pytest.mark.gpu
 
 # workspace byte offset of the [8][32] exchange flags for batch 1: status (256 B), then
-# the attention counters and the LM counter (9 int32, padded to 256 B), the LM-head
-# argmax key (8 B, padded to 256 B)
-XFLAGS_OFFSET = 768
+# the attention counters (8 int32, padded to 256 B), the LM-head argmax hand-off
+# (8 group keys and counters and the top counter on 128-byte lines: 2176 B, padded
+# to 2304 B)
+XFLAGS_OFFSET = 2816
 
 
 @pytest.fixture(scope="module")
