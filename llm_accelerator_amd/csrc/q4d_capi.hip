@@ -8,7 +8,7 @@
 
 // Device scratch of q4d_run_one_token_noalloc (see noalloc_scratch below).
 constexpr size_t kNoallocScratchBytes = size_t(4) << 20;
-constexpr int kNoallocClearWords = 1024;  // status, counters and LM-head key region (4 KB)
+constexpr int kNoallocClearWords = 1024;  // status, counters, LM-head hand-off and exchange flags (4 KB)
 static __device__ __align__(256) unsigned char scratch[kNoallocScratchBytes];
 
 namespace q4d {
@@ -365,8 +365,9 @@ int noalloc_scratch(hipStream_t st, void** out) {
   if (!ptrs[dev]) {
     void* p = nullptr;
     if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) return Q4D_ERR_LAUNCH;
-    // the counters and the LM-head argmax key start at zero (the kernels leave them zero
-    // again); cleared once here with a fill kernel in case the module's zero fill is not relied on
+    // the counters, the LM-head hand-off region and the exchange flags start at zero (the
+    // kernels leave them as the next launch expects); cleared once here with a fill kernel
+    // in case the module's zero fill is not relied on
     const int rc = launch_fill_i32(static_cast<int32_t*>(p), 0, kNoallocClearWords, st);
     if (rc) return rc;
     ptrs[dev] = p;
