@@ -46,23 +46,33 @@ constexpr int kGemmBK = 64;
 constexpr int kGemmPad = 16;
 constexpr int kGemmLds = kGemmBK + kGemmPad;
 
+// Dequantise 8 consecutive int4 (one 32-bit word, low nibble first) times `scale` to
+// fp16, in column order: word p of the result holds columns 2p, 2p + 1.
+__device__ __forceinline__ u32x4 dequant8(uint32_t w, h2 scale2) {
+  const h2 bias = make_h2((_Float16)1032.0f, (_Float16)1032.0f);
+  const uint32_t v = w ^ 0x88888888u;
+  const uint32_t lo = v & 0x0F0F0F0Fu;         // nibbles 0, 2, 4, 6 in bytes 0..3
+  const uint32_t hi = (v >> 4) & 0x0F0F0F0Fu;  // nibbles 1, 3, 5, 7
+  u32x4 out;
+#pragma unroll
+  for (int p = 0; p < 4; ++p) {
+    // fp16 pair (nibble 2p, nibble 2p+1): low byte of each half from lo / hi byte p
+    const uint32_t sel = (uint32_t)(p) | (0x0Cu << 8) | ((uint32_t)(4 + p) << 16) | (0x0Cu << 24);
+    const uint32_t pr = __builtin_amdgcn_perm(hi, lo, sel) | 0x64006400u;
+    const h2 q = __builtin_bit_cast(h2, pr) - bias;
+    out[p] = __builtin_bit_cast(uint32_t, q * scale2);
+  }
+  return out;
+}
+
 // Dequantise 32 consecutive int4 (one 16-byte chunk) times `scale` to fp16,
 // in column order.
 __device__ __forceinline__ void dequant32(const u32x4 w, h2 scale2, uint32_t (&out)[16]) {
-  const h2 bias = make_h2((_Float16)1032.0f, (_Float16)1032.0f);
 #pragma unroll
   for (int m = 0; m < 4; ++m) {
-    const uint32_t v = w[m] ^ 0x88888888u;
-    const uint32_t lo = v & 0x0F0F0F0Fu;         // nibbles 0, 2, 4, 6 in bytes 0..3
-    const uint32_t hi = (v >> 4) & 0x0F0F0F0Fu;  // nibbles 1, 3, 5, 7
+    const u32x4 o = dequant8(w[m], scale2);
 #pragma unroll
-    for (int p = 0; p < 4; ++p) {
-      // fp16 pair (nibble 2p, nibble 2p+1): low byte of each half from lo / hi byte p
-      const uint32_t sel = (uint32_t)(p) | (0x0Cu << 8) | ((uint32_t)(4 + p) << 16) | (0x0Cu << 24);
-      const uint32_t pr = __builtin_amdgcn_perm(hi, lo, sel) | 0x64006400u;
-      const h2 q = __builtin_bit_cast(h2, pr) - bias;
-      out[4 * m + p] = __builtin_bit_cast(uint32_t, q * scale2);
-    }
+    for (int p = 0; p < 4; ++p) out[4 * m + p] = o[p];
   }
 }
 
@@ -761,6 +771,146 @@ __global__ __launch_bounds__(512) void q4_gemm_pipe_kernel(const GemmArgs a) {
   }
 }
 
+// ---- skinny GEMM: at most 64 activation rows (batched decode) -------------------------
+// Y^T[n, m] = sum_k W[n, k] X[m, k] with the weights as the MFMA A operand (16 rows per
+// block; a gate/up pair: 8 gate rows and the matching 8 up rows) and the activation rows
+// as B (4 tiles of 16).  Each wave takes 128 consecutive columns of K and issues every
+// load of its work at entry: one 16-byte chunk of codes per lane straight into registers
+// (no LDS for the weights), the two scale codes of its row, and 16 x 16 bytes of X; a
+// block of NW waves covers 128 NW columns (a K split takes the rest), and its waves' 16 x 64
+// partial tiles are summed through LDS in wave order, so the result is deterministic.
+//
+// MFMA k order: in step s the lanes of row group G (lanes 16G..16G+15) supply columns
+// 32s + 8G .. +7 of the wave's 128, so that one load instruction reads 64 contiguous bytes
+// of each of 16 X rows.  A lane's 16 bytes of codes hold columns 32G .. 32G+31 instead;
+// a 4 x 4 transpose of 32-bit words across the four row groups (two v_permlane32_swap,
+// two v_permlane16_swap) brings the codes into that order before dequantisation.
+constexpr int kSkRows = 16;        // weight rows per block
+constexpr int kSkKW = 128;         // K columns per wave
+constexpr int kSkMaxWaves = 8;     // waves per block at most (K columns per block <= 1024)
+constexpr int kSkRedStride = 68;   // LDS row stride of the partial tiles (floats; conflict-free)
+
+// Word s of lane row group G becomes word G of row group s (lane l % 16 kept).
+// v_permlane32_swap(A, B) returns (A.lo | B.lo, A.hi | B.hi) over lanes 0-31 | 32-63;
+// v_permlane16_swap(A, B) returns (A.r0 | B.r0 | A.r2 | B.r2, A.r1 | B.r1 | A.r3 | B.r3)
+// over the 16-lane rows r0..r3.
+__device__ __forceinline__ void rows_transpose4(uint32_t (&d)[4]) {
+  // the off-diagonal 2 x 2 blocks: rows 0-1 words 2-3 <-> rows 2-3 words 0-1
+  const auto a = __builtin_amdgcn_permlane32_swap(d[0], d[2], false, false);
+  const auto b = __builtin_amdgcn_permlane32_swap(d[1], d[3], false, false);
+  const uint32_t e0 = a[0], e2 = a[1], e1 = b[0], e3 = b[1];
+  // inside each 2 x 2 block: the even rows' odd words <-> the odd rows' even words
+  const auto c = __builtin_amdgcn_permlane16_swap(e0, e1, false, false);
+  const auto f = __builtin_amdgcn_permlane16_swap(e2, e3, false, false);
+  d[0] = c[0];
+  d[1] = c[1];
+  d[2] = f[0];
+  d[3] = f[1];
+}
+
+template <int EP, bool PAIR>
+__global__ __launch_bounds__(kSkMaxWaves * 64) void q4_skinny_kernel(const GemmArgs a) {
+  __shared__ float red[kSkMaxWaves][kSkRows][kSkRedStride];
+  const int t = threadIdx.x, lane = t & 63, w = t >> 6, nw = (int)blockDim.x >> 6;
+  const int nl = lane & 15, G = lane >> 4;
+  const int nb = blockIdx.x, z = blockIdx.z;
+  const int k0 = (z * nw + w) * kSkKW;
+
+  // the lane's weight row (a block's 16 rows lie in one segment: seg_end % 16 == 0)
+  const uint8_t* wb;
+  const uint16_t* sb;
+  int grow;
+  if (PAIR) {
+    const bool up = nl >= 8;
+    grow = nb * 8 + (nl & 7);
+    wb = up ? a.w[1] : a.w[0];
+    sb = up ? a.s[1] : a.s[0];
+  } else {
+    const int r0 = nb * kSkRows;
+    if (r0 < a.seg_end[0]) {
+      grow = r0 + nl; wb = a.w[0]; sb = a.s[0];
+    } else if (r0 < a.seg_end[1]) {
+      grow = r0 + nl - a.seg_end[0]; wb = a.w[1]; sb = a.s[1];
+    } else {
+      grow = r0 + nl - a.seg_end[1]; wb = a.w[2]; sb = a.s[2];
+    }
+  }
+  // codes: columns k0 + 32G .. +31 of the row (read once: non-temporal); the scale codes
+  // of the two 64-column groups k0 / 64, k0 / 64 + 1 (one aligned 32-bit word)
+  const u32x4 wc = __builtin_nontemporal_load(
+      reinterpret_cast<const u32x4*>(wb + (size_t)grow * (a.K / 2) + k0 / 2 + 16 * G));
+  const uint32_t sc2 = *reinterpret_cast<const uint32_t*>(sb + (size_t)grow * (a.K / 64) + k0 / 64);
+  // X: rows m = 16 ct + l % 16 (rows past M read row M - 1; their columns are not
+  // stored), columns k0 + 32 s + 8 G .. +7
+  u32x4 xf[4][4];
+#pragma unroll
+  for (int ct = 0; ct < 4; ++ct) {
+    const int m = min(16 * ct + nl, a.M - 1);
+    const uint16_t* xr = a.x + (size_t)m * a.K + k0 + 8 * G;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) xf[ct][s] = *reinterpret_cast<const u32x4*>(xr + 32 * s);
+  }
+  // every load above goes out before the first use (left alone, the scheduler sinks most
+  // of the X loads between the MFMAs, one memory round trip per step)
+  __builtin_amdgcn_sched_barrier(0);
+
+  uint32_t d[4] = {wc[0], wc[1], wc[2], wc[3]};
+  rows_transpose4(d);
+  const _Float16 slo = (_Float16)((float)(sc2 & 0xFFFFu) * (1.0f / 16384.0f));
+  const _Float16 shi = (_Float16)((float)(sc2 >> 16) * (1.0f / 16384.0f));
+  f32x4 acc[4];
+#pragma unroll
+  for (int ct = 0; ct < 4; ++ct) acc[ct] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+    const _Float16 sc = s < 2 ? slo : shi;
+    const h8 af = __builtin_bit_cast(h8, dequant8(d[s], make_h2(sc, sc)));
+#pragma unroll
+    for (int ct = 0; ct < 4; ++ct)
+      acc[ct] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, __builtin_bit_cast(h8, xf[ct][s]), acc[ct], 0, 0, 0);
+  }
+  // lane holds rows 4G + r (weight rows) of column 16 ct + l % 16 (activation rows)
+#pragma unroll
+  for (int ct = 0; ct < 4; ++ct)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) red[w][4 * G + r][16 * ct + nl] = acc[ct][r];
+  __syncthreads();
+
+  if constexpr (PAIR) {
+    // SwiGLU of gate row i (tile row i) and up row i (tile row 8 + i)
+    for (int o = t; o < 8 * 64; o += (int)blockDim.x) {
+      const int i = o & 7, mm = o >> 3;
+      if (mm >= a.M) continue;
+      float g = red[0][i][mm], u = red[0][8 + i][mm];
+      for (int v = 1; v < nw; ++v) {
+        g += red[v][i][mm];
+        u += red[v][8 + i][mm];
+      }
+      static_cast<_Float16*>(a.y)[(size_t)mm * a.ldy + nb * 8 + i] = (_Float16)((g / (1.0f + expf(-g))) * u);
+    }
+  } else {
+    const bool split = gridDim.z > 1;
+    for (int o = t; o < kSkRows * 64; o += (int)blockDim.x) {
+      const int row = o & 15, mm = o >> 4;
+      if (mm >= a.M) continue;
+      float v = red[0][row][mm];
+      for (int q = 1; q < nw; ++q) v += red[q][row][mm];
+      const int n = nb * kSkRows + row;
+      if (split) {
+        a.part[((size_t)z * a.M + mm) * a.N + n] = v;  // raw split tile [z][m][n]
+        continue;
+      }
+      const size_t oo = (size_t)mm * a.ldy + n;
+      if constexpr (EP == EP_F16)
+        static_cast<_Float16*>(a.y)[oo] = (_Float16)v;
+      else if constexpr (EP == EP_RESID)
+        static_cast<float*>(a.y)[oo] = a.resid[oo] + v;
+      else
+        static_cast<float*>(a.y)[oo] = v;
+    }
+  }
+}
+
 // Sum of the split-K tiles in split order, then the epilogue; one thread per
 // four consecutive outputs of the [M, N] result (N % 4 == 0).
 template <int EP, bool PAIR>
@@ -962,6 +1112,41 @@ static int launch_gemm_pipe(const GemmArgs& a, hipStream_t st) {
   return check_launch();
 }
 
+// Split of the skinny kernel (K columns per block = 128 x waves), or 0 where it does not
+// apply: at most 64 activation rows, no split asked for, K % 128 == 0, 16-row tiles
+// (a gate/up pair: 8 + 8 rows) and at most 8 waves per block without a split.  With a
+// partial buffer the split grows (over divisors of K / 128, at least 2 waves per block)
+// until the grid has 256 blocks.
+static int skinny_split(const GemmArgs& a, int ep, bool pair) {
+  if (a.M > 64 || a.ksplit != 0 || a.K % kSkKW) return 0;
+  if (pair ? ep != EP_SWIGLU : (ep != EP_F32 && ep != EP_F16 && ep != EP_RESID)) return 0;
+  if (pair ? a.N % 8 : (a.N % kSkRows || a.seg_end[0] % kSkRows || a.seg_end[1] % kSkRows)) return 0;
+  const int nk = a.K / kSkKW, tiles = pair ? a.N / 8 : a.N / kSkRows;
+  int ks = 1;
+  while (ks <= nk && (nk % ks || nk / ks > kSkMaxWaves)) ++ks;
+  if (ks > nk) return 0;
+  const bool can_split = !pair && a.part && a.N % 4 == 0;
+  if (ks > 1 && !can_split) return 0;
+  if (can_split) {
+    for (int k2 = ks + 1; tiles * ks < 256 && k2 <= kGemmMaxSplit && nk / k2 >= 2; ++k2)
+      if (nk % k2 == 0) ks = k2;
+  }
+  if (ks > 1 && (size_t)ks * a.M * a.N > a.part_cap) return 0;
+  return ks;
+}
+
+template <int EP, bool PAIR>
+static int launch_skinny(const GemmArgs& a, int ks, hipStream_t st) {
+  const int tiles = PAIR ? a.N / 8 : a.N / kSkRows, nw = a.K / kSkKW / ks;
+  if (a.ksplit_used) *a.ksplit_used = ks;
+  hipLaunchKernelGGL((q4_skinny_kernel<EP, PAIR>), dim3(tiles, 1, ks), dim3(64 * nw), 0, st, a);
+  int rc = check_launch();
+  if (rc || ks == 1 || a.defer_reduce) return rc;
+  const int n4 = a.M * (a.N / 4);
+  hipLaunchKernelGGL((splitk_reduce_kernel<EP, PAIR>), dim3((n4 + 255) / 256), dim3(256), 0, st, a, ks);
+  return check_launch();
+}
+
 template <int BM>
 static int launch_gemm_bm(const GemmArgs& a, int ep, bool pair, hipStream_t st) {
   if (pair) return ep == EP_SWIGLU ? launch_gemm_inst<BM, EP_SWIGLU, true>(a, st) : Q4D_ERR_SHAPE;
@@ -1011,6 +1196,15 @@ int launch_gemm(const GemmArgs& a, int ep, bool pair, hipStream_t st) {
       case EP_RESID: return launch_gemm_pipe<EP_RESID, false>(a, st);
       case EP_ROPE: return launch_gemm_pipe<EP_ROPE, false>(a, st);
       default: return Q4D_ERR_SHAPE;
+    }
+  }
+  // at most 64 activation rows (batched decode): the skinny kernel where it applies
+  if (const int ks = skinny_split(a, ep, pair)) {
+    if (pair) return launch_skinny<EP_SWIGLU, true>(a, ks, st);
+    switch (ep) {
+      case EP_F32: return launch_skinny<EP_F32, false>(a, ks, st);
+      case EP_F16: return launch_skinny<EP_F16, false>(a, ks, st);
+      default: return launch_skinny<EP_RESID, false>(a, ks, st);
     }
   }
   // small M (batched decode) uses 64-row tiles, and so does a large M whose
