@@ -46,6 +46,19 @@ static_assert(kAttnChunk == 64 && kAttnChunkLong == 128, "thread mapping assumes
 
 namespace {
 
+// Merged head output element oi = (sequence * q heads + head) * head_dim + dim, as fp32,
+// fp16, or fp16 in the tiled layout (row = sequence, column = head * head_dim + dim).
+__device__ __forceinline__ void store_out(const AttnArgs& a, size_t oi, float r) {
+  if (a.out_dtype == kF16Tiled) {
+    const size_t w = (size_t)a.qh * a.d;
+    static_cast<_Float16*>(a.out)[xt_index((int)(oi / w), (int)(oi % w))] = (_Float16)r;
+  } else if (a.out_dtype == Q4D_F16) {
+    static_cast<_Float16*>(a.out)[oi] = (_Float16)r;
+  } else {
+    static_cast<float*>(a.out)[oi] = r;
+  }
+}
+
 __device__ __forceinline__ void unpack8(const u32x4 w, float (&f)[8]) {
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
@@ -351,10 +364,7 @@ __global__ __launch_bounds__(256) void attn_kernel(const AttnArgs a) {
   if (nsplit == 1) {
     const float r = acc / sml[hh][1];
     const size_t oi = ((size_t)b * a.qh + h) * D + d;
-    if (a.out_dtype == Q4D_F16)
-      static_cast<_Float16*>(a.out)[oi] = (_Float16)r;
-    else
-      static_cast<float*>(a.out)[oi] = r;
+    store_out(a, oi, r);
     return;
   }
   store_dev(&a.part_acc[(pbase + s) * D + d], acc);
@@ -396,10 +406,7 @@ __global__ __launch_bounds__(256) void attn_kernel(const AttnArgs a) {
   }
   const float r = o / L;
   const size_t oi = ((size_t)b * a.qh + h) * D + d;
-  if (a.out_dtype == Q4D_F16)
-    static_cast<_Float16*>(a.out)[oi] = (_Float16)r;
-  else
-    static_cast<float*>(a.out)[oi] = r;
+  store_out(a, oi, r);
   if (t == 0) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);  // next launch
 }
 
@@ -653,10 +660,7 @@ __global__ __launch_bounds__(256) void attn_span_kernel(const AttnArgs a, int sp
   if (nsplit == 1) {
     const float r = acc / Lb;
     const size_t oi = ((size_t)b * a.qh + h) * D + d;
-    if (a.out_dtype == Q4D_F16)
-      static_cast<_Float16*>(a.out)[oi] = (_Float16)r;
-    else
-      static_cast<float*>(a.out)[oi] = r;
+    store_out(a, oi, r);
     return;
   }
   store_dev(&a.part_acc[(pbase + s) * D + d], acc);
@@ -694,10 +698,7 @@ __global__ __launch_bounds__(256) void attn_span_kernel(const AttnArgs a, int sp
   }
   const float r = o / Lx;
   const size_t oi = ((size_t)b * a.qh + h) * D + d;
-  if (a.out_dtype == Q4D_F16)
-    static_cast<_Float16*>(a.out)[oi] = (_Float16)r;
-  else
-    static_cast<float*>(a.out)[oi] = r;
+  store_out(a, oi, r);
   if (t == 0) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);  // next launch
 }
 

@@ -626,6 +626,7 @@ int q4d_gemm_splitk(const q4d_matrix_t* w, const uint16_t* x, int32_t M, void* y
   a.part = part;
   a.part_cap = part_bytes / 4;
   a.ksplit = ksplit;
+  a.skinny = ksplit == 0;  // the library chooses: the skinny kernel for M <= 64
   return launch_gemm(a, resid ? EP_RESID : (y_dtype == Q4D_F16 ? EP_F16 : EP_F32), false, as_stream(stream));
 }
 
@@ -675,11 +676,13 @@ int q4d_decode_batch(const q4d_model_t* model, const int32_t* tokens, const int3
   uint16_t* act = ws_ptr<uint16_t>(ws, W.act);
   int32_t* status = ws_ptr<int32_t>(ws, W.status);
   float* part = ws_ptr<float>(ws, W.gemm_part);  // split-K tiles of the M = batch GEMMs
+  // the GEMMs' fp16 inputs (xh, attn, act) in the tiled layout for 2..64 sequences
+  const int xt = xt_batch(batch) ? 1 : 0;
+  const int xdt = xt ? kF16Tiled : Q4D_F16;
   if ((rc = launch_embedding(&model->embed_tokens, tokens, batch, hidden, status, st))) return rc;
   // the first layer's input RMSNorm; later ones come out of the previous layer's down
   // projection, whose split-K reduction and residual run fused with it
-  if ((rc = launch_rms_norm(hidden, model->layers[0].input_layernorm, model->rms_norm_eps, batch, H, xh, Q4D_F16,
-                            st)))
+  if ((rc = launch_rms_norm(hidden, model->layers[0].input_layernorm, model->rms_norm_eps, batch, H, xh, xdt, st)))
     return rc;
   // o_proj / down + residual, then the RMSNorm that follows (gamma): the split-K sums,
   // the residual and the norm as one kernel when the GEMM was split
@@ -687,10 +690,13 @@ int q4d_decode_batch(const q4d_model_t* model, const int32_t* tokens, const int3
     int ks = 1;
     g.defer_reduce = 1;
     g.ksplit_used = &ks;
+    g.skinny = 1;
+    g.x_tiled = xt;
     int r = launch_gemm(g, EP_RESID, false, st);
     if (r) return r;
+    g.y_tiled = xt;
     if (ks > 1) return launch_splitk_resid_norm(g, ks, gamma, model->rms_norm_eps, xh, st);
-    return launch_rms_norm(hidden, gamma, model->rms_norm_eps, batch, H, xh, Q4D_F16, st);
+    return launch_rms_norm(hidden, gamma, model->rms_norm_eps, batch, H, xh, xdt, st);
   };
   for (int l = 0; l < model->num_layers; ++l) {
     const q4d_layer_t& L = model->layers[l];
@@ -707,6 +713,8 @@ int q4d_decode_batch(const q4d_model_t* model, const int32_t* tokens, const int3
     g.K = H;
     g.M = batch;
     g.x = xh;
+    g.skinny = 1;
+    g.x_tiled = xt;
     g.y = qkv;
     g.ldy = g.N;
     g.part = part; g.part_cap = W.gemm_part_floats;
@@ -734,7 +742,7 @@ int q4d_decode_batch(const q4d_model_t* model, const int32_t* tokens, const int3
     t.part_acc = ws_ptr<float>(ws, W.part_acc);
     t.counters = ws_ptr<int>(ws, W.counters);
     t.out = attn;
-    t.out_dtype = Q4D_F16;
+    t.out_dtype = xdt;
     t.status = status;
     t.merge = 1;
     if ((rc = launch_attention(t, st))) return rc;
@@ -755,6 +763,8 @@ int q4d_decode_batch(const q4d_model_t* model, const int32_t* tokens, const int3
     g.nseg = 2;
     g.N = I; g.K = H; g.M = batch;
     g.x = xh; g.y = act; g.ldy = I;
+    g.skinny = 1;
+    g.x_tiled = g.y_tiled = xt;
     g.part = part; g.part_cap = W.gemm_part_floats;
     if ((rc = launch_gemm(g, EP_SWIGLU, true, st))) return rc;
 
@@ -767,8 +777,10 @@ int q4d_decode_batch(const q4d_model_t* model, const int32_t* tokens, const int3
     g.part = part; g.part_cap = W.gemm_part_floats;
     if (l + 1 < model->num_layers) {
       if ((rc = resid_then_norm(g, model->layers[l + 1].input_layernorm))) return rc;
-    } else if ((rc = launch_gemm(g, EP_RESID, false, st))) {
-      return rc;
+    } else {
+      g.skinny = 1;
+      g.x_tiled = xt;
+      if ((rc = launch_gemm(g, EP_RESID, false, st))) return rc;
     }
   }
   return run_lm_head_batch(model, hidden, batch, next_tokens, scores, logits, ws, W, st);

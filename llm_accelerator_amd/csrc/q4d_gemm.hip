@@ -841,14 +841,22 @@ __global__ __launch_bounds__(kSkMaxWaves * 64) void q4_skinny_kernel(const GemmA
       reinterpret_cast<const u32x4*>(wb + (size_t)grow * (a.K / 2) + k0 / 2 + 16 * G));
   const uint32_t sc2 = *reinterpret_cast<const uint32_t*>(sb + (size_t)grow * (a.K / 64) + k0 / 64);
   // X: rows m = 16 ct + l % 16 (rows past M read row M - 1; their columns are not
-  // stored), columns k0 + 32 s + 8 G .. +7
+  // stored), columns k0 + 32 s + 8 G .. +7.  Row-major X gives each load instruction 16
+  // pieces of 64 bytes; the tiled layout makes it 1 KB of contiguous memory (a 3072 x 1024
+  // pair GEMM at M = 64: 11.1 -> ~7 us)
   u32x4 xf[4][4];
 #pragma unroll
   for (int ct = 0; ct < 4; ++ct) {
     const int m = min(16 * ct + nl, a.M - 1);
-    const uint16_t* xr = a.x + (size_t)m * a.K + k0 + 8 * G;
+    if (a.x_tiled) {
 #pragma unroll
-    for (int s = 0; s < 4; ++s) xf[ct][s] = *reinterpret_cast<const u32x4*>(xr + 32 * s);
+      for (int s = 0; s < 4; ++s)
+        xf[ct][s] = *reinterpret_cast<const u32x4*>(a.x + xt_index(m, k0 + 32 * s) + 8 * G);
+    } else {
+      const uint16_t* xr = a.x + (size_t)m * a.K + k0 + 8 * G;
+#pragma unroll
+      for (int s = 0; s < 4; ++s) xf[ct][s] = *reinterpret_cast<const u32x4*>(xr + 32 * s);
+    }
   }
   // every load above goes out before the first use (left alone, the scheduler sinks most
   // of the X loads between the MFMAs, one memory round trip per step)
@@ -886,7 +894,8 @@ __global__ __launch_bounds__(kSkMaxWaves * 64) void q4_skinny_kernel(const GemmA
         g += red[v][i][mm];
         u += red[v][8 + i][mm];
       }
-      static_cast<_Float16*>(a.y)[(size_t)mm * a.ldy + nb * 8 + i] = (_Float16)((g / (1.0f + expf(-g))) * u);
+      const size_t yo = a.y_tiled ? xt_index(mm, nb * 8 + i) : (size_t)mm * a.ldy + nb * 8 + i;
+      static_cast<_Float16*>(a.y)[yo] = (_Float16)((g / (1.0f + expf(-g))) * u);
     }
   } else {
     const bool split = gridDim.z > 1;
@@ -976,8 +985,8 @@ __global__ __launch_bounds__(256) void splitk_resid_norm_kernel(const GemmArgs a
     if (t + 256 * i < nv) {
       h2 lo = make_h2((_Float16)((y[i][0] * inv) * gamma[n]), (_Float16)((y[i][1] * inv) * gamma[n + 1]));
       h2 hi = make_h2((_Float16)((y[i][2] * inv) * gamma[n + 2]), (_Float16)((y[i][3] * inv) * gamma[n + 3]));
-      *reinterpret_cast<u32x2*>(xn + (size_t)m * a.N + n) = u32x2{__builtin_bit_cast(uint32_t, lo),
-                                                                 __builtin_bit_cast(uint32_t, hi)};
+      const size_t xo = a.y_tiled ? xt_index(m, n) : (size_t)m * a.N + n;  // 4 columns of one chunk
+      *reinterpret_cast<u32x2*>(xn + xo) = u32x2{__builtin_bit_cast(uint32_t, lo), __builtin_bit_cast(uint32_t, hi)};
     }
   }
 }
@@ -986,6 +995,7 @@ int launch_splitk_resid_norm(const GemmArgs& a, int ksplit, const float* gamma, 
                              hipStream_t st) {
   if (!a.part || !a.resid || !a.y || !gamma || !xn) return Q4D_ERR_NULL;
   if (a.N % 4 || a.N > 4096 || a.M <= 0 || ksplit < 1 || (size_t)ksplit * a.M * a.N > a.part_cap) return Q4D_ERR_SHAPE;
+  if (a.y_tiled && (a.M > kXtRows || a.N % 32)) return Q4D_ERR_SHAPE;
   if (a.ldy % 4 || !aligned(a.y, 16) || !aligned(a.resid, 16) || !aligned(xn, 8) || !aligned(a.part, 16))
     return Q4D_ERR_BAD_ADDR;
   hipLaunchKernelGGL(splitk_resid_norm_kernel, dim3(a.M), dim3(256), 0, st, a, ksplit, gamma, eps,
@@ -1113,12 +1123,13 @@ static int launch_gemm_pipe(const GemmArgs& a, hipStream_t st) {
 }
 
 // Split of the skinny kernel (K columns per block = 128 x waves), or 0 where it does not
-// apply: at most 64 activation rows, no split asked for, K % 128 == 0, 16-row tiles
+// apply: asked for (GemmArgs::skinny), at most 64 activation rows, no split asked for,
+// K % 128 == 0, 16-row tiles
 // (a gate/up pair: 8 + 8 rows) and at most 8 waves per block without a split.  With a
 // partial buffer the split grows (over divisors of K / 128, at least 2 waves per block)
 // until the grid has 256 blocks.
 static int skinny_split(const GemmArgs& a, int ep, bool pair) {
-  if (a.M > 64 || a.ksplit != 0 || a.K % kSkKW) return 0;
+  if (!a.skinny || a.M > 64 || a.ksplit != 0 || a.K % kSkKW) return 0;
   if (pair ? ep != EP_SWIGLU : (ep != EP_F32 && ep != EP_F16 && ep != EP_RESID)) return 0;
   if (pair ? a.N % 8 : (a.N % kSkRows || a.seg_end[0] % kSkRows || a.seg_end[1] % kSkRows)) return 0;
   const int nk = a.K / kSkKW, tiles = pair ? a.N / 8 : a.N / kSkRows;
@@ -1198,8 +1209,12 @@ int launch_gemm(const GemmArgs& a, int ep, bool pair, hipStream_t st) {
       default: return Q4D_ERR_SHAPE;
     }
   }
-  // at most 64 activation rows (batched decode): the skinny kernel where it applies
-  if (const int ks = skinny_split(a, ep, pair)) {
+  // at most 64 activation rows (batched decode): the skinny kernel where it applies (the
+  // only kernel that reads or writes the tiled layout)
+  const int sks = skinny_split(a, ep, pair);
+  if ((a.x_tiled || a.y_tiled) && (!sks || a.M > kXtRows || a.K % 32 || (a.y_tiled && a.N % 32)))
+    return Q4D_ERR_SHAPE;
+  if (const int ks = sks) {
     if (pair) return launch_skinny<EP_SWIGLU, true>(a, ks, st);
     switch (ep) {
       case EP_F32: return launch_skinny<EP_F32, false>(a, ks, st);

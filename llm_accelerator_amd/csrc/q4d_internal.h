@@ -25,6 +25,18 @@ constexpr int kXcdInter = 3072;
 
 inline size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
+// fp16 activations of at most 64 rows in 32-column chunks ("tiled"): element (m, k) at
+// ((k / 32) * 64 + m) * 32 + k % 32, so 16 rows x 32 columns (one MFMA operand fragment
+// set) are 1 KB of contiguous memory.  The batched decode step (2 <= batch <= 64) keeps
+// the GEMMs' fp16 inputs this way; kF16Tiled is the y_dtype / out_dtype code of the
+// kernels that write it.
+constexpr int kXtRows = 64;
+constexpr int kF16Tiled = 0x100;
+__host__ __device__ inline size_t xt_index(int m, int k) {
+  return ((size_t)(k >> 5) * kXtRows + m) * 32 + (k & 31);
+}
+inline bool xt_batch(int batch) { return batch > 1 && batch <= kXtRows; }
+
 // The streaming LM head's two-level argmax hand-off: blocks g, g + 8, ... fold their
 // best (score, index) key into group key g (u64 at byte 128 g) and count in on group
 // counter g (int32 at 1024 + 128 g); the last block of each group counts in on the top
@@ -67,6 +79,7 @@ inline WsLayout ws_layout(const q4d_model_t* m, int batch) {
   const size_t A = 256;
   const int d = m->head_dim, qh = m->num_q_heads, kvh = m->num_kv_heads;
   L.nsplit_max = (m->max_ctx + kAttnChunk - 1) / kAttnChunk;
+  const int xrows = xt_batch(batch) ? kXtRows : batch;  // rows of the fp16 GEMM inputs
   size_t o = 0;
   L.status = o;   o = align_up(o + 64 * 4, A);
   L.counters = o; o = align_up(o + (size_t)(batch * kvh) * 4, A);
@@ -75,15 +88,15 @@ inline WsLayout ws_layout(const q4d_model_t* m, int batch) {
   L.hidden = o;   o = align_up(o + (size_t)batch * m->hidden_size * 4, A);
   L.qkv = o;      o = align_up(o + (size_t)batch * (qh + 2 * kvh) * d * 4, A);
   L.qrope = o;    o = align_up(o + (size_t)batch * qh * d * 4, A);
-  L.attn = o;     o = align_up(o + (size_t)batch * qh * d * 4, A);
-  L.act = o;      o = align_up(o + (size_t)batch * m->intermediate_size * 4, A);
+  L.attn = o;     o = align_up(o + (size_t)(batch > xrows ? batch : xrows) * qh * d * 4, A);
+  L.act = o;      o = align_up(o + (size_t)(batch > xrows ? batch : xrows) * m->intermediate_size * 4, A);
   L.part_ml = o;  o = align_up(o + (size_t)batch * qh * L.nsplit_max * 2 * 4, A);
   L.part_acc = o; o = align_up(o + (size_t)batch * qh * L.nsplit_max * d * 4, A);
   int wmax = m->hidden_size;
   if (qh * d > wmax) wmax = qh * d;
   if (m->intermediate_size > wmax) wmax = m->intermediate_size;
   const size_t nparts = (size_t)(m->vocab_size + 127) / 128;
-  L.xh = o;        o = align_up(o + (size_t)batch * wmax * 2, A);
+  L.xh = o;        o = align_up(o + (size_t)xrows * wmax * 2, A);
   L.row_score = o; o = align_up(o + (size_t)batch * nparts * 4, A);
   L.row_idx = o;   o = align_up(o + (size_t)batch * nparts * 4, A);
   {
@@ -321,6 +334,14 @@ struct GemmArgs {
   size_t part_cap;
   int ksplit;
   int defer_reduce;  // with a split, leave the partials for launch_splitk_resid_norm
+  // skinny: with M <= 64 the skinny kernel may run (its sums are grouped differently
+  // from the tiled kernels', so callers that compare against those opt out: prefill
+  // chunks must equal one call bit for bit).  x_tiled: X in the tiled layout (xt_index);
+  // y_tiled: the fp16 output of EP_SWIGLU, and xn of launch_splitk_resid_norm, written
+  // tiled (both only through the skinny kernel).
+  int skinny;
+  int x_tiled;
+  int y_tiled;
   int* ksplit_used;  // optional: receives the split launch_gemm ran (1: the epilogue was applied)
   // EP_ROPE (prefill q|k|v, no split): the 128 columns of an output tile are one
   // head, q heads then k heads then v heads; q rows go normed, roped and scaled to

@@ -23,6 +23,8 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(const float* x, const flo
     const float v = (xr[i] * inv) * gamma[i];
     if (y_dtype == Q4D_F16)
       static_cast<_Float16*>(y)[(size_t)row * dim + i] = (_Float16)v;
+    else if (y_dtype == kF16Tiled)
+      static_cast<_Float16*>(y)[xt_index(row, i)] = (_Float16)v;
     else
       static_cast<float*>(y)[(size_t)row * dim + i] = v;
   }
