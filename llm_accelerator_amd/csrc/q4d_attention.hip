@@ -411,22 +411,24 @@ __global__ __launch_bounds__(256) void attn_kernel(const AttnArgs a) {
 }
 
 // Long-context variant of attn_kernel<64> with merge = 1 (batched decode,
-// q4d_cached_attention): a block covers `span` positions (a multiple of 64)
-// as consecutive 32-position sub-chunks, with the next sub-chunk's K/V loads
+// q4d_cached_attention): a block covers one of nsplit nearly equal parts of the
+// T = pos + 1 positions (nsplit = ceil(T / span), parts of whole 64-position
+// sub-chunks) as consecutive sub-chunks, with the next sub-chunk's K/V loads
 // in flight while the current one is used.  Each wave keeps its own online
 // softmax (running maximum M and sum L per head; its output accumulators are
-// rescaled by 2^(M_old - M_new) when M grows) over its 8 positions of every
+// rescaled by 2^(M_old - M_new) when M grows) over its 16 positions of every
 // sub-chunk, so the sub-chunk loop has no barrier; the four waves' states are
 // merged once after the span.  K/V are read with non-temporal loads (read once
-// per step).  Measured on the 64 x 4097-position batch: the loads alone run
-// as fast as the whole kernel, and 64-position sub-chunks (two rows more in
-// flight per thread) or block-wide softmax per sub-chunk were 5 % slower.
-// `span` is chosen so a head has at most eight splits, which the last block
-// merges with one batch of loads.  Same prologue and partial format as
+// per step).  The launcher sizes `span` for about two blocks per CU over the
+// batch's (sequence, kv head) pairs: a few long contiguous K/V streams per CU
+// read HBM faster than many short ones (64 x 4097 positions, 28 layers: eight
+// 576-position spans per head, 5 resident blocks per CU and 32-position
+// sub-chunks took 6.35 ms per step; equal parts 6.27; one block per head with
+// 64-position sub-chunks 5.48).  Same prologue and partial format as
 // attn_kernel<64>; thread t owns dims 8 (t % 16) .. +7 of positions t / 16 + 16 i.
 __global__ __launch_bounds__(256) void attn_span_kernel(const AttnArgs a, int span) {
   attn_preload(a);
-  constexpr int D = 128, CH = 32, NPT = CH / 16;
+  constexpr int D = 128, CH = 64, NPT = CH / 16;
   const int s = blockIdx.x, j = blockIdx.y, b = blockIdx.z;
   const int t = threadIdx.x, lane = t & 63;
   const int wid = __builtin_amdgcn_readfirstlane(t >> 6);
@@ -438,8 +440,9 @@ __global__ __launch_bounds__(256) void attn_span_kernel(const AttnArgs a, int sp
   const int T = pos + 1;
   const int nsplit = (T + span - 1) / span;
   if (s >= nsplit) return;
-  const int start = s * span;
-  const int end = min(T, start + span);
+  const int nsub_all = (T + CH - 1) / CH;
+  const int start = (s * nsub_all / nsplit) * CH;
+  const int end = min(T, ((s + 1) * nsub_all / nsplit) * CH);
   const int nsub = (end - start + CH - 1) / CH;
   const int cached = a.fused ? pos : T;
   const bool last = (s == nsplit - 1);  // block-uniform: holds pos
@@ -708,13 +711,16 @@ int launch_attention(const AttnArgs& a, hipStream_t stream) {
   if (!a.part_ml || !a.part_acc || (a.merge && !a.counters)) return Q4D_ERR_NULL;
   if (a.merge) {
     // contexts past kSpanSplits x 64 positions: spans of several 64-position
-    // sub-chunks, at most kSpanSplits per head
+    // sub-chunks, at most kSpanSplits per head, as many as make about two blocks
+    // per CU over the (sequence, kv head) pairs
     constexpr int kSpanSplits = 8;
     const int nch = (a.max_ctx + kAttnChunk - 1) / kAttnChunk;
     if (nch <= kSpanSplits) {
       hipLaunchKernelGGL(attn_kernel<kAttnChunk>, dim3(a.nsplit_max, a.kvh, a.batch), dim3(256), 0, stream, a);
     } else {
-      const int span = kAttnChunk * ((nch + kSpanSplits - 1) / kSpanSplits);
+      const int pairs = a.batch * a.kvh;
+      const int ns = max(1, min(kSpanSplits, (2 * device_cus() + pairs - 1) / pairs));
+      const int span = kAttnChunk * ((nch + ns - 1) / ns);
       const int nsplit = (a.max_ctx + span - 1) / span;
       hipLaunchKernelGGL(attn_span_kernel, dim3(nsplit, a.kvh, a.batch), dim3(256), 0, stream, a, span);
     }

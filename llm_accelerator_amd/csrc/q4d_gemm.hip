@@ -1067,8 +1067,7 @@ static int launch_gemm_inst(const GemmArgs& a, hipStream_t st) {
   return check_launch();
 }
 
-// Compute units of the current device (cached per process; 256 on MI355X).
-static int device_cus() {
+int device_cus() {
   static int cached = 0;
   if (cached == 0) {
     int dev = 0, cus = 0;

@@ -350,6 +350,8 @@ struct GemmArgs {
   PrefillArgs rope;
 };
 constexpr int kGemmMaxSplit = 16;
+// Compute units of the current device (cached per process; 256 on MI355X).
+int device_cus();
 int launch_gemm(const GemmArgs& a, int ep, bool pair, hipStream_t st);
 // The deferred reduction of an EP_RESID split GEMM fused with the RMSNorm that follows it:
 // y = resid + sum_z part[z] (fp32, in order of z), then xn = fp16(y * rsqrt(mean(y^2) + eps)
