@@ -67,7 +67,7 @@ BATCH_SEQS, BATCH_CTX = 64, 4096  # batched decode: 64 sequences over 4096 cache
 STAGE_KERNELS = {"qkv": "input RMSNorm + q|k|v Q4 GEMV", "attention": "q/k norm + RoPE + KV append + split-K GQA attention",
                  "o_proj": "o_proj Q4 GEMV + residual", "gate_up": "post-norm + gate/up Q4 GEMV + SwiGLU",
                  "down": "down Q4 GEMV + residual"}
-GEMV_KERNEL = "gemv_kernel<1, 4, 0, 1, 0, false, 1>"
+GEMV_KERNEL = "gemv_kernel<1, 8, 0, 1, 0, false, 1>"
 PROFILES = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles")
 
 

@@ -657,11 +657,13 @@ int launch_inst(const GemvArgs& a, hipStream_t stream) {
   return check_launch();
 }
 
-// Block shapes: K = 1024 -> 4 one-slice waves; K = 2048 -> 2 teams of 2;
-// K = 3072 -> 2 teams of 3 (384 threads).
-template <int KS>
+// Block shapes: K = 1024 -> 4 one-slice waves (fp16 activations: 8, which stage the
+// vector once for twice the rows; the 3072 x 1024 GEMV from HBM in a chain of launches:
+// 2.38 -> 2.29 us, with 2, 6, 12 or 16 waves or two row pairs per wave slower);
+// K = 2048 -> 2 teams of 2; K = 3072 -> 2 teams of 3 (384 threads).
+template <int KS, int XM>
 constexpr int nwb_of() {
-  return KS == 3 ? 6 : 4;
+  return KS == 3 ? 6 : (KS == 1 && XM == X_F16) ? 8 : 4;
 }
 
 template <int KS, int XM, int XP, int EP, bool PAIR>
@@ -674,7 +676,7 @@ int launch_sel(const GemvArgs& a, hipStream_t st) {
     // (same waves in total) cut that re-read
     return launch_inst<KS, KS * (kAttnMergeWaves / KS), XM, XP, EP, PAIR, 1>(a, st);
   } else {
-    return launch_inst<KS, nwb_of<KS>(), XM, XP, EP, PAIR, 1>(a, st);
+    return launch_inst<KS, nwb_of<KS, XM>(), XM, XP, EP, PAIR, 1>(a, st);
   }
 }
 

@@ -149,12 +149,14 @@ def teacher(c3):
     vrow = np.zeros_like(krow)
     logits, argmax, bitwise = [], [], []
     fused = torch.zeros_like(s.logits)
+    plan = s.lib.q4d_decode_plan_active(ctypes.byref(s.desc), current_stream())
+    print(f"[c3 teacher] decode plan {plan} (0: XCD-split, 1: staged)", flush=True)
     for pos in range(STEPS):
         s.step(a["feed"][pos], pos)
         if pos in BITWISE_POSITIONS:
             ref = s.logits.clone()
             s.fused_step(a["feed"][pos], pos, fused)
-            bitwise.append((pos, bool(torch.equal(ref, fused))))
+            bitwise.append((pos, bool(torch.equal(ref, fused)), float((ref - fused).abs().max())))
         torch.cuda.synchronize()
         hidden[pos] = s.trace.cpu().numpy()
         for j, li in enumerate(KV_LAYERS):
@@ -230,7 +232,7 @@ def test_teacher_forced_logits_and_argmax(c3, teacher):
 
 
 def test_fused_step_equals_layerwise_launches_bitwise(teacher):
-    assert teacher["bitwise"] and all(ok for _, ok in teacher["bitwise"]), teacher["bitwise"]
+    assert teacher["bitwise"] and all(ok for _, ok, _ in teacher["bitwise"]), teacher["bitwise"]
 
 
 def test_free_running_graph_trajectory(c3, teacher):
