@@ -621,6 +621,15 @@ int q4d_session_fixed_runner(void* runner_context, uint32_t input_token_id, uint
  * status[1]; those groups' outputs are not meaningful. */
 int q4d_quantize_q4(const void* weight, int32_t dtype, int64_t ld, int32_t rows, int32_t cols, uint8_t* packed,
                     uint16_t* scale, int32_t* status, void* stream);
+/* The same conversion for `count` matrices of one shape, dtype and row pitch (the
+ * reference converts a checkpoint's matrices one quantize_weight_q4 call each, 56_...:241-291):
+ * weights[i], packed[i], scales[i] are device pointers as in q4d_quantize_q4, passed in HOST
+ * arrays of count entries.  Up to 64 matrices go in one launch (more are split into launches
+ * of 64); the codes and scales equal count separate q4d_quantize_q4 calls bit for bit, and
+ * status[0] / status[1] receive the bad-group counts summed over all the matrices. */
+int q4d_quantize_q4_batch(const void* const* weights, int32_t dtype, int64_t ld, int32_t rows, int32_t cols,
+                          int32_t count, uint8_t* const* packed, uint16_t* const* scales, int32_t* status,
+                          void* stream);
 
 /* ---- diagnostics --------------------------------------------------------------
  * No counterpart in the reference; for measurement.  Launches n dependent kernels on

@@ -186,6 +186,7 @@ SIGNATURES = {
     "q4d_fixed_embedding": ([POINTER(Q4dMatrix), _P, c_int32, _P, _P], c_int32),
     "q4d_fixed_q4_gemv": ([POINTER(Q4dMatrix), _P, _P, _P, _P], c_int32),
     "q4d_quantize_q4": ([_P, c_int32, ctypes.c_int64, c_int32, c_int32, _P, _P, _P, _P], c_int32),
+    "q4d_quantize_q4_batch": ([_P, c_int32, ctypes.c_int64, c_int32, c_int32, c_int32, _P, _P, _P, _P], c_int32),
     "q4d_fixed_decoder_layer": ([_FM, c_int32, _P, _P, _FKV, _P, _P, c_size_t, _P], c_int32),
     "q4d_fixed_run_one_token": ([_FM, _P, _P, _FKV, _P, _P, _P, _P, _P, c_size_t, _P], c_int32),
     "q4d_session_default_options": ([POINTER(Q4dSessionOptions)], None),

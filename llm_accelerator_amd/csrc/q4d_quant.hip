@@ -27,6 +27,7 @@
 // codes equal numpy's bit for bit with one multiply instead of one division per element
 // (no fast-math in this build).
 #include <math.h>
+#include <string.h>
 
 #include <algorithm>
 
@@ -245,24 +246,64 @@ __global__ __launch_bounds__(256) void quantize_q4_kernel(const QuantArgs a, uin
   add_status(a.status, 1, nf_total);
 }
 
-}  // namespace
-}  // namespace q4d
+// Several matrices of one shape per launch: blockIdx.y picks the matrix, whose pointers
+// come from the kernel-argument block (read through the kernarg segment pointer, so the
+// runtime index does not copy the block to scratch); within a matrix the work is that of
+// quantize_q4_kernel, so the codes are the same bit for bit.
+constexpr int kQuantBatchMax = 64;
 
-using namespace q4d;
+struct QuantBatchArgs {
+  QuantArgs g;  // the shared geometry (its w / packed / scale unused)
+  const void* w[kQuantBatchMax];
+  uint8_t* packed[kQuantBatchMax];
+  uint16_t* scale[kQuantBatchMax];
+};
 
-extern "C" int q4d_quantize_q4(const void* weight, int32_t dtype, int64_t ld, int32_t rows, int32_t cols,
-                               uint8_t* packed, uint16_t* scale, int32_t* status, void* stream) {
-  if (!weight || !packed || !scale || !status) return Q4D_ERR_NULL;
+template <bool BF16>
+__global__ __launch_bounds__(256) void quantize_q4_batch_kernel(const QuantBatchArgs args, uint32_t batches) {
+  typedef __attribute__((address_space(4))) const QuantBatchArgs* KernargPtr;
+  const KernargPtr P = (KernargPtr)__builtin_amdgcn_kernarg_segment_ptr();
+  const int m = blockIdx.y;
+  QuantArgs a = args.g;  // fixed offsets: read as kernel arguments
+  a.w = P->w[m];
+  a.packed = P->packed[m];
+  a.scale = P->scale[m];
+  const int lane = threadIdx.x & 63;
+  const uint32_t first = blockIdx.x * 4 + (threadIdx.x >> 6), stride = gridDim.x * 4;
+  int ovf_total = 0, nf_total = 0;
+  u32x4 cur[kQuantChunks][2], nxt[kQuantChunks][2];
+  long long cur_off[kQuantChunks], nxt_off[kQuantChunks];
+  if (first < batches) {
+#pragma unroll
+    for (int c = 0; c < kQuantChunks; ++c) load_chunk<BF16>(a, first * kQuantChunks + c, lane, cur[c], cur_off[c]);
+  }
+  for (uint32_t b = first; b < batches; b += stride) {
+    const uint32_t nb = b + stride;
+    if (nb < batches) {
+#pragma unroll
+      for (int c = 0; c < kQuantChunks; ++c) load_chunk<BF16>(a, nb * kQuantChunks + c, lane, nxt[c], nxt_off[c]);
+    }
+#pragma unroll
+    for (int c = 0; c < kQuantChunks; ++c)
+      quantize_chunk<BF16>(a, b * kQuantChunks + c, lane, cur[c], cur_off[c], ovf_total, nf_total);
+#pragma unroll
+    for (int c = 0; c < kQuantChunks; ++c) {
+      cur[c][0] = nxt[c][0];
+      cur[c][1] = nxt[c][1];
+      cur_off[c] = nxt_off[c];
+    }
+  }
+  add_status(a.status, 0, ovf_total);
+  add_status(a.status, 1, nf_total);
+}
+
+// Checks shared by both entry points; fills the geometry of a (not its pointers).
+int quant_geometry(int32_t dtype, int64_t ld, int32_t rows, int32_t cols, QuantArgs& a, long long& batches) {
   if (dtype != Q4D_F32 && dtype != Q4D_BF16) return Q4D_ERR_DTYPE;
   if (rows <= 0 || cols <= 0 || cols % 64 || ld < cols) return Q4D_ERR_SHAPE;
   const size_t esz = dtype == Q4D_F32 ? 4 : 2;
-  // 16-byte loads (rows 16-byte aligned); 8-byte (bf16) / 4-byte (fp32) packed stores
-  if (!aligned(weight, 16) || (ld * (int64_t)esz) % 16 || !aligned(packed, dtype == Q4D_BF16 ? 8 : 4) ||
-      !aligned(scale, 2) ||
-      !aligned(status, 4))
-    return Q4D_ERR_BAD_ADDR;
-  QuantArgs a;
-  a.w = weight;
+  if ((ld * (int64_t)esz) % 16) return Q4D_ERR_BAD_ADDR;  // 16-byte aligned rows
+  memset(&a, 0, sizeof(a));
   a.ld = ld;
   a.rows = rows;
   a.cols = cols;
@@ -278,12 +319,34 @@ extern "C" int q4d_quantize_q4(const void* weight, int32_t dtype, int64_t ld, in
     a.sh1 = l < 1 ? l : 1;
     a.sh2 = l > 1 ? l - 1 : 0;
   }
+  const int per_chunk = dtype == Q4D_F32 ? 8 : 16;  // groups per 64-lane chunk
+  const long long chunks = ((long long)a.groups + per_chunk - 1) / per_chunk;
+  batches = (chunks + kQuantChunks - 1) / kQuantChunks;
+  return Q4D_OK;
+}
+
+// 16-byte loads; 8-byte (bf16) / 4-byte (fp32) packed stores
+bool quant_ptrs_ok(const void* w, int32_t dtype, const uint8_t* packed, const uint16_t* scale) {
+  return aligned(w, 16) && aligned(packed, dtype == Q4D_BF16 ? 8 : 4) && aligned(scale, 2);
+}
+
+}  // namespace
+}  // namespace q4d
+
+using namespace q4d;
+
+extern "C" int q4d_quantize_q4(const void* weight, int32_t dtype, int64_t ld, int32_t rows, int32_t cols,
+                               uint8_t* packed, uint16_t* scale, int32_t* status, void* stream) {
+  if (!weight || !packed || !scale || !status) return Q4D_ERR_NULL;
+  QuantArgs a;
+  long long batches = 0;
+  int rc = quant_geometry(dtype, ld, rows, cols, a, batches);
+  if (rc) return rc;
+  if (!quant_ptrs_ok(weight, dtype, packed, scale) || !aligned(status, 4)) return Q4D_ERR_BAD_ADDR;
+  a.w = weight;
   a.packed = packed;
   a.scale = scale;
   a.status = status;
-  const int per_chunk = dtype == Q4D_F32 ? 8 : 16;  // groups per 64-lane chunk
-  const long long chunks = ((long long)a.groups + per_chunk - 1) / per_chunk;
-  const long long batches = (chunks + kQuantChunks - 1) / kQuantChunks;
   // enough waves to fill every SIMD several times over; each loops over its batches
   const long long blocks = std::min<long long>((batches + 3) / 4, 4096);
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
@@ -292,4 +355,40 @@ extern "C" int q4d_quantize_q4(const void* weight, int32_t dtype, int64_t ld, in
   else
     hipLaunchKernelGGL(quantize_q4_kernel<true>, dim3((unsigned)blocks), dim3(256), 0, st, a, (uint32_t)batches);
   return check_launch();
+}
+
+extern "C" int q4d_quantize_q4_batch(const void* const* weights, int32_t dtype, int64_t ld, int32_t rows,
+                                     int32_t cols, int32_t count, uint8_t* const* packed, uint16_t* const* scales,
+                                     int32_t* status, void* stream) {
+  if (!weights || !packed || !scales || !status) return Q4D_ERR_NULL;
+  if (count <= 0) return Q4D_ERR_SHAPE;
+  QuantBatchArgs A;
+  long long batches = 0;
+  int rc = quant_geometry(dtype, ld, rows, cols, A.g, batches);
+  if (rc) return rc;
+  if (!aligned(status, 4)) return Q4D_ERR_BAD_ADDR;
+  for (int i = 0; i < count; ++i) {
+    if (!weights[i] || !packed[i] || !scales[i]) return Q4D_ERR_NULL;
+    if (!quant_ptrs_ok(weights[i], dtype, packed[i], scales[i])) return Q4D_ERR_BAD_ADDR;
+  }
+  A.g.status = status;
+  // the grid-stride share of one matrix: up to 4096 blocks spread over the matrices of a launch
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  for (int i0 = 0; i0 < count; i0 += kQuantBatchMax) {
+    const int n = std::min(kQuantBatchMax, count - i0);
+    for (int k = 0; k < kQuantBatchMax; ++k) {
+      const int i = i0 + (k < n ? k : 0);  // unused slots repeat the first matrix, never read
+      A.w[k] = weights[i];
+      A.packed[k] = packed[i];
+      A.scale[k] = scales[i];
+    }
+    const long long bx = std::max<long long>(1, std::min<long long>((batches + 3) / 4, 4096 / n));
+    const dim3 grid((unsigned)bx, (unsigned)n);
+    if (dtype == Q4D_F32)
+      hipLaunchKernelGGL(quantize_q4_batch_kernel<false>, grid, dim3(256), 0, st, A, (uint32_t)batches);
+    else
+      hipLaunchKernelGGL(quantize_q4_batch_kernel<true>, grid, dim3(256), 0, st, A, (uint32_t)batches);
+    if ((rc = check_launch())) return rc;
+  }
+  return Q4D_OK;
 }

@@ -15,6 +15,7 @@ from the HF model in fp32 (``56_...:241-291``, ``as_float32``).
 
 from __future__ import annotations
 
+import ctypes
 import json
 from pathlib import Path
 
@@ -36,11 +37,9 @@ def _unpack(packed: torch.Tensor, cols: int) -> torch.Tensor:
     return torch.where(q >= 8, q - 16, q)
 
 
-def quantize_weight_q4(weight: torch.Tensor, return_codes: bool = True):
-    """Q4 quantisation of a 2-D fp32 / bf16 matrix on the GPU -> (packed uint8 [N, K/2],
-    scale uint16 [N, K/64], q int8 [N, K] or None), device tensors.  Raises ValueError as
-    the reference does: not 2-D, K not a multiple of 64, or a scale that does not fit
-    Q2.14 (absmax above ~28, or a non-finite weight)."""
+def _prepare(weight) -> tuple:
+    """(device matrix with 16-byte aligned rows, rows, cols, Q4D dtype), with the reference's
+    ValueErrors for the shape."""
     if not isinstance(weight, torch.Tensor):
         weight = torch.from_numpy(np.ascontiguousarray(weight, dtype=np.float32))
     if weight.dim() != 2:
@@ -56,17 +55,62 @@ def quantize_weight_q4(weight: torch.Tensor, return_codes: bool = True):
     w = weight.to(dev)
     if w.stride(1) != 1 or w.stride(0) < cols or (w.stride(0) * w.element_size()) % 16 or w.data_ptr() % 16:
         w = w.contiguous()   # the kernel reads 16-byte aligned rows
-    packed = torch.empty(rows, cols // 2, dtype=torch.uint8, device=dev)
-    scale = torch.empty(rows, cols // GROUP_SIZE, dtype=torch.uint16, device=dev)
-    status = torch.zeros(2, dtype=torch.int32, device=dev)
-    dtype = Q4D_F32 if w.dtype == torch.float32 else Q4D_BF16
-    check(_lib.load().q4d_quantize_q4(w.data_ptr(), dtype, w.stride(0), rows, cols, packed.data_ptr(),
-                                      scale.data_ptr(), status.data_ptr(), current_stream()), "q4d_quantize_q4")
+    return w, rows, cols, (Q4D_F32 if w.dtype == torch.float32 else Q4D_BF16)
+
+
+def _raise_on_status(status: torch.Tensor) -> None:
     overflow, nonfinite = status.tolist()
     if overflow or nonfinite:
         raise ValueError(f"Q4 scale does not fit unsigned 16-bit Q2.14 storage ({overflow} groups with absmax "
                          f"too large, {nonfinite} groups with non-finite values)")
+
+
+def quantize_weight_q4(weight: torch.Tensor, return_codes: bool = True):
+    """Q4 quantisation of a 2-D fp32 / bf16 matrix on the GPU -> (packed uint8 [N, K/2],
+    scale uint16 [N, K/64], q int8 [N, K] or None), device tensors.  Raises ValueError as
+    the reference does: not 2-D, K not a multiple of 64, or a scale that does not fit
+    Q2.14 (absmax above ~28, or a non-finite weight)."""
+    w, rows, cols, dtype = _prepare(weight)
+    dev = w.device
+    packed = torch.empty(rows, cols // 2, dtype=torch.uint8, device=dev)
+    scale = torch.empty(rows, cols // GROUP_SIZE, dtype=torch.uint16, device=dev)
+    status = torch.zeros(2, dtype=torch.int32, device=dev)
+    check(_lib.load().q4d_quantize_q4(w.data_ptr(), dtype, w.stride(0), rows, cols, packed.data_ptr(),
+                                      scale.data_ptr(), status.data_ptr(), current_stream()), "q4d_quantize_q4")
+    _raise_on_status(status)
     return packed, scale, (_unpack(packed, cols) if return_codes else None)
+
+
+def quantize_weights_q4(weights) -> list:
+    """quantize_weight_q4 over a list of matrices -> [(packed, scale)] in the same order,
+    the same codes bit for bit; matrices of one shape, dtype and row pitch are converted
+    by one launch each (q4d_quantize_q4_batch).  Raises the same ValueErrors, naming the
+    first failing matrix's index."""
+    prepared = [_prepare(w) for w in weights]
+    out = [None] * len(prepared)
+    groups = {}
+    for i, (w, rows, cols, dtype) in enumerate(prepared):
+        groups.setdefault((rows, cols, dtype, w.stride(0), w.device), []).append(i)
+    lib = _lib.load()
+    for (rows, cols, dtype, ld, dev), idx in groups.items():
+        packed = [torch.empty(rows, cols // 2, dtype=torch.uint8, device=dev) for _ in idx]
+        scale = [torch.empty(rows, cols // GROUP_SIZE, dtype=torch.uint16, device=dev) for _ in idx]
+        status = torch.zeros(2, dtype=torch.int32, device=dev)
+        n = len(idx)
+        wp = (ctypes.c_void_p * n)(*[prepared[i][0].data_ptr() for i in idx])
+        pp = (ctypes.c_void_p * n)(*[t.data_ptr() for t in packed])
+        sp = (ctypes.c_void_p * n)(*[t.data_ptr() for t in scale])
+        check(lib.q4d_quantize_q4_batch(wp, dtype, ld, rows, cols, n, pp, sp, status.data_ptr(), current_stream()),
+              "q4d_quantize_q4_batch")
+        if status.any():  # find the first failing matrix of the group, as one call each would
+            for i in idx:
+                try:
+                    quantize_weight_q4(prepared[i][0], return_codes=False)
+                except ValueError as e:
+                    raise ValueError(f"matrix {i}: {e}") from None
+        for k, i in enumerate(idx):
+            out[i] = (packed[k], scale[k])
+    return out
 
 
 # Hugging Face Qwen3 tensor names (transformers' Qwen3ForCausalLM state dict).
@@ -136,21 +180,23 @@ def convert_checkpoint(path: str | Path, cfg: Qwen3Config | None = None, device=
                 shapes[name] = tuple(h.get_slice(name).get_shape())
         check_checkpoint(shapes, cfg)
 
-        def q4(name):
-            packed, scale, _ = quantize_weight_q4(where[name].get_tensor(name).to(device), return_codes=False)
-            return packed.cpu().numpy(), scale.cpu().numpy()
-
         def vec(name):
             return where[name].get_tensor(name).float().numpy().astype(np.float32)
 
+        # every matrix on the device, then one grouped conversion (one launch per shape)
+        names = [f"model.layers.{li}.{v}.weight" for li in range(cfg.num_hidden_layers) for v in _LAYER_MATS.values()]
+        names.append("model.embed_tokens.weight")
+        q = quantize_weights_q4([where[n].get_tensor(n).to(device) for n in names])
+        q4 = {n: (p.cpu().numpy(), sc.cpu().numpy()) for n, (p, sc) in zip(names, q)}
+        del q
         layers = []
         for li in range(cfg.num_hidden_layers):
             pre = f"model.layers.{li}."
-            L = {k: q4(pre + v + ".weight") for k, v in _LAYER_MATS.items()}
+            L = {k: q4[pre + v + ".weight"] for k, v in _LAYER_MATS.items()}
             L.update({k: vec(pre + v + ".weight") for k, v in _LAYER_VECS.items()})
             layers.append(L)
-        host = {"layers": layers, "embed_tokens": q4("model.embed_tokens.weight"), "norm": vec("model.norm.weight")}
+        host = {"layers": layers, "embed_tokens": q4["model.embed_tokens.weight"], "norm": vec("model.norm.weight")}
     return cfg, host
 
 
-__all__ = ["quantize_weight_q4", "convert_checkpoint", "expected_tensors", "check_checkpoint", "checkpoint_files"]
+__all__ = ["quantize_weight_q4", "quantize_weights_q4", "convert_checkpoint", "expected_tensors", "check_checkpoint", "checkpoint_files"]

@@ -267,3 +267,22 @@ def test_launch_chain_validates_on_host(lib):
         y, _b = arr(*bad_gy)
         b, _c = arr(*bad_bl)
         assert f(x, y, b, 2, FAKE, None) == -11, (bad_gx, bad_gy, bad_bl)
+
+
+def test_quantize_batch_validates_on_host(lib):
+    """q4d_quantize_q4_batch rejects bad arguments before any launch."""
+    f = lib.q4d_quantize_q4_batch
+    arr = lambda *v: (ctypes.c_void_p * len(v))(*v)  # noqa: E731
+    good = arr(FAKE, FAKE + 4096)
+    # count, shapes, dtype
+    assert f(good, 2, 1024, 4, 1024, 0, good, good, FAKE, None) == -11
+    assert f(good, 2, 1024, 4, 1000, 2, good, good, FAKE, None) == -11   # cols % 64
+    assert f(good, 2, 512, 4, 1024, 2, good, good, FAKE, None) == -11    # ld < cols
+    assert f(good, 5, 1024, 4, 1024, 2, good, good, FAKE, None) == -13
+    # null arrays or entries, misaligned matrices or outputs
+    assert f(None, 2, 1024, 4, 1024, 2, good, good, FAKE, None) == -7
+    assert f(good, 2, 1024, 4, 1024, 2, good, good, None, None) == -7
+    assert f(arr(FAKE, None), 2, 1024, 4, 1024, 2, good, good, FAKE, None) == -7
+    assert f(arr(FAKE, FAKE + 8), 2, 1024, 4, 1024, 2, good, good, FAKE, None) == -4
+    assert f(good, 2, 1024, 4, 1024, 2, arr(FAKE, FAKE + 4), good, FAKE, None) == -4
+    assert f(good, 2, 1028, 4, 1024, 2, good, good, FAKE, None) == -4    # rows not 16-byte aligned

@@ -146,3 +146,69 @@ def test_checkpoint_conversion(dev, tmp_path):
     tokens, _ = greedy_generate(build_model(cfg, host, max_ctx=16, device=dev), [5, 9], 4, use_graph=False)
     print(f"[quant] converted checkpoint decodes {tokens}", flush=True)
     assert len(tokens) == 4 and all(0 <= t < cfg.vocab_size for t in tokens)
+
+
+def _batch_call(ws, dtype_code, status):
+    """q4d_quantize_q4_batch over device matrices of one shape -> [(packed, scale)]."""
+    import ctypes
+    from llm_accelerator_amd import _lib
+    from llm_accelerator_amd.model import current_stream
+    rows, cols = ws[0].shape
+    dev = ws[0].device
+    packed = [torch.empty(rows, cols // 2, dtype=torch.uint8, device=dev) for _ in ws]
+    scale = [torch.empty(rows, cols // 64, dtype=torch.uint16, device=dev) for _ in ws]
+    n = len(ws)
+    wp = (ctypes.c_void_p * n)(*[w.data_ptr() for w in ws])
+    pp = (ctypes.c_void_p * n)(*[t.data_ptr() for t in packed])
+    sp = (ctypes.c_void_p * n)(*[t.data_ptr() for t in scale])
+    _lib.check(_lib.load().q4d_quantize_q4_batch(wp, dtype_code, ws[0].stride(0), rows, cols, n, pp, sp,
+                                                 status.data_ptr(), current_stream()), "q4d_quantize_q4_batch")
+    return list(zip(packed, scale))
+
+
+@pytest.mark.parametrize("dtype,rows,cols,count", [(torch.bfloat16, 3072, 1024, 3), (torch.bfloat16, 37, 2048, 70),
+                                                   (torch.float32, 129, 1024, 5), (torch.float32, 1, 64, 2)])
+def test_batch_equals_single_calls(dev, dtype, rows, cols, count):
+    """One launch over `count` matrices (70: two launches, 64 + 6) equals count single
+    conversions bit for bit; sampled matrices also equal the oracle."""
+    from llm_accelerator_amd._lib import Q4D_BF16, Q4D_F32
+    g = torch.Generator(device=dev).manual_seed(rows + count)
+    ws = [(torch.randn(rows, cols, device=dev, generator=g) * (0.02 * (i + 1))).to(dtype) for i in range(count)]
+    ws[0][0, :64] = 0                      # an all-zero group
+    status = torch.zeros(2, dtype=torch.int32, device=dev)
+    print(f"[quant] batch {count} x {rows}x{cols} {dtype}", flush=True)
+    got = _batch_call(ws, Q4D_BF16 if dtype == torch.bfloat16 else Q4D_F32, status)
+    assert status.tolist() == [0, 0]
+    for i, w in enumerate(ws):
+        p, s, _ = quantize_weight_q4(w, return_codes=False)
+        assert torch.equal(got[i][0], p) and torch.equal(got[i][1], s), i
+    for i in (0, count - 1):
+        w32 = ws[i][:64].float().cpu().numpy()
+        want_p, want_s, _ = o.quantize_weight_q4(w32)
+        np.testing.assert_array_equal(got[i][0][:64].cpu().numpy(), want_p)
+        np.testing.assert_array_equal(got[i][1][:64].cpu().numpy(), want_s)
+
+
+def test_batch_status_sums_and_python_errors(dev):
+    """Bad groups of several matrices add up in the one status pair; the list wrapper
+    returns the matrices in order (mixed shapes and dtypes) and names the first failing one."""
+    from llm_accelerator_amd._lib import Q4D_F32
+    from llm_accelerator_amd.quantize import quantize_weights_q4
+    rng = np.random.default_rng(11)
+    base = [(rng.standard_normal((4, 256)) * 0.1).astype(np.float32) for _ in range(4)]
+    base[1][2, 70] = 30.0                  # overflow in matrix 1
+    base[3][0, 5] = np.inf                 # non-finite in matrix 3
+    base[3][3, 200] = 40.0                 # and an overflow
+    ws = [torch.from_numpy(b).to(dev) for b in base]
+    status = torch.zeros(2, dtype=torch.int32, device=dev)
+    _batch_call(ws, Q4D_F32, status)
+    assert status.tolist() == [2, 1]
+    with pytest.raises(ValueError, match="matrix 1: Q4 scale does not fit"):
+        quantize_weights_q4(ws)
+    mixed = [torch.from_numpy((rng.standard_normal(s) * 0.05).astype(np.float32)).to(dev)
+             for s in ((8, 128), (16, 64), (8, 128), (3, 192))]
+    mixed[2] = mixed[2].to(torch.bfloat16)
+    got = quantize_weights_q4(mixed)
+    for w, (p, s) in zip(mixed, got):
+        want_p, want_s, _ = quantize_weight_q4(w, return_codes=False)
+        assert torch.equal(p, want_p) and torch.equal(s, want_s)
