@@ -86,11 +86,12 @@ def parse():
     ap.add_argument("--precision", type=int, default=2, choices=(1, 2),
                     help="fp32 activations enter the decode GEMVs as fp16 hi+lo pairs (2) or fp16 (1)")
     ap.add_argument("--no-extras", action="store_true", help="run the GEMV headline only")
-    ap.add_argument("--legs", default="decode,lm,layer,prefill,batch,fx,q4c",
+    ap.add_argument("--legs", default="decode,lm,layer,prefill,batch,fx,q4c,group",
                     help="comma list of the legs beside the GEMV headline: decode (28-layer decode), "
                          "lm (LM head alone), lmsweep (LM head over 4096..151936 rows, not by default), "
                          "layer (one decoder layer at --ctx), prefill, batch (batched decode), "
-                         "fx fixed-point (RTL-exact) layer and token, q4c float -> Q4 conversion of the model")
+                         "fx fixed-point (RTL-exact) layer and token, q4c float -> Q4 conversion of the model, "
+                         "group (the headline GEMV over 64 matrices per launch)")
     ap.add_argument("--extras", dest="legs", default=argparse.SUPPRESS, help="the same as --legs")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
@@ -677,6 +678,50 @@ def leg_q4c(lib, torch, dev, st):
     return out
 
 
+def leg_group(lib, torch, dev, st):
+    """The headline GEMV's kernel over 64 independent 3072 x 1024 matrices per launch
+    (q4d_linear_group; each matrix its own fp16 x and y).  Launches rotate over 256 copies
+    (430 MB, past the 256 MB cache): launch i reads copies 64 (i % 4) .. + 63, so every launch
+    reads weights that left the cache.  Time per launch = graph time / launches."""
+    import numpy as np
+    from llm_accelerator_amd._lib import Q4dMatrix, check
+    from llm_accelerator_amd.model import Q4Tensor, gemv_bytes, random_q4
+    G, NCOP = 64, 256
+    rng = np.random.default_rng(0)
+    packed, scale = random_q4(rng, GEMV_ROWS, GEMV_COLS)
+    P = torch.from_numpy(packed).to(dev).unsqueeze(0).repeat(NCOP, 1, 1).contiguous()
+    S = torch.from_numpy(scale).to(dev).unsqueeze(0).repeat(NCOP, 1, 1).contiguous()
+    gen = torch.Generator(device=dev).manual_seed(1)
+    X = torch.randn(NCOP, GEMV_COLS, generator=gen, device=dev).half()
+    Y = torch.empty(NCOP, GEMV_ROWS, device=dev, dtype=torch.float16)
+    sets = []
+    for r in range(NCOP // G):
+        idx = range(r * G, (r + 1) * G)
+        sets.append(((Q4dMatrix * G)(*[Q4Tensor(P[i], S[i]).descriptor() for i in idx]),
+                     (ctypes.c_void_p * G)(*[X[i].data_ptr() for i in idx]),
+                     (ctypes.c_void_p * G)(*[Y[i].data_ptr() for i in idx])))
+
+    def launch(i):
+        d, xp, yp = sets[i % len(sets)]
+        check(lib.q4d_linear_group(d, xp, 0, yp, 0, 1, G, st()), "q4d_linear_group")
+    for i in range(len(sets)):
+        launch(i)
+    torch.cuda.synchronize()
+    g = graph_of(launch, 4 * len(sets), torch)
+    g.replay()
+    us = time_graph(g, 25, torch) / (4 * len(sets)) * 1e3
+    gb = G * gemv_bytes(GEMV_ROWS, GEMV_COLS)
+    ok = bool(torch.isfinite(Y.float()).all().item())
+    out = {"workload": f"{G} independent 3072x1024 Q4 GEMVs per launch (fp16 x / y, batch 1), flushed",
+           "bytes_per_launch": gb, "us_per_launch": round(us, 3), "GBps": round(gb / us / 1e3, 1),
+           "hbm_frac": round(gb / us / 1e3 / HBM_PEAK_GBPS, 4), "finite": ok,
+           "kernel": "gemv_group_kernel<1, 8, 0, 1, 0> (the headline gemv_kernel's body per matrix)"}
+    log(f"[bench] grouped GEMV: {json.dumps(out)}")
+    del P, S, X, Y, g
+    torch.cuda.empty_cache()
+    return out
+
+
 def leg_copy(torch, dev):
     """torch's device copy of 512 MiB windows rotating over 2 GiB (past the 256 MB
     cache): read + written bytes over the time."""
@@ -719,7 +764,7 @@ def main():
     st = lambda: torch.cuda.current_stream().cuda_stream  # noqa: E731
 
     legs = set() if args.no_extras else {x.strip() for x in args.legs.split(",") if x.strip()}
-    known = {"decode", "lm", "lmsweep", "layer", "prefill", "batch", "fx", "q4c"}
+    known = {"decode", "lm", "lmsweep", "layer", "prefill", "batch", "fx", "q4c", "group"}
     if legs - known:
         sys.exit(f"unknown legs {sorted(legs - known)}")
 
@@ -756,6 +801,8 @@ def main():
         torch.cuda.empty_cache()
     if "q4c" in legs:
         extras["q4c_quantize"] = leg_q4c(lib, torch, dev, st)
+    if "group" in legs:
+        extras["gemv_group_64x3072x1024"] = leg_group(lib, torch, dev, st)
     if legs:
         extras["hbm_copy"] = leg_copy(torch, dev)
 

@@ -183,6 +183,15 @@ int q4d_read_status(const void* ws, size_t ws_bytes, const q4d_model_t* model, i
  * Supported cols: 1024, 2048, 3072; rows even. */
 int q4d_linear(const q4d_matrix_t* w, const void* x, int32_t x_dtype, void* y, int32_t y_dtype,
                int32_t batch, void* stream);
+/* No counterpart in the reference (it applies one matrix per call,
+ * manual_linear_from_weight, common.py:137-145): q4d_linear over `count` independent matrices of one shape, each with
+ * its own activations and output, up to 64 per launch: w is a host array of count
+ * descriptors (equal rows and cols), x and y host arrays of count device pointers as in
+ * q4d_linear.  Each y[i] equals q4d_linear(&w[i], x[i], ...) bit for bit.  For callers that
+ * apply many small matrices at once (expert or adapter weights), where one launch per matrix
+ * would cost more than its bytes. */
+int q4d_linear_group(const q4d_matrix_t* w, const void* const* x, int32_t x_dtype, void* const* y, int32_t y_dtype,
+                     int32_t batch, int32_t count, void* stream);
 /* y = x * rsqrt(mean(x^2) + eps) * gamma over the last dim (fp32 in). */
 int q4d_rms_norm(const float* x, const float* gamma, float eps, int32_t rows, int32_t dim,
                  void* y, int32_t y_dtype, void* stream);

@@ -136,6 +136,7 @@ SIGNATURES = {
     "q4d_diag_set_xcd_check": ([c_int32], c_int32),
     "q4d_read_status": ([_P, c_size_t, POINTER(Q4dModel), c_int32, POINTER(c_int32), _P], c_int32),
     "q4d_linear": ([POINTER(Q4dMatrix), _P, c_int32, _P, c_int32, c_int32, _P], c_int32),
+    "q4d_linear_group": ([POINTER(Q4dMatrix), _P, c_int32, _P, c_int32, c_int32, c_int32, _P], c_int32),
     "q4d_rms_norm": ([_P, _P, c_float, c_int32, c_int32, _P, c_int32, _P], c_int32),
     "q4d_qk_norm_rope": ([_P, _P, _P, c_float, c_int32, c_int32, c_int32, _P, _P, c_int32, _P, _P, _P], c_int32),
     "q4d_kv_append": ([POINTER(Q4dKVCache), c_int32, _P, _P, _P, _P, _P], c_int32),

@@ -469,6 +469,31 @@ int q4d_linear(const q4d_matrix_t* w, const void* x, int32_t x_dtype, void* y, i
                         y_dtype == Q4D_F16 ? EP_F16 : EP_F32, false, as_stream(stream));
 }
 
+int q4d_linear_group(const q4d_matrix_t* w, const void* const* x, int32_t x_dtype, void* const* y, int32_t y_dtype,
+                     int32_t batch, int32_t count, void* stream) {
+  if (!w || !x || !y) return Q4D_ERR_NULL;
+  if (count <= 0 || batch <= 0) return Q4D_ERR_SHAPE;
+  if (x_dtype != Q4D_F16 && x_dtype != Q4D_F32) return Q4D_ERR_DTYPE;
+  if (y_dtype != Q4D_F16 && y_dtype != Q4D_F32) return Q4D_ERR_DTYPE;
+  constexpr int kChunk = 64;  // descriptors unpacked per step
+  const uint8_t* wp[kChunk];
+  const uint16_t* sp[kChunk];
+  for (int i0 = 0; i0 < count; i0 += kChunk) {
+    const int n = count - i0 < kChunk ? count - i0 : kChunk;
+    for (int k = 0; k < n; ++k) {
+      const int rc = check_matrix(&w[i0 + k], w[0].rows, w[0].cols);
+      if (rc) return rc;
+      wp[k] = w[i0 + k].w;
+      sp[k] = w[i0 + k].s;
+    }
+    const int rc = launch_gemv_group(w[0].rows, w[0].cols, batch, wp, sp, x + i0, y + i0, n,
+                                     x_dtype == Q4D_F16 ? X_F16 : X_F32, x_dtype == Q4D_F16 ? 1 : g_act_precision,
+                                     y_dtype == Q4D_F16 ? EP_F16 : EP_F32, as_stream(stream));
+    if (rc) return rc;
+  }
+  return Q4D_OK;
+}
+
 int q4d_rms_norm(const float* x, const float* gamma, float eps, int32_t rows, int32_t dim, void* y,
                  int32_t y_dtype, void* stream) {
   if (!x || !gamma || !y) return Q4D_ERR_NULL;

@@ -59,6 +59,7 @@
 // Weights and scales are read with non-temporal loads, and a wave's issue
 // priority falls as it progresses, so the waves of a SIMD finish together.
 #include <math.h>
+#include <string.h>
 
 #include "q4d_device.h"
 #include "q4d_internal.h"
@@ -238,7 +239,7 @@ __device__ __forceinline__ void attn_finish(const GemvArgs& a, int bat, const At
 
 // ---- one-shot kernel ----------------------------------------------------------
 template <int KS, int NWB, int XM, int XP, int EP, bool PAIR, int U>
-__global__ __launch_bounds__(NWB * 64) void gemv_kernel(const GemvArgs a) {
+__device__ __forceinline__ void gemv_body(const GemvArgs& a) {
   constexpr int K = KS * kSlice;
   constexpr int TEAMS = NWB / KS;
   static_assert(NWB % KS == 0, "a block holds whole teams");
@@ -358,6 +359,45 @@ __global__ __launch_bounds__(NWB * 64) void gemv_kernel(const GemvArgs a) {
       }
     }
   }
+}
+
+template <int KS, int NWB, int XM, int XP, int EP, bool PAIR, int U>
+__global__ __launch_bounds__(NWB * 64) void gemv_kernel(const GemvArgs a) {
+  gemv_body<KS, NWB, XM, XP, EP, PAIR, U>(a);
+}
+
+// Grouped plain linear: blockIdx.z picks one of up to kGemvGroupMax independent matrices of
+// one shape, each with its own activations and output (the pointers sit in the argument
+// block and are read through the kernarg segment pointer, so the runtime index does not
+// copy the block to scratch); within a matrix the work is gemv_kernel's, so each output
+// equals a launch of its own bit for bit.
+constexpr int kGemvGroupMax = 64;
+
+struct GemvGroupArgs {
+  GemvArgs a;  // the shared geometry (segment 0 only; its pointers unused)
+  const uint8_t* w[kGemvGroupMax];
+  const uint16_t* s[kGemvGroupMax];
+  const void* x[kGemvGroupMax];
+  void* y[kGemvGroupMax];
+};
+
+// Row pairs per wave of the grouped kernel: a launch over many matrices streams, so each
+// wave takes several pairs (the activation staging and the reduction are per block).
+constexpr int kGroupU = 4;
+
+template <int KS, int NWB, int XM, int XP, int EP>
+__global__ __launch_bounds__(NWB * 64) void gemv_group_kernel(const GemvGroupArgs G) {
+  typedef __attribute__((address_space(4))) const GemvGroupArgs* KernargPtr;
+  const KernargPtr P = (KernargPtr)__builtin_amdgcn_kernarg_segment_ptr();
+  const int g = blockIdx.z;
+  GemvArgs a = G.a;
+  const uint8_t* w = P->w[g];
+  const uint16_t* sc = P->s[g];
+  a.w[0] = a.w[1] = a.w[2] = w;
+  a.s[0] = a.s[1] = a.s[2] = sc;
+  a.x = P->x[g];
+  a.y = P->y[g];
+  gemv_body<KS, NWB, XM, XP, EP, false, kGroupU>(a);
 }
 
 // ---- streaming LM-head kernel -------------------------------------------------
@@ -680,6 +720,27 @@ int launch_sel(const GemvArgs& a, hipStream_t st) {
   }
 }
 
+template <int KS, int XM, int XP, int EP>
+int launch_group_inst(const GemvGroupArgs& G, int count, hipStream_t stream) {
+  constexpr int NWB = nwb_of<KS, XM>(), TEAMS = NWB / KS;
+  const int NP = G.a.rows / 2;
+  const int blocks = (NP + TEAMS * kGroupU - 1) / (TEAMS * kGroupU);
+  hipLaunchKernelGGL((gemv_group_kernel<KS, NWB, XM, XP, EP>), dim3(blocks, G.a.batch, count), dim3(NWB * 64), 0,
+                     stream, G);
+  return check_launch();
+}
+
+template <int KS>
+int dispatch_group_k(const GemvGroupArgs& G, int count, int xm, int xp, int ep, hipStream_t st) {
+  if (xm == X_F16) return ep == EP_F16 ? launch_group_inst<KS, X_F16, 1, EP_F16>(G, count, st)
+                                       : launch_group_inst<KS, X_F16, 1, EP_F32>(G, count, st);
+  if (xm == X_F32 && xp == 1) return ep == EP_F16 ? launch_group_inst<KS, X_F32, 1, EP_F16>(G, count, st)
+                                                  : launch_group_inst<KS, X_F32, 1, EP_F32>(G, count, st);
+  if (xm == X_F32 && xp == 2) return ep == EP_F16 ? launch_group_inst<KS, X_F32, 2, EP_F16>(G, count, st)
+                                                  : launch_group_inst<KS, X_F32, 2, EP_F32>(G, count, st);
+  return Q4D_ERR_SHAPE;
+}
+
 template <int KS>
 int dispatch_k(const GemvArgs& a, int xm, int xp, int ep, bool pair, hipStream_t st) {
   // primitive linear: fp16 / fp32 in, fp16 / fp32 out
@@ -770,6 +831,44 @@ int launch_gemv_xp(const GemvArgs& a, int xm, int xp, int ep, bool pair, hipStre
     case 2048: return dispatch_k<2>(b, xm, xp, ep, pair, st);
     default: return dispatch_k<3>(b, xm, xp, ep, pair, st);
   }
+}
+
+int launch_gemv_group(int rows, int cols, int batch, const uint8_t* const* w, const uint16_t* const* s,
+                      const void* const* x, void* const* y, int count, int xm, int xp, int ep, hipStream_t st) {
+  if (cols != 1024 && cols != 2048 && cols != 3072) return Q4D_ERR_SHAPE;
+  if (rows <= 0 || (rows % 2) || batch <= 0 || batch > 65535 || count <= 0) return Q4D_ERR_SHAPE;
+  if ((long long)rows * (cols / 2) >= (1ll << 31)) return Q4D_ERR_SHAPE;  // 32-bit buffer sizes
+  if (!(xm == X_F16 && xp == 1) && !(xm == X_F32 && (xp == 1 || xp == 2))) return Q4D_ERR_DTYPE;
+  if (ep != EP_F16 && ep != EP_F32) return Q4D_ERR_DTYPE;
+  for (int i = 0; i < count; ++i) {
+    if (!w[i] || !s[i] || !x[i] || !y[i]) return Q4D_ERR_NULL;
+    if (!aligned(w[i], 16) || !aligned(s[i], 4) || !aligned(x[i], 16)) return Q4D_ERR_BAD_ADDR;
+  }
+  GemvGroupArgs G;
+  memset(&G, 0, sizeof(G));
+  G.a.rows = rows;
+  G.a.cols = cols;
+  G.a.batch = batch;
+  G.a.nseg = 1;
+  G.a.seg_end[0] = G.a.seg_end[1] = G.a.seg_end[2] = rows;  // segments 1, 2 empty
+  for (int i0 = 0; i0 < count; i0 += kGemvGroupMax) {
+    const int n = count - i0 < kGemvGroupMax ? count - i0 : kGemvGroupMax;
+    for (int k = 0; k < kGemvGroupMax; ++k) {
+      const int i = i0 + (k < n ? k : 0);  // unused slots repeat the first matrix, never read
+      G.w[k] = w[i];
+      G.s[k] = s[i];
+      G.x[k] = x[i];
+      G.y[k] = y[i];
+    }
+    int rc;
+    switch (cols) {
+      case 1024: rc = dispatch_group_k<1>(G, n, xm, xp, ep, st); break;
+      case 2048: rc = dispatch_group_k<2>(G, n, xm, xp, ep, st); break;
+      default: rc = dispatch_group_k<3>(G, n, xm, xp, ep, st); break;
+    }
+    if (rc) return rc;
+  }
+  return Q4D_OK;
 }
 
 int launch_gemv(const GemvArgs& a, int xmode, int epmode, bool pair, hipStream_t stream) {

@@ -194,6 +194,10 @@ struct GemvArgs {
 
 // Validates geometry, picks the kernel instance and launches.  Returns Q4D_*.
 int launch_gemv(const GemvArgs& a, int xmode, int epmode, bool pair, hipStream_t stream);
+// count independent [rows, cols] matrices with their own activations and outputs, up to 64
+// per launch (plain linear modes only: X_F16 / X_F32 in, EP_F16 / EP_F32 out).
+int launch_gemv_group(int rows, int cols, int batch, const uint8_t* const* w, const uint16_t* const* s,
+                      const void* const* x, void* const* y, int count, int xm, int xp, int ep, hipStream_t st);
 
 // ---- other launchers ---------------------------------------------------------
 int launch_rms_norm(const float* x, const float* gamma, float eps, int rows, int dim, void* y,

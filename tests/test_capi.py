@@ -286,3 +286,20 @@ def test_quantize_batch_validates_on_host(lib):
     assert f(arr(FAKE, FAKE + 8), 2, 1024, 4, 1024, 2, good, good, FAKE, None) == -4
     assert f(good, 2, 1024, 4, 1024, 2, arr(FAKE, FAKE + 4), good, FAKE, None) == -4
     assert f(good, 2, 1028, 4, 1024, 2, good, good, FAKE, None) == -4    # rows not 16-byte aligned
+
+
+def test_linear_group_validates_on_host(lib):
+    """q4d_linear_group rejects bad arguments before any launch."""
+    f = lib.q4d_linear_group
+    ptrs = (ctypes.c_void_p * 2)(FAKE, FAKE + 4096)
+    mats = (Q4dMatrix * 2)(Q4dMatrix(FAKE, FAKE, 256, 1024), Q4dMatrix(FAKE, FAKE, 256, 1024))
+    assert f(mats, ptrs, 1, ptrs, 1, 1, 0, None) == -11        # count
+    assert f(mats, ptrs, 1, ptrs, 1, 0, 2, None) == -11        # batch
+    assert f(mats, ptrs, 7, ptrs, 1, 1, 2, None) == -13        # x dtype
+    assert f(None, ptrs, 1, ptrs, 1, 1, 2, None) == -7
+    odd = (Q4dMatrix * 2)(Q4dMatrix(FAKE, FAKE, 256, 1024), Q4dMatrix(FAKE, FAKE, 258, 1024))
+    assert f(odd, ptrs, 1, ptrs, 1, 1, 2, None) == -3          # shapes differ
+    bad = (Q4dMatrix * 2)(Q4dMatrix(FAKE, FAKE, 256, 1000), Q4dMatrix(FAKE, FAKE, 256, 1000))
+    assert f(bad, ptrs, 1, ptrs, 1, 1, 2, None) == -11         # K not 1024 / 2048 / 3072
+    assert f(mats, (ctypes.c_void_p * 2)(FAKE, FAKE + 8), 1, ptrs, 1, 1, 2, None) == -4   # x alignment
+    assert f(mats, (ctypes.c_void_p * 2)(FAKE, None), 1, ptrs, 1, 1, 2, None) == -7

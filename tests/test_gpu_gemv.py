@@ -151,3 +151,41 @@ def test_lm_head_repeatable_and_counter_resets(dev):
     top = np.argsort(ref)[-2:]
     if ref[top[1]] - ref[top[0]] > 1e-3:
         assert res[0][0] == int(top[1])
+
+
+@pytest.mark.parametrize("k,xdtype,ydtype,batch,count", [(1024, torch.float16, Q4D_F16, 1, 70),
+                                                         (2048, torch.float32, Q4D_F32, 3, 5),
+                                                         (3072, torch.float32, Q4D_F16, 2, 9),
+                                                         (1024, torch.float32, Q4D_F32, 1, 64)])
+def test_linear_group_equals_single_calls(dev, k, xdtype, ydtype, batch, count):
+    """q4d_linear_group over `count` matrices (70: launches of 64 + 6), each with its own
+    x and y, equals one q4d_linear call per matrix bit for bit; one matrix also meets the
+    oracle's accumulation bound."""
+    import ctypes
+    from llm_accelerator_amd import _lib
+    from llm_accelerator_amd.model import current_stream
+    rng = np.random.default_rng(k + count)
+    n = 2 * (96 + count)  # rows: even, not a multiple of the block's rows
+    mats = [q4(rng.integers(0, 256, size=(n, k // 2), dtype=np.uint8),
+               rng.integers(50, 3000, size=(n, k // 64)).astype(np.uint16), dev) for _ in range(count)]
+    xs = [torch.randn(batch, k, device=dev, dtype=torch.float32).to(xdtype) for _ in range(count)]
+    ydt = torch.float16 if ydtype == Q4D_F16 else torch.float32
+    ys = [torch.full((batch, n), float('nan'), device=dev, dtype=ydt) for _ in range(count)]
+    descs = (_lib.Q4dMatrix * count)(*[m.descriptor() for m in mats])
+    xp = (ctypes.c_void_p * count)(*[x.data_ptr() for x in xs])
+    yp = (ctypes.c_void_p * count)(*[y.data_ptr() for y in ys])
+    print(f"[gemv] group {count} x {n}x{k} batch {batch}", flush=True)
+    xcode = Q4D_F16 if xdtype == torch.float16 else Q4D_F32
+    _lib.check(_lib.load().q4d_linear_group(descs, xp, xcode, yp, ydtype, batch, count, current_stream()),
+               "q4d_linear_group")
+    for i in range(count):
+        want = linear(mats[i], xs[i], ydtype)
+        assert torch.equal(ys[i], want), i
+    W = o.dequantize_q4(mats[0].packed.cpu().numpy(), mats[0].scale.cpu().numpy(), dtype=np.float64)
+    x0 = xs[0][0].float().cpu().numpy()
+    ref = W @ x0.astype(np.float64)
+    y0 = ys[0][0].float().cpu().numpy()
+    half_ulp = np.abs(ref) * 2.0 ** -11 + 2.0 ** -25 if ydtype == Q4D_F16 else 0.0
+    # fp32 activations enter as fp16 hi + lo halves (~22 bits): 2^-21 relative each
+    xerr = 2.0 ** -21 * abs_dot_bound(W, x0) if xdtype == torch.float32 else 0.0
+    assert np.all(np.abs(y0 - ref) <= half_ulp + xerr + ACC * abs_dot_bound(W, x0))
