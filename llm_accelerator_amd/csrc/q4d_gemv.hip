@@ -384,6 +384,7 @@ struct GemvGroupArgs {
 // Row pairs per wave of the grouped kernel: a launch over many matrices streams, so each
 // wave takes several pairs (the activation staging and the reduction are per block).
 constexpr int kGroupU = 4;
+constexpr int kGroupWaves = 8;  // waves per block at K = 1024
 
 template <int KS, int NWB, int XM, int XP, int EP>
 __global__ __launch_bounds__(NWB * 64) void gemv_group_kernel(const GemvGroupArgs G) {
@@ -722,7 +723,7 @@ int launch_sel(const GemvArgs& a, hipStream_t st) {
 
 template <int KS, int XM, int XP, int EP>
 int launch_group_inst(const GemvGroupArgs& G, int count, hipStream_t stream) {
-  constexpr int NWB = nwb_of<KS, XM>(), TEAMS = NWB / KS;
+  constexpr int NWB = KS == 1 ? kGroupWaves : nwb_of<KS, XM>(), TEAMS = NWB / KS;
   const int NP = G.a.rows / 2;
   const int blocks = (NP + TEAMS * kGroupU - 1) / (TEAMS * kGroupU);
   hipLaunchKernelGGL((gemv_group_kernel<KS, NWB, XM, XP, EP>), dim3(blocks, G.a.batch, count), dim3(NWB * 64), 0,
