@@ -155,7 +155,7 @@ int q4d_set_activation_precision(int32_t mode);
  * layer as two launches split over the GPU's eight XCDs, one kv head per XCD, with the
  * XCD's workgroups exchanging data through its L2; Q4D_DECODE_STAGED runs the five
  * per-stage launches of q4d_layer_stage.  XCD applies to the Qwen3-0.6B shape (hidden
- * 1024, 16/8 heads of 128, intermediate 3072), max_ctx <= 4096 and activation
+ * 1024, 16/8 heads of 128, intermediate 3072), max_ctx <= 32768 and activation
  * precision 2, on a device that passes a one-time check (at least 256 CUs, one 320-thread
  * workgroup of each XCD-split kernel fits on a CU, and a probe launch of 256 workgroups
  * places workgroups b, b + 8, b + 16, ... on one XCD and the eight residues on eight

@@ -536,6 +536,9 @@ __global__ __launch_bounds__(kXThreads) void xcd_attn_kernel(const XcdAttnArgs a
     }
     float M = -INFINITY, L = 0.f, o0 = 0.f, o1 = 0.f;
     for (int i = 0; i < NPT; ++i) {
+      // groups past the chunk add nothing (every score masked): with room for long
+      // contexts, stop at the chunk's end (wave-uniform) instead of running all NPT
+      if (NPT >= 4 && 16 * i >= cn) break;
       const int pl_ = 16 * i + ap;  // position within the chunk
       const int gb = cstart + 16 * i;  // first position of the group
       if (i > 0) {
@@ -806,7 +809,8 @@ bool xcd_device_probe(int dev, hipStream_t st) {
       cus < kXcdGroups * kXcdBlocks)
     return false;
   if (!attn_kernels_fit<1>(dev) || !attn_kernels_fit<2>(dev) || !attn_kernels_fit<4>(dev) ||
-      !attn_kernels_fit<8>(dev))
+      !attn_kernels_fit<8>(dev) || !attn_kernels_fit<16>(dev) || !attn_kernels_fit<32>(dev) ||
+      !attn_kernels_fit<64>(dev))
     return false;
   int n = 0;
   if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, reinterpret_cast<const void*>(&xcd_mlp_kernel), kXThreads,
@@ -862,7 +866,7 @@ int xcd_set_check_mode(int mode) {
 int xcd_npt(int max_ctx) {
   const int cm = max(16, (max_ctx + kXcdBlocks - 1) / kXcdBlocks);
   const int n = (cm + 15) / 16;
-  return n <= 1 ? 1 : n <= 2 ? 2 : n <= 4 ? 4 : n <= 8 ? 8 : 0;
+  return n <= 1 ? 1 : n <= 2 ? 2 : n <= 4 ? 4 : n <= 8 ? 8 : n <= 16 ? 16 : n <= 32 ? 32 : n <= 64 ? 64 : 0;
 }
 
 template <int NPT>
@@ -882,6 +886,9 @@ int launch_xcd_attn(const XcdAttnArgs& a, hipStream_t st) {
     case 2: launch_xcd_attn_npt<2>(a, st); break;
     case 4: launch_xcd_attn_npt<4>(a, st); break;
     case 8: launch_xcd_attn_npt<8>(a, st); break;
+    case 16: launch_xcd_attn_npt<16>(a, st); break;
+    case 32: launch_xcd_attn_npt<32>(a, st); break;
+    case 64: launch_xcd_attn_npt<64>(a, st); break;
     default: return Q4D_ERR_CAPACITY;
   }
   return check_launch();

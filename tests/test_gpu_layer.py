@@ -234,6 +234,9 @@ def test_attention_context_lengths_and_batch(dev, lengths):
 LONG_CASES = [(plan, cap, pos) for plan, cap, name in ((0, 4096, "xcd-4096"), (0, 2048, "xcd-2048"),
                                                        (1, 4097, "staged-4097"))
               for pos in (1024, 1151, 2047, 4095) if pos < cap]
+# the XCD-split layer past 4096 positions (16, 32 or 64 groups of 16 per workgroup, and the
+# loop stopping at a short chunk's end)
+LONG_CASES += [(0, 8193, 4100), (0, 8193, 8192), (0, 32768, 1000), (0, 32768, 32767)]
 LONG_IDS = [f"{'xcd' if p == 0 else 'staged'}-{c}-{q}" for p, c, q in LONG_CASES]
 
 
@@ -241,10 +244,10 @@ LONG_IDS = [f"{'xcd' if p == 0 else 'staged'}-{c}-{q}" for p, c, q in LONG_CASES
 def test_decoder_layer_long_context(dev, layer_setup, position, plan, max_ctx):
     """Batch-1 decode layer past 1024 cached positions against the fp16-KV oracle at
     the layer-test bar, for both kernel plans: the XCD-split layer at a capacity of
-    4096 / 2048 positions (each of the 32 attention workgroups of an XCD takes 8 / 4
-    groups of 16 positions), and the five staged launches past 4096 positions (the
-    o_proj prologue merges more than eight 128-position chunks, its loop over further
-    batches of eight)."""
+    2048 to 32768 positions (each of the 32 attention workgroups of an XCD takes up to
+    4 .. 64 groups of 16 positions, fewer when the chunk is short), and the five staged
+    launches past 4096 positions (the o_proj prologue merges more than eight 128-position
+    chunks, its loop over further batches of eight)."""
     from llm_accelerator_amd.model import with_context
     cfg, model, om64, _, _, _, hidden = layer_setup
     m = with_context(model, max_ctx)
