@@ -751,6 +751,10 @@ def main():
         sys.exit(f"bench.py measures one GPU only (got --gpus {args.gpus}); this build has no multi-GPU path")
     if args.steps < 1 or args.warmup < 0:
         sys.exit("--steps must be >= 1 and --warmup >= 0")
+    legs = set() if args.no_extras else {x.strip() for x in args.legs.split(",") if x.strip()}
+    known = {"decode", "lm", "lmsweep", "layer", "prefill", "batch", "fx", "q4c", "group"}
+    if legs - known:
+        sys.exit(f"unknown legs {sorted(legs - known)}")
     import numpy as np
     import torch
 
@@ -763,10 +767,6 @@ def main():
     dev = torch.device("cuda:0")
     st = lambda: torch.cuda.current_stream().cuda_stream  # noqa: E731
 
-    legs = set() if args.no_extras else {x.strip() for x in args.legs.split(",") if x.strip()}
-    known = {"decode", "lm", "lmsweep", "layer", "prefill", "batch", "fx", "q4c", "group"}
-    if legs - known:
-        sys.exit(f"unknown legs {sorted(legs - known)}")
 
     gemv = leg_gemv(args, lib, torch, np, dev, st)
     extras = {"gemv_resident_us": round(gemv["resident_us"], 3),
