@@ -187,7 +187,9 @@ int q4d_linear(const q4d_matrix_t* w, const void* x, int32_t x_dtype, void* y, i
  * manual_linear_from_weight, common.py:137-145): q4d_linear over `count` independent matrices of one shape, each with
  * its own activations and output, up to 64 per launch: w is a host array of count
  * descriptors (equal rows and cols), x and y host arrays of count device pointers as in
- * q4d_linear.  Each y[i] equals q4d_linear(&w[i], x[i], ...) bit for bit.  For callers that
+ * q4d_linear.  Each y[i] equals q4d_linear(&w[i], x[i], ...) bit for bit.  Every descriptor
+ * and pointer is checked before the first launch: a call that returns an error has written
+ * no output.  For callers that
  * apply many small matrices at once (expert or adapter weights), where one launch per matrix
  * would cost more than its bytes. */
 int q4d_linear_group(const q4d_matrix_t* w, const void* const* x, int32_t x_dtype, void* const* y, int32_t y_dtype,

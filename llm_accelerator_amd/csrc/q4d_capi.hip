@@ -475,14 +475,20 @@ int q4d_linear_group(const q4d_matrix_t* w, const void* const* x, int32_t x_dtyp
   if (count <= 0 || batch <= 0) return Q4D_ERR_SHAPE;
   if (x_dtype != Q4D_F16 && x_dtype != Q4D_F32) return Q4D_ERR_DTYPE;
   if (y_dtype != Q4D_F16 && y_dtype != Q4D_F32) return Q4D_ERR_DTYPE;
+  // every descriptor and pointer is checked before the first launch, so a call that
+  // returns an error has written no output
+  for (int i = 0; i < count; ++i) {
+    const int rc = check_matrix(&w[i], w[0].rows, w[0].cols);
+    if (rc) return rc;
+    if (!x[i] || !y[i]) return Q4D_ERR_NULL;
+    if (!aligned(x[i], 16)) return Q4D_ERR_BAD_ADDR;
+  }
   constexpr int kChunk = 64;  // descriptors unpacked per step
   const uint8_t* wp[kChunk];
   const uint16_t* sp[kChunk];
   for (int i0 = 0; i0 < count; i0 += kChunk) {
     const int n = count - i0 < kChunk ? count - i0 : kChunk;
     for (int k = 0; k < n; ++k) {
-      const int rc = check_matrix(&w[i0 + k], w[0].rows, w[0].cols);
-      if (rc) return rc;
       wp[k] = w[i0 + k].w;
       sp[k] = w[i0 + k].s;
     }

@@ -303,3 +303,19 @@ def test_linear_group_validates_on_host(lib):
     assert f(bad, ptrs, 1, ptrs, 1, 1, 2, None) == -11         # K not 1024 / 2048 / 3072
     assert f(mats, (ctypes.c_void_p * 2)(FAKE, FAKE + 8), 1, ptrs, 1, 1, 2, None) == -4   # x alignment
     assert f(mats, (ctypes.c_void_p * 2)(FAKE, None), 1, ptrs, 1, 1, 2, None) == -7
+
+
+def test_linear_group_checks_every_matrix_before_the_first_launch(lib):
+    """A bad entry past the first launch's 64 matrices is reported before anything runs
+    (without a GPU, a launch would fail with a HIP error instead)."""
+    f = lib.q4d_linear_group
+    n = 70
+    good = Q4dMatrix(FAKE, FAKE, 256, 1024)
+    ptrs = (ctypes.c_void_p * n)(*[FAKE + 4096 * i for i in range(n)])
+    mats = (Q4dMatrix * n)(*([good] * (n - 1) + [Q4dMatrix(FAKE, FAKE, 258, 1024)]))
+    assert f(mats, ptrs, 1, ptrs, 1, 1, n, None) == -3          # shape of matrix 69
+    mats = (Q4dMatrix * n)(*([good] * n))
+    ys = (ctypes.c_void_p * n)(*([FAKE] * (n - 1) + [None]))
+    assert f(mats, ptrs, 1, ys, 1, 1, n, None) == -7            # y[69]
+    xs = (ctypes.c_void_p * n)(*([FAKE] * (n - 1) + [FAKE + 8]))
+    assert f(mats, xs, 1, ptrs, 1, 1, n, None) == -4            # x[69] alignment
