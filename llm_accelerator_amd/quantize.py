@@ -108,6 +108,7 @@ def quantize_weights_q4(weights) -> list:
                     quantize_weight_q4(prepared[i][0], return_codes=False)
                 except ValueError as e:
                     raise ValueError(f"matrix {i}: {e}") from None
+            _raise_on_status(status)  # no single call failed: report the group's own status
         for k, i in enumerate(idx):
             out[i] = (packed[k], scale[k])
     return out
