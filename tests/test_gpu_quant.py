@@ -212,3 +212,28 @@ def test_batch_status_sums_and_python_errors(dev):
     for w, (p, s) in zip(mixed, got):
         want_p, want_s, _ = quantize_weight_q4(w, return_codes=False)
         assert torch.equal(p, want_p) and torch.equal(s, want_s)
+
+
+@pytest.mark.parametrize("dtype,count", [(torch.bfloat16, 70), (torch.float32, 3)])
+def test_batch_strided_rows(dev, dtype, count):
+    """Column slices of wider matrices (one row pitch for all, 16-byte aligned starts) through
+    one batch call and through the list wrapper equal single conversions of contiguous copies."""
+    from llm_accelerator_amd._lib import Q4D_BF16, Q4D_F32
+    from llm_accelerator_amd.quantize import quantize_weights_q4
+    g = torch.Generator(device=dev).manual_seed(count)
+    rows, cols, pad = 24, 1024, 64 if dtype == torch.float32 else 128
+    wides = [(torch.randn(rows, cols + pad, device=dev, generator=g) * 0.03).to(dtype) for _ in range(count)]
+    views = [w[:, pad:] for w in wides]
+    assert views[0].stride(0) == cols + pad and views[0].data_ptr() % 16 == 0
+    status = torch.zeros(2, dtype=torch.int32, device=dev)
+    print(f"[quant] strided batch {count} x {rows}x{cols} pitch {cols + pad} {dtype}", flush=True)
+    got = _batch_call(views, Q4D_BF16 if dtype == torch.bfloat16 else Q4D_F32, status)
+    assert status.tolist() == [0, 0]
+    listed = quantize_weights_q4(views)
+    for i, v in enumerate(views):
+        p, s, _ = quantize_weight_q4(v.contiguous(), return_codes=False)
+        assert torch.equal(got[i][0], p) and torch.equal(got[i][1], s), i
+        assert torch.equal(listed[i][0], p) and torch.equal(listed[i][1], s), i
+    want_p, want_s, _ = o.quantize_weight_q4(views[-1].float().cpu().numpy())
+    np.testing.assert_array_equal(got[-1][0].cpu().numpy(), want_p)
+    np.testing.assert_array_equal(got[-1][1].cpu().numpy(), want_s)
