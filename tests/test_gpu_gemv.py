@@ -153,13 +153,15 @@ def test_lm_head_repeatable_and_counter_resets(dev):
         assert res[0][0] == int(top[1])
 
 
-@pytest.mark.parametrize("k,xdtype,ydtype,batch,count", [(1024, torch.float16, Q4D_F16, 1, 70),
-                                                         (2048, torch.float32, Q4D_F32, 3, 5),
-                                                         (3072, torch.float32, Q4D_F16, 2, 9),
-                                                         (1024, torch.float32, Q4D_F32, 1, 64)])
-def test_linear_group_equals_single_calls(dev, k, xdtype, ydtype, batch, count):
+@pytest.mark.parametrize("k,xdtype,ydtype,batch,count,precision", [(1024, torch.float16, Q4D_F16, 1, 70, 2),
+                                                                   (2048, torch.float32, Q4D_F32, 3, 5, 2),
+                                                                   (3072, torch.float32, Q4D_F16, 2, 9, 2),
+                                                                   (1024, torch.float32, Q4D_F32, 1, 64, 2),
+                                                                   (2048, torch.float32, Q4D_F32, 2, 66, 1)])
+def test_linear_group_equals_single_calls(dev, k, xdtype, ydtype, batch, count, precision):
     """q4d_linear_group over `count` matrices (70: launches of 64 + 6), each with its own
-    x and y, equals one q4d_linear call per matrix bit for bit; one matrix also meets the
+    x and y, equals one q4d_linear call per matrix bit for bit, at either activation
+    precision (fp32 x as hi + lo fp16 pairs, or one fp16 value); one matrix also meets the
     oracle's accumulation bound."""
     import ctypes
     from llm_accelerator_amd import _lib
@@ -176,16 +178,22 @@ def test_linear_group_equals_single_calls(dev, k, xdtype, ydtype, batch, count):
     yp = (ctypes.c_void_p * count)(*[y.data_ptr() for y in ys])
     print(f"[gemv] group {count} x {n}x{k} batch {batch}", flush=True)
     xcode = Q4D_F16 if xdtype == torch.float16 else Q4D_F32
-    _lib.check(_lib.load().q4d_linear_group(descs, xp, xcode, yp, ydtype, batch, count, current_stream()),
-               "q4d_linear_group")
-    for i in range(count):
-        want = linear(mats[i], xs[i], ydtype)
-        assert torch.equal(ys[i], want), i
+    lib = _lib.load()
+    _lib.check(lib.q4d_set_activation_precision(precision), "q4d_set_activation_precision")
+    try:
+        _lib.check(lib.q4d_linear_group(descs, xp, xcode, yp, ydtype, batch, count, current_stream()),
+                   "q4d_linear_group")
+        for i in range(count):
+            want = linear(mats[i], xs[i], ydtype)
+            assert torch.equal(ys[i], want), i
+    finally:
+        _lib.check(lib.q4d_set_activation_precision(2), "q4d_set_activation_precision")
     W = o.dequantize_q4(mats[0].packed.cpu().numpy(), mats[0].scale.cpu().numpy(), dtype=np.float64)
     x0 = xs[0][0].float().cpu().numpy()
     ref = W @ x0.astype(np.float64)
     y0 = ys[0][0].float().cpu().numpy()
     half_ulp = np.abs(ref) * 2.0 ** -11 + 2.0 ** -25 if ydtype == Q4D_F16 else 0.0
-    # fp32 activations enter as fp16 hi + lo halves (~22 bits): 2^-21 relative each
-    xerr = 2.0 ** -21 * abs_dot_bound(W, x0) if xdtype == torch.float32 else 0.0
+    # fp32 activations enter as fp16 hi + lo halves (~22 bits, 2^-21 relative each) at
+    # precision 2, as one fp16 value (2^-11) at precision 1
+    xerr = (2.0 ** -21 if precision == 2 else 2.0 ** -11) * abs_dot_bound(W, x0) if xdtype == torch.float32 else 0.0
     assert np.all(np.abs(y0 - ref) <= half_ulp + xerr + ACC * abs_dot_bound(W, x0))
