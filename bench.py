@@ -89,7 +89,8 @@ def parse():
     ap.add_argument("--legs", default="decode,lm,layer,prefill,batch,fx,q4c,group",
                     help="comma list of the legs beside the GEMV headline: decode (28-layer decode), "
                          "lm (LM head alone), lmsweep (LM head over 4096..151936 rows, not by default), "
-                         "layer (one decoder layer at --ctx), prefill, batch (batched decode), "
+                         "layer (one decoder layer at --ctx), layerlong (one layer at 4096..32768 cached "
+                         "positions under both decode plans, not by default), prefill, batch (batched decode), "
                          "fx fixed-point (RTL-exact) layer and token, q4c float -> Q4 conversion of the model, "
                          "group (the headline GEMV over 64 matrices per launch)")
     ap.add_argument("--extras", dest="legs", default=argparse.SUPPRESS, help="the same as --legs")
@@ -213,6 +214,60 @@ def leg_gemv(args, lib, torch, np, dev, st):
 
 
 # ------------------------------------------------------------------ decoder layer
+# (KV capacity, position) cases of the long-context layer leg: the first position past each
+# power-of-two capacity, Qwen3's full 32768-position context, and short positions in long caches
+LAYER_LONG_CASES = ((4097, 4096), (8193, 8192), (16385, 16384), (32768, 32767), (32768, 1000),
+                    (4096, 200), (4096, 1000), (4096, 4000))
+
+
+def leg_layer_long(lib, torch, dev, st):
+    """One decoder layer (resident weights, random cache) at long contexts, under the
+    XCD-split plan (q4d_set_decode_plan(0)) and the staged plan (1)."""
+    from llm_accelerator_amd import model as M
+    from llm_accelerator_amd._lib import check
+    cfg = M.Qwen3Config(num_hidden_layers=1, vocab_size=2048)
+    host = M.random_host_weights(cfg, seed=0, num_layers=1)
+    rows = []
+    for cap, pos_v in LAYER_LONG_CASES:
+        model = M.build_model(cfg, host, max_ctx=cap, device=dev)
+        kv = M.KVCache(cfg, 1, 1, cap, dev)
+        gen = torch.Generator(device=dev).manual_seed(2)
+        kv.data.normal_(generator=gen)
+        ws = M.Workspace(model, 1)
+        pos = torch.tensor([pos_v], dtype=torch.int32, device=dev)
+        h_in = torch.randn(1, 1024, generator=gen, device=dev, dtype=torch.float32)
+        h_out = torch.empty_like(h_in)
+        desc, kvd = model.descriptor(), kv.descriptor()
+
+        def step(i):
+            check(lib.q4d_decoder_layer(ctypes.byref(desc), 0, h_in.data_ptr(), h_out.data_ptr(), ctypes.byref(kvd),
+                                        pos.data_ptr(), ws.ptr, ws.nbytes, st()), "q4d_decoder_layer")
+
+        row = {"max_ctx": cap, "position": pos_v}
+        for name, plan in (("xcd", 0), ("staged", 1)):
+            prev = lib.q4d_set_decode_plan(plan)
+            try:
+                active = int(lib.q4d_decode_plan_active(ctypes.byref(desc), st()))
+                step(0)
+                g = graph_of(step, 20, torch)
+                g.replay()
+                us = min(time_graph(g, 10, torch) for _ in range(3)) / 20 * 1e3
+                del g
+            finally:
+                lib.q4d_set_decode_plan(prev)
+            row[f"{name}_us"] = round(us, 2)
+            row[f"{name}_plan_active"] = active
+            row[f"{name}_status"] = ws.status()
+        log(f"[bench] layer at max_ctx {cap}, position {pos_v}: xcd {row['xcd_us']} us, staged {row['staged_us']} us")
+        rows.append(row)
+        del model, kv, ws
+        torch.cuda.empty_cache()
+    return {"workload": "one Qwen3-0.6B decoder layer, one decode step, resident weights, fp16 cache of "
+                        "max_ctx positions (random), graphs of 20 steps (best of 3 x 10 replays)",
+            "plan_active": "q4d_decode_plan_active: 0 the XCD-split layer, 1 the staged launches",
+            "cases": rows}
+
+
 def leg_layer(args, lib, torch, dev, st):
     from llm_accelerator_amd import model as M
     from llm_accelerator_amd._lib import check
@@ -752,7 +807,7 @@ def main():
     if args.steps < 1 or args.warmup < 0:
         sys.exit("--steps must be >= 1 and --warmup >= 0")
     legs = set() if args.no_extras else {x.strip() for x in args.legs.split(",") if x.strip()}
-    known = {"decode", "lm", "lmsweep", "layer", "prefill", "batch", "fx", "q4c", "group"}
+    known = {"decode", "lm", "lmsweep", "layer", "layerlong", "prefill", "batch", "fx", "q4c", "group"}
     if legs - known:
         sys.exit(f"unknown legs {sorted(legs - known)}")
     import numpy as np
@@ -773,6 +828,8 @@ def main():
               "gemv_resident_GBps": round(gemv["resident_GBps"], 1)}
     if "layer" in legs:
         extras["decoder_layer"] = leg_layer(args, lib, torch, dev, st)
+    if "layerlong" in legs:
+        extras["decoder_layer_long_context"] = leg_layer_long(lib, torch, dev, st)
 
     decode = lm = None
     if legs & {"decode", "lm", "lmsweep", "prefill", "batch", "fx"}:
