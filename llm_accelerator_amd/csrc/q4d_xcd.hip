@@ -384,6 +384,7 @@ __global__ __launch_bounds__(kXThreads) void xcd_attn_kernel(const XcdAttnArgs a
   __shared__ float sres[16];
   __shared__ alignas(16) float sqkv[4 * D];
   __shared__ alignas(16) float sq[2][D];
+  __shared__ alignas(16) float sodd[2][4 + D];  // odd groups' softmax state (long chunks)
   __shared__ alignas(16) uint16_t snew[2][D];
   __shared__ float swt[2][kXcdBlocks];
   __shared__ alignas(16) float spart[4][2 * D];
@@ -524,18 +525,23 @@ __global__ __launch_bounds__(kXThreads) void xcd_attn_kernel(const XcdAttnArgs a
   }
   block_sync_lds();
 
-  // ---- attention of q head 2g + wid over this workgroup's chunk, one wave per head:
-  // scores over the 4 quarter lanes of a position, an online softmax over the
-  // 16-position groups, P.V with each lane owning two dims of the head ----
-  if (wid < 2 && attn_active) {
+  // ---- attention of q head 2g + (wid & 1) over this workgroup's chunk: scores over the
+  // 4 quarter lanes of a position, an online softmax over the 16-position groups, P.V
+  // with each lane owning two dims of the head.  Waves 0 and 1 take every group, except in
+  // chunks of more than one group in the long-chunk instances (8 groups and up): there
+  // waves 0 and 1 take the even groups and waves 2 and 3 the odd ones, whose softmax state
+  // then merges into waves 0 and 1 through LDS.  `split` is uniform over the workgroup
+  // (cn is the workgroup's chunk), so the barrier it adds is too ----
+  const bool split = NPT >= 8 && cn > 16;
+  float M = -INFINITY, L = 0.f, o0 = 0.f, o1 = 0.f;
+  if ((wid < 2 || (split && wid < 4)) && attn_active) {
     float q[32];
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
-      const f32x4 v = *reinterpret_cast<const f32x4*>(&sq[wid][32 * aq + 4 * k]);
+      const f32x4 v = *reinterpret_cast<const f32x4*>(&sq[wid & 1][32 * aq + 4 * k]);
       q[4 * k] = v[0]; q[4 * k + 1] = v[1]; q[4 * k + 2] = v[2]; q[4 * k + 3] = v[3];
     }
-    float M = -INFINITY, L = 0.f, o0 = 0.f, o1 = 0.f;
-    for (int i = 0; i < NPT; ++i) {
+    for (int i = split ? (wid >> 1) : 0; i < NPT; i += split ? 2 : 1) {
       // groups past the chunk add nothing (every score masked): with room for long
       // contexts, stop at the chunk's end (wave-uniform) instead of running all NPT
       if (NPT >= 4 && 16 * i >= cn) break;
@@ -585,6 +591,28 @@ __global__ __launch_bounds__(kXThreads) void xcd_attn_kernel(const XcdAttnArgs a
         o0 = fmaf(ei, (float)v.x, o0);
         o1 = fmaf(ei, (float)v.y, o1);
       }
+      M = Mn;
+    }
+    if (split && wid >= 2) {
+      *reinterpret_cast<float2*>(&sodd[wid & 1][4 + 2 * lane]) = make_float2(o0, o1);
+      if (lane == 0) {
+        sodd[wid & 1][0] = M;
+        sodd[wid & 1][1] = L;
+      }
+    }
+  }
+  if (split) block_sync_lds();
+  if (wid < 2 && attn_active) {
+    if (split) {
+      // the odd groups' state (a split chunk has at least two groups, so it holds scores)
+      const float Mb = sodd[wid][0], Lb = sodd[wid][1];
+      const float2 ob = *reinterpret_cast<const float2*>(&sodd[wid][4 + 2 * lane]);
+      const float Mn = fmaxf(M, Mb);  // group 0 is never empty: M is finite
+      const float sa = exp2f(M - Mn);
+      const float sb = Mb == -INFINITY ? 0.f : exp2f(Mb - Mn);
+      L = L * sa + Lb * sb;
+      o0 = o0 * sa + ob.x * sb;
+      o1 = o1 * sa + ob.y * sb;
       M = Mn;
     }
     float* rec = X.ap + (size_t)((g * kXcdBlocks + j) * 2 + wid) * kXcdApRec;
