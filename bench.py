@@ -217,7 +217,7 @@ def leg_gemv(args, lib, torch, np, dev, st):
 # (KV capacity, position) cases of the long-context layer leg: the first position past each
 # power-of-two capacity, Qwen3's full 32768-position context, and short positions in long caches
 LAYER_LONG_CASES = ((4097, 4096), (8193, 8192), (16385, 16384), (32768, 32767), (32768, 1000),
-                    (4096, 200), (4096, 1000), (4096, 4000))
+                    (4096, 200), (4096, 1000), (4096, 4000), (1024, 1000), (2048, 300), (2048, 2000))
 
 
 def leg_layer_long(lib, torch, dev, st):

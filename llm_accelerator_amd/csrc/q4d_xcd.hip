@@ -228,6 +228,10 @@ __device__ __forceinline__ void unpack8h(const u32x4 w, float (&f)[8]) {
 
 // Attention chunking for context T = pos + 1: nA = min(32, ceil(T / 16)) workgroups
 // of ceil(T / nA) positions (at most 16 while T <= 512).
+// Group-loop instances (groups of 16 positions per chunk) from which a chunk of more than
+// one group is scored by four waves (even / odd groups) instead of two.
+constexpr int kXcdSplitMinGroups = 4;
+
 __device__ __forceinline__ void attn_split(int T, int& nA, int& chunk) {
   nA = min(kXcdBlocks, (T + 15) / 16);
   chunk = (T + nA - 1) / nA;
@@ -528,11 +532,11 @@ __global__ __launch_bounds__(kXThreads) void xcd_attn_kernel(const XcdAttnArgs a
   // ---- attention of q head 2g + (wid & 1) over this workgroup's chunk: scores over the
   // 4 quarter lanes of a position, an online softmax over the 16-position groups, P.V
   // with each lane owning two dims of the head.  Waves 0 and 1 take every group, except in
-  // chunks of more than one group in the long-chunk instances (8 groups and up): there
+  // chunks of more than one group in the instances of kXcdSplitMinGroups groups and up: there
   // waves 0 and 1 take the even groups and waves 2 and 3 the odd ones, whose softmax state
   // then merges into waves 0 and 1 through LDS.  `split` is uniform over the workgroup
   // (cn is the workgroup's chunk), so the barrier it adds is too ----
-  const bool split = NPT >= 8 && cn > 16;
+  const bool split = NPT >= kXcdSplitMinGroups && cn > 16;
   float M = -INFINITY, L = 0.f, o0 = 0.f, o1 = 0.f;
   if ((wid < 2 || (split && wid < 4)) && attn_active) {
     float q[32];
